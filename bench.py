@@ -1,0 +1,224 @@
+"""Benchmark of the fused per-token layer kernels on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A step is one launch of the headline kernel over the whole batch: the AdaLN chain (LayerNorm without affine, then
+x * (1 + scale) + shift, GELU-tanh, out = res + gate * y) on X, res [16896 x 4096] bf16, token grid T16 x H24 x W44.
+``value`` is its achieved HBM bandwidth: algorithmic bytes (X and res read once, out written once) divided by the
+mean kernel time, timed with HIP events on the stream the kernel runs on, inputs already in HBM. The other fused
+kernels are timed the same way and reported under ``kernels``; the int8 GEMM also as int8 TOPS. ``cpu_baseline``
+times the CPU oracle (the C restatement of the reference arithmetic) on the same workload on this host.
+Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_GBS = 8000.0          # MI355X HBM3E
+PEAK_I8_TOPS = 5000.0      # MI355X dense int8 matrix peak
+
+M2 = 16 * 24 * 44          # 16896 tokens (T16 x H24 x W44)
+M4 = 47104
+C = 4096
+
+
+def bytes_cfg():
+    """Algorithmic bytes per launch (minimum HBM traffic: every input read once, every output written once)."""
+    return {
+        "cfg1_rmsnorm_quant_2159": 2159 * C * 2 + 2159 * C + 2159 * 4,
+        "cfg2_ln_mod_gelu_gate_16896": 3 * M2 * C * 2,
+        "cfg3_qk_rmsnorm_rope3d_16896": 4 * M2 * 32 * 128 * 2 + M2 * 64 * 2 * 4,
+        "cfg4_rmsnorm_wht128_quant_47104": M4 * C * 2 + M4 * C + M4 * 4,
+        "cfg5a_rmsnorm_mod_quant_47104": M4 * C * 2 + M4 * C + M4 * 4,
+        "cfg5b_int8_gemm_silu_47104x16384": M4 * C + 16384 * C + M4 * 4 + 16384 * 4 + M4 * 16384 * 2,
+    }
+
+
+def rope_table(T, Hh, Ww, dims=(32, 48, 48), theta=10000.0):
+    """(cos, sin) per token and rotated pair [M, 64, 2], float32: positions from the grid, angle = pos * theta^(-2i/d)
+    per axis in float32, the axes one after the other (engine/h3-core/src/dit.rs:190-203)."""
+    import numpy as np
+
+    t, h, w = np.meshgrid(np.arange(T), np.arange(Hh), np.arange(Ww), indexing="ij")
+    pos = np.stack([t.ravel(), h.ravel(), w.ravel()], -1).astype(np.float32)
+    cols = []
+    for a, d in enumerate(dims):
+        inv = (np.float32(1.0) / np.power(np.float32(theta), np.arange(0, d, 2, dtype=np.float32) / np.float32(d))).astype(np.float32)
+        cols.append(pos[:, a:a + 1] * inv[None, :])
+    ang = np.concatenate(cols, 1).astype(np.float32)
+    return np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of kernel keys to time (default all)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the per-token kernels shard "
+              "by token rows with no exchange; see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from sycl_minimax_h3_amd import Device, DType, Tensor, ops
+    import sycl_minimax_h3_amd.api as A
+
+    torch.manual_seed(0)
+    dev_t = torch.device("cuda:0")
+    dev = Device.from_torch()
+    T = lambda t, dt=None: Tensor.from_torch(t, dt, dev)   # noqa: E731
+    B = bytes_cfg()
+    only = set(filter(None, args.only.split(",")))
+
+    def bf16(*shape, scale=1.0):
+        return (torch.randn(*shape, device=dev_t) * scale).to(torch.bfloat16)
+
+    def timed(fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps   # ms per launch
+
+    kernels = {}
+
+    # ---- config 2 (headline): LN (no affine) -> * (1 + scale) + shift -> GELU-tanh -> res + gate * y ----
+    x2, r2, o2 = bf16(M2, C), bf16(M2, C), torch.empty(M2, C, dtype=torch.bfloat16, device=dev_t)
+    tab = [bf16(1, C, scale=0.5) for _ in range(3)]
+    tb2 = ops.Tables(scale=T(tab[0]), shift=T(tab[1]), gate=T(tab[2]))
+    X2, R2, O2 = T(x2), T(r2), T(o2)
+    f2 = lambda: ops.norm_mod_act_gate(X2, A.NORM_LAYER, None, None, 1e-5, tb2, A.ACT_GELU_TANH, R2, O2)  # noqa: E731
+    ms2 = timed(f2, args.steps, args.warmup)
+    kernels["cfg2_ln_mod_gelu_gate_16896"] = ms2
+
+    def run(key, fn, steps=20):
+        if only and key not in only:
+            return
+        kernels[key] = timed(fn, steps, 3)
+
+    # ---- config 1: RMSNorm (eps 1e-6) + per-token int8 quant, [2159 x 4096] ----
+    x1 = bf16(2159, C)
+    g1 = (1 + 0.1 * torch.randn(C, device=dev_t)).float()
+    q1, s1 = torch.empty(2159, C, dtype=torch.int8, device=dev_t), torch.empty(2159, device=dev_t)
+    X1, G1, Q1, S1 = T(x1), T(g1), T(q1), T(s1)
+    run("cfg1_rmsnorm_quant_2159", lambda: ops.norm_quant(X1, G1, 1e-6, None, Q1, S1), 200)
+
+    # ---- config 3: qk-RMSNorm + 3D RoPE in place, q, k [16896 x 32 x 128], split 32/48/48 ----
+    q3, k3 = bf16(M2, 32 * 128), bf16(M2, 32 * 128)
+    wq, wk = (1 + 0.1 * torch.randn(128, device=dev_t)).float(), (1 + 0.1 * torch.randn(128, device=dev_t)).float()
+    cs = torch.from_numpy(rope_table(16, 24, 44)).to(dev_t)
+    Q3, K3, WQ, WK, CS = T(q3), T(k3), T(wq), T(wk), T(cs)
+    run("cfg3_qk_rmsnorm_rope3d_16896", lambda: ops.qk_rms_rope(ops.Rows(Q3, 0, 4096, M2, 32, 128), ops.Rows(K3, 0, 4096, M2, 32, 128),
+                                                                 WQ, WK, 1e-5, CS, 128))
+
+    # ---- config 4: RMSNorm -> Sylvester WHT-128 -> int8 quant, [47104 x 4096], 1% of channels x20 ----
+    ch = torch.randperm(C, generator=torch.Generator().manual_seed(4))[:41].to(dev_t)
+    x4 = torch.randn(M4, C, device=dev_t)
+    x4[:, ch] *= 20
+    x4 = x4.to(torch.bfloat16)
+    q4, s4 = torch.empty(M4, C, dtype=torch.int8, device=dev_t), torch.empty(M4, device=dev_t)
+    X4, Q4, S4 = T(x4), T(q4), T(s4)
+    run("cfg4_rmsnorm_wht128_quant_47104", lambda: ops.norm_quant(X4, G1, 1e-6, None, Q4, S4, rot=A.ROT_SYLVESTER, group=128))
+
+    # ---- config 5a: RMSNorm + modulate + int8 quant, [47104 x 4096]; 5b: int8 GEMM + dequant + SiLU ----
+    x5 = bf16(M4, C)
+    sc5, sh5 = bf16(1, C, scale=0.5), bf16(1, C, scale=0.5)
+    tb5 = ops.Tables(scale=T(sc5), shift=T(sh5))
+    X5 = T(x5)
+    run("cfg5a_rmsnorm_mod_quant_47104", lambda: ops.norm_quant(X5, G1, 1e-6, tb5, Q4, S4))
+    w5 = torch.randint(-127, 128, (16384, C), dtype=torch.int8, device=dev_t)
+    ws5 = (0.005 + 0.015 * torch.rand(16384, device=dev_t)).float()
+    out5 = torch.empty(M4, 16384, dtype=torch.bfloat16, device=dev_t)
+    layer = ops.Int8Linear(T(w5), T(ws5))
+    O5 = T(out5)
+    run("cfg5b_int8_gemm_silu_47104x16384", lambda: ops.int8_gemm_dequant(Q4, S4, layer, A.ACT_SILU, O5), 5)
+
+    per = {}
+    for k, ms in kernels.items():
+        gbs = B[k] / (ms * 1e-3) / 1e9
+        e = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_GBS, 4), "bytes": B[k]}
+        if k.startswith("cfg5b"):
+            tops = 2 * M4 * C * 16384 / (ms * 1e-3) / 1e12
+            e.update({"TOPS_i8": round(tops, 1), "frac_i8_peak": round(tops / PEAK_I8_TOPS, 4)})
+        per[k] = e
+
+    value = B["cfg2_ln_mod_gelu_gate_16896"] / (ms2 * 1e-3) / 1e9
+    line = {
+        "metric": "achieved HBM GB/s (% of 8 TB/s) per fused kernel at 16.8k/47k tokens x 4096",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms2, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (torch.randn on the device; shift/scale/gate ~N(0,0.5))",
+        "config": {"workload": "AdaLN chain: LayerNorm(no affine) -> x*(1+scale)+shift -> GELU-tanh -> res + gate*y, "
+                               "X,res [16896 x 4096] bf16 (grid T16xH24xW44)", "tokens": M2, "hidden": C},
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / PEAK_GBS, 4), "traffic": None},
+        "kernels": per,
+        "device": dev.name(),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(x2, r2, tab)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline(x2, r2, tab):
+    """The CPU oracle (oracle/h3oracle.c, C restatement of the reference arithmetic, row-parallel with contiguous row
+    chunks as engine/h3-core/src/reference.rs:43-80) on the headline workload, on this host."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as o
+
+    threads = min(16, os.cpu_count() or 1)
+    o.set_threads(threads)
+    x = x2.view(torch.int16).cpu().numpy().view(np.uint16).ravel()
+    r = r2.view(torch.int16).cpu().numpy().view(np.uint16).ravel()
+    t = [a.view(torch.int16).cpu().numpy().view(np.uint16).ravel() for a in tab]
+    run = lambda: o.norm_mod_act_gate(x, o.BF16, M2, C, o.NORM_LAYER, None, None, 1e-5, None, t[0], t[1], t[2], o.BF16,  # noqa: E731
+                                      o.ACT_GELU_TANH, r, o.BF16, o.BF16)
+    run()
+    times = []
+    t_end = time.perf_counter() + 10.0
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    gbs = bytes_cfg()["cfg2_ln_mod_gelu_gate_16896"] / med / 1e9
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except Exception:
+        pass
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the full 16896 x 4096 workload, median of {len(times)} runs ({med * 1e3:.1f} ms each) on {cpu}"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

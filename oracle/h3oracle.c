@@ -1,0 +1,583 @@
+/* h3oracle.c - CPU restatement of the reference's per-token layer arithmetic (see h3oracle.h).
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker the GPU library is compared against, never part of the product path.
+ * Build with -ffp-contract=off (oracle/Makefile): every rounding step below is the one written.
+ */
+#include "h3oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static __thread char g_err[256];
+static int g_threads = 1;
+
+static int fail(const char* msg) {
+    snprintf(g_err, sizeof g_err, "%s", msg);
+    return -1;
+}
+const char* h3o_last_error(void) { return g_err; }
+
+void h3o_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+int h3o_get_threads(void) { return g_threads; }
+
+/* ---- row-parallel driver: contiguous row chunks, one per thread (engine/h3-core/src/reference.rs:43-80) ---- */
+typedef void (*row_fn)(void* ctx, int64_t r0, int64_t r1);
+typedef struct { row_fn fn; void* ctx; int64_t r0, r1; } job;
+static void* run_job(void* p) {
+    job* j = (job*) p;
+    j->fn(j->ctx, j->r0, j->r1);
+    return NULL;
+}
+static void parallel_rows(int64_t M, row_fn fn, void* ctx) {
+    int t = g_threads > 256 ? 256 : g_threads;
+    if (t > M) t = (int) (M > 0 ? M : 1);
+    if (t <= 1) { fn(ctx, 0, M); return; }
+    const int64_t per = (M + t - 1) / t;
+    pthread_t th[256];
+    job jobs[256];
+    int made[256] = {0};
+    for (int i = 0; i < t; ++i) {
+        const int64_t a = (int64_t) i * per, b = a + per < M ? a + per : M;
+        if (a >= b) break;
+        jobs[i] = (job){fn, ctx, a, b};
+        if (pthread_create(&th[i], NULL, run_job, &jobs[i]) == 0) made[i] = 1;
+        else fn(ctx, a, b);                                  /* no thread: do the chunk here */
+    }
+    for (int i = 0; i < t; ++i)
+        if (made[i]) pthread_join(th[i], NULL);
+}
+
+/* ---- element types: dtype.rs:53-121 (bf16 narrowing also kernels/h3sycl.cpp:42-49) ---- */
+static inline uint32_t fbits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float bitsf(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+float h3o_bf16_to_f32(uint16_t b) { return bitsf((uint32_t) b << 16); }                       /* dtype.rs:54-56 */
+uint16_t h3o_f32_to_bf16(float f) {                                                            /* dtype.rs:59-66 */
+    uint32_t u = fbits(f);
+    if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t) (u >> 16);   /* inf / nan: truncate */
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t) (u >> 16);
+}
+float h3o_f16_to_f32(uint16_t h) {                                                             /* dtype.rs:69-85 */
+    const uint32_t sign = (uint32_t) (h >> 15) << 31, exp = (h >> 10) & 0x1f, man = h & 0x3ff;
+    uint32_t bits;
+    if (exp == 0 && man == 0) bits = sign;
+    else if (exp == 0) {
+        uint32_t m = man, shift = 0;
+        while (!(m & 0x400)) { m <<= 1; ++shift; }          /* leading_zeros(man) - 21 of a u32 */
+        bits = sign | ((113 - shift) << 23) | ((m & 0x3ff) << 13);
+    } else if (exp == 31) bits = sign | 0x7f800000u | (man << 13);
+    else bits = sign | ((exp + 112) << 23) | (man << 13);
+    return bitsf(bits);
+}
+uint16_t h3o_f32_to_f16(float f) {                                                             /* dtype.rs:88-121 */
+    const uint32_t u = fbits(f);
+    const uint16_t sign = (uint16_t) ((u >> 16) & 0x8000);
+    const int exp = (int) ((u >> 23) & 0xff);
+    const uint32_t man = u & 0x7fffff;
+    if (exp == 0xff) return sign | 0x7c00 | (man ? 0x200 : 0);
+    const int e = exp - 127 + 15;
+    if (e >= 31) return sign | 0x7c00;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        const uint32_t m = man | 0x800000, shift = (uint32_t) (14 - e), half = 1u << (shift - 1);
+        const uint32_t rest = m & ((1u << shift) - 1);
+        uint32_t hv = m >> shift;
+        if (rest > half || (rest == half && (hv & 1))) hv += 1;
+        return sign | (uint16_t) hv;
+    }
+    uint32_t hv = ((uint32_t) e << 10) | (man >> 13);
+    const uint32_t rest = man & 0x1fff;
+    if (rest > 0x1000 || (rest == 0x1000 && (hv & 1))) hv += 1;
+    return sign | (uint16_t) hv;
+}
+float h3o_load(const void* p, int dt, int64_t i) {                                             /* h3sycl.cpp:50-56 */
+    switch (dt) {
+        case H3O_F16: return h3o_f16_to_f32(((const uint16_t*) p)[i]);
+        case H3O_BF16: return h3o_bf16_to_f32(((const uint16_t*) p)[i]);
+        default: return ((const float*) p)[i];
+    }
+}
+void h3o_store(void* p, int dt, int64_t i, float v) {                                          /* h3sycl.cpp:57-63 */
+    switch (dt) {
+        case H3O_F16: ((uint16_t*) p)[i] = h3o_f32_to_f16(v); break;
+        case H3O_BF16: ((uint16_t*) p)[i] = h3o_f32_to_bf16(v); break;
+        default: ((float*) p)[i] = v;
+    }
+}
+float h3o_round_to(float v, int dt) {
+    switch (dt) {
+        case H3O_F16: return h3o_f16_to_f32(h3o_f32_to_f16(v));
+        case H3O_BF16: return h3o_bf16_to_f32(h3o_f32_to_bf16(v));
+        default: return v;
+    }
+}
+static int vec_of(int dt) { return dt == H3O_F32 ? 4 : 8; }   /* 16 bytes of the type: the kernels' load width */
+static int dt_ok(int dt) { return dt == H3O_F32 || dt == H3O_F16 || dt == H3O_BF16; }
+
+/* ---- seeded inputs: engine/h3-core/src/rng.rs:9-43 ---- */
+void h3o_rng_new(h3o_rng* r, uint64_t seed) {                                                  /* rng.rs:9-20 */
+    uint64_t z = seed;
+    for (int i = 0; i < 4; ++i) {
+        z += 0x9e3779b97f4a7c15ull;
+        uint64_t x = z;
+        x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+        x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+        r->s[i] = x ^ (x >> 31);
+    }
+}
+void h3o_rng_from_state(h3o_rng* r, const uint64_t s[4]) { memcpy(r->s, s, sizeof r->s); }
+static inline uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+uint64_t h3o_rng_next_u64(h3o_rng* r) {                                                        /* rng.rs:22-31 */
+    uint64_t* s = r->s;
+    const uint64_t res = rotl(s[1] * 5, 7) * 9;
+    const uint64_t t = s[1] << 17;
+    s[2] ^= s[0];
+    s[3] ^= s[1];
+    s[1] ^= s[2];
+    s[0] ^= s[3];
+    s[2] ^= t;
+    s[3] = rotl(s[3], 45);
+    return res;
+}
+float h3o_rng_uniform(h3o_rng* r) {                                                            /* rng.rs:34-36 */
+    return (float) (h3o_rng_next_u64(r) >> 40) / (float) (1ull << 24);
+}
+float h3o_rng_normal(h3o_rng* r) {                                                             /* rng.rs:39-43 */
+    float u = h3o_rng_uniform(r);
+    u = u > 1e-7f ? u : 1e-7f;
+    const float v = h3o_rng_uniform(r);
+    const float tau = 6.28318530717958647692f;
+    return sqrtf(-2.0f * logf(u)) * cosf(tau * v);
+}
+void h3o_fill_normal(uint64_t seed, float scale, int64_t n, void* out, int dt) {
+    h3o_rng r;
+    h3o_rng_new(&r, seed);
+    for (int64_t i = 0; i < n; ++i) h3o_store(out, dt, i, h3o_rng_normal(&r) * scale);
+}
+void h3o_fill_uniform(uint64_t seed, float lo, float hi, int64_t n, float* out) {
+    h3o_rng r;
+    h3o_rng_new(&r, seed);
+    for (int64_t i = 0; i < n; ++i) out[i] = lo + (hi - lo) * h3o_rng_uniform(&r);
+}
+void h3o_choose(uint64_t seed, int64_t n, int64_t k, int64_t* out) {
+    h3o_rng r;
+    h3o_rng_new(&r, seed);
+    int64_t* idx = (int64_t*) malloc((size_t) n * sizeof(int64_t));
+    for (int64_t i = 0; i < n; ++i) idx[i] = i;
+    for (int64_t i = 0; i < k && i < n; ++i) {
+        const int64_t j = i + (int64_t) (h3o_rng_next_u64(&r) % (uint64_t) (n - i));
+        const int64_t t = idx[i]; idx[i] = idx[j]; idx[j] = t;
+        out[i] = idx[i];
+    }
+    free(idx);
+}
+
+/* ---- canonical reduction ---- */
+static float butterfly(float* p, int L) {
+    float tmp[64];
+    for (int off = L / 2; off >= 1; off /= 2) {
+        for (int l = 0; l < L; ++l) tmp[l] = p[l] + p[l ^ off];
+        memcpy(p, tmp, (size_t) L * sizeof(float));
+    }
+    return p[0];
+}
+float h3o_canon_sum(const float* x, int64_t n, int V, int L, int kind, float mean) {
+    float p[64];
+    for (int l = 0; l < L; ++l) p[l] = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        const int l = (int) ((i / V) % L);
+        const float v = x[i];
+        if (kind == H3O_SUM) p[l] = p[l] + v;
+        else if (kind == H3O_SUMSQ) p[l] = fmaf(v, v, p[l]);
+        else { const float d = v - mean; p[l] = fmaf(d, d, p[l]); }
+    }
+    return butterfly(p, L);
+}
+
+/* 1 / sqrt(mean + eps), each step correctly rounded (the reference's sycl::rsqrt, h3sycl.cpp:779, 1264) */
+static inline float inv_root(float sum, int64_t n, float eps) { return 1.0f / sqrtf(sum / (float) n + eps); }
+
+/* ---- rms_norm_mod: kernels/h3sycl.cpp:766-810 (per element h3sycl.cpp:752-758, 802-806) ---- */
+typedef struct {
+    const void* x; int x_dt; int64_t C; const float* w; float eps; const int32_t* rows; const float* scale;
+    const float* shift; void* out; int out_dt;
+} rmsn_ctx;
+static void rmsn_rows(void* p, int64_t r0, int64_t r1) {
+    const rmsn_ctx* c = (const rmsn_ctx*) p;
+    const int64_t C = c->C;
+    float* row = (float*) malloc((size_t) C * sizeof(float));
+    for (int64_t r = r0; r < r1; ++r) {
+        for (int64_t i = 0; i < C; ++i) row[i] = h3o_load(c->x, c->x_dt, r * C + i);
+        const float inv = inv_root(h3o_canon_sum(row, C, vec_of(c->x_dt), 64, H3O_SUMSQ, 0.0f), C, c->eps);
+        for (int64_t i = 0; i < C; ++i) {
+            float v = row[i] * inv * c->w[i];
+            if (c->rows) {
+                const int64_t m = (int64_t) c->rows[r] * C + i;
+                v = v * (1.0f + c->scale[m]) + c->shift[m];
+            }
+            h3o_store(c->out, c->out_dt, r * C + i, v);
+        }
+    }
+    free(row);
+}
+int h3o_rms_norm_mod(const void* x, int x_dt, int64_t M, int64_t C, const float* weight, float eps, const int32_t* rows,
+                     const float* scale, const float* shift, void* out, int out_dt) {
+    if (M <= 0 || C <= 0) return 0;
+    if (!dt_ok(x_dt) || !dt_ok(out_dt)) return fail("rms_norm_mod: unknown element type");
+    const int mod = rows && scale && shift;
+    rmsn_ctx c = {x, x_dt, C, weight, eps, mod ? rows : NULL, scale, shift, out, out_dt};
+    parallel_rows(M, rmsn_rows, &c);
+    return 0;
+}
+
+/* ---- layer_norm: kernels/h3sycl.cpp:1248-1274 (two passes over the row, then (x - mean) * inv, * w, + b) ---- */
+typedef struct {
+    const void* x; int x_dt; int64_t C; const float* w; const float* b; float eps; void* out; int out_dt;
+} ln_ctx;
+static void ln_stats(const float* row, int64_t C, int V, float eps, float* mean, float* inv) {
+    *mean = h3o_canon_sum(row, C, V, 64, H3O_SUM, 0.0f) / (float) C;
+    *inv = inv_root(h3o_canon_sum(row, C, V, 64, H3O_SUMSQ_DIFF, *mean), C, eps);
+}
+static void ln_rows(void* p, int64_t r0, int64_t r1) {
+    const ln_ctx* c = (const ln_ctx*) p;
+    const int64_t C = c->C;
+    float* row = (float*) malloc((size_t) C * sizeof(float));
+    for (int64_t r = r0; r < r1; ++r) {
+        for (int64_t i = 0; i < C; ++i) row[i] = h3o_load(c->x, c->x_dt, r * C + i);
+        float mean, inv;
+        ln_stats(row, C, vec_of(c->x_dt), c->eps, &mean, &inv);
+        for (int64_t i = 0; i < C; ++i) {
+            float v = (row[i] - mean) * inv;
+            if (c->w) v *= c->w[i];
+            if (c->b) v += c->b[i];
+            h3o_store(c->out, c->out_dt, r * C + i, v);
+        }
+    }
+    free(row);
+}
+int h3o_layer_norm(const void* x, int x_dt, int64_t M, int64_t C, const float* weight, const float* bias, float eps,
+                   void* out, int out_dt) {
+    if (M <= 0 || C <= 0) return 0;
+    if (!dt_ok(x_dt) || !dt_ok(out_dt)) return fail("layer_norm: unknown element type");
+    ln_ctx c = {x, x_dt, C, weight, bias, eps, out, out_dt};
+    parallel_rows(M, ln_rows, &c);
+    return 0;
+}
+
+/* ---- rms_rope: kernels/h3sycl.cpp:1276-1376 ----
+ * Canonical per-head order: a head's D features are chunks of V; "slots" are the rotated pairs of chunks
+ * (p, p + half / V) for p < half / V, then the passed-through chunks from rot_dim on, one per slot. Slot p
+ * accumulates its chunk(s) in that order; the P slot partials (padded with zeros to a power of two) are combined by
+ * the xor butterfly. */
+static int pow2ceil(int n) { int p = 1; while (p < n) p *= 2; return p; }
+typedef struct {
+    void* x; int x_dt; int64_t H, D, stride; const float* w; float eps; const float* cs; int rot;
+} rope_ctx;
+static void rope_rows(void* p, int64_t r0, int64_t r1) {
+    const rope_ctx* c = (const rope_ctx*) p;
+    const int64_t D = c->D, half = c->rot / 2;
+    const int V = vec_of(c->x_dt);
+    const int nrot = (int) (half / V), npass = (int) ((D - c->rot) / V), P = nrot + npass, P2 = pow2ceil(P);
+    float* v = (float*) malloc((size_t) D * sizeof(float));
+    for (int64_t m = r0; m < r1; ++m)
+        for (int64_t h = 0; h < c->H; ++h) {
+            const int64_t base = m * c->stride + h * D;
+            for (int64_t i = 0; i < D; ++i) v[i] = h3o_load(c->x, c->x_dt, base + i);
+            float part[64];
+            for (int s = 0; s < P2; ++s) part[s] = 0.0f;
+            for (int s = 0; s < P; ++s) {
+                int64_t chunks[2];
+                int nc = 0;
+                if (s < nrot) { chunks[nc++] = s; chunks[nc++] = s + nrot; }
+                else chunks[nc++] = 2 * nrot + (s - nrot);
+                for (int k = 0; k < nc; ++k)
+                    for (int e = 0; e < V; ++e) {
+                        const float a = v[chunks[k] * V + e];
+                        part[s] = fmaf(a, a, part[s]);
+                    }
+            }
+            const float inv = inv_root(butterfly(part, P2), D, c->eps);
+            for (int64_t j = 0; j < half; ++j) {
+                const float a = v[j] * inv * c->w[j], b = v[half + j] * inv * c->w[half + j];
+                const int64_t t = m * half + j;
+                const float co = c->cs[2 * t], si = c->cs[2 * t + 1];
+                h3o_store(c->x, c->x_dt, base + j, a * co - b * si);
+                h3o_store(c->x, c->x_dt, base + half + j, b * co + a * si);
+            }
+            for (int64_t i = c->rot; i < D; ++i) h3o_store(c->x, c->x_dt, base + i, v[i] * inv * c->w[i]);
+        }
+    free(v);
+}
+int h3o_rms_rope(void* x, int x_dt, int64_t M, int64_t H, int64_t D, int64_t stride, const float* weight, float eps,
+                 const float* cs, int rot_dim) {
+    if (M <= 0 || H <= 0 || D <= 0) return 0;
+    if (rot_dim < 0 || rot_dim > D || rot_dim % 2 != 0 || (D - rot_dim) % 2 != 0)
+        return fail("rms_rope: rot_dim must be even, at most D, and leave an even remainder");
+    if (stride < H * D) return fail("rms_rope: the row stride is shorter than a row");
+    if (!dt_ok(x_dt)) return fail("rms_rope: unknown element type");
+    const int V = vec_of(x_dt);
+    if ((rot_dim / 2) % V != 0 || (D - rot_dim) % V != 0 || pow2ceil((int) ((rot_dim / 2) / V + (D - rot_dim) / V)) > 64)
+        return fail("rms_rope: rot_dim / 2 and D - rot_dim must be multiples of the 16-byte vector, at most 64 slots");
+    rope_ctx c = {x, x_dt, H, D, stride, weight, eps, cs, rot_dim};
+    parallel_rows(M, rope_rows, &c);
+    return 0;
+}
+
+/* ---- activations: SiLU h3sycl.cpp:1395, 1416; GELU-tanh engine/h3-core/src/audio.rs:440 ---- */
+float h3o_act(float v, int act) {
+    if (act == H3O_ACT_SILU) return v / (1.0f + expf(-v));
+    if (act == H3O_ACT_GELU_TANH) {
+        const float k = sqrtf(2.0f / 3.14159265358979323846f);
+        return 0.5f * v * (1.0f + tanhf(k * (v + 0.044715f * v * v * v)));
+    }
+    return v;
+}
+
+/* ---- swiglu: kernels/h3sycl.cpp:1378-1419 ---- */
+int h3o_swiglu(const void* x, int x_dt, int64_t M, int64_t C, void* out, int out_dt) {
+    if (M <= 0 || C <= 0) return 0;
+    for (int64_t r = 0; r < M; ++r)
+        for (int64_t i = 0; i < C; ++i) {
+            const float g = h3o_load(x, x_dt, r * 2 * C + i), u = h3o_load(x, x_dt, r * 2 * C + C + i);
+            h3o_store(out, out_dt, r * C + i, g / (1.0f + expf(-g)) * u);
+        }
+    return 0;
+}
+
+/* ---- gate_add: kernels/h3sycl.cpp:1421-1431 ---- */
+int h3o_gate_add(void* x, int x_dt, int64_t M, int64_t C, const void* other, int other_dt, const int32_t* rows,
+                 const float* gate) {
+    if (M <= 0 || C <= 0) return 0;
+    if (gate && !rows) return fail("gate_add: a gate needs the row table");
+    for (int64_t r = 0; r < M; ++r)
+        for (int64_t i = 0; i < C; ++i) {
+            const int64_t p = r * C + i;
+            const float g = gate ? gate[(int64_t) rows[r] * C + i] : 1.0f;
+            h3o_store(x, x_dt, p, h3o_load(x, x_dt, p) + h3o_load(other, other_dt, p) * g);
+        }
+    return 0;
+}
+
+/* ---- rotations ---- */
+/* regular: one base-4 digit at a time, low digit first; for the four values x0..x3 that differ only in that digit,
+ * t = ((x0 + x1) + x2) + x3 and y_a = t - 2 x_(3-a) (kernels/h3sycl.cpp:408-412, 433-459); then * 1/sqrt(g), a power
+ * of two. Sylvester: h = 1, 2, ..., g/2, (a, b) -> (a + b, a - b); then * fl(1/sqrt(g)). */
+void h3o_rotate_group(float* y, int g, int kind) {
+    if (kind == H3O_ROT_REGULAR) {
+        for (int d = 1; d < g; d *= 4)
+            for (int i = 0; i < g; ++i) {
+                if ((i / d) % 4 != 0) continue;
+                const float x0 = y[i], x1 = y[i + d], x2 = y[i + 2 * d], x3 = y[i + 3 * d];
+                const float t = x0 + x1 + x2 + x3;
+                y[i] = t - 2.0f * x3;
+                y[i + d] = t - 2.0f * x2;
+                y[i + 2 * d] = t - 2.0f * x1;
+                y[i + 3 * d] = t - 2.0f * x0;
+            }
+    } else if (kind == H3O_ROT_SYLVESTER) {
+        for (int h = 1; h < g; h *= 2)
+            for (int i = 0; i < g; ++i) {
+                if (i & h) continue;
+                const float a = y[i], b = y[i + h];
+                y[i] = a + b;
+                y[i + h] = a - b;
+            }
+    } else return;
+    const float c = (float) (1.0 / sqrt((double) g));
+    for (int i = 0; i < g; ++i) y[i] = y[i] * c;
+}
+void h3o_hadamard_regular(int g, float* h) {                                                   /* reference.rs:4-23 */
+    static const int h4[4][4] = {{1, 1, 1, -1}, {1, 1, -1, 1}, {1, -1, 1, 1}, {-1, 1, 1, 1}};
+    const float norm = 1.0f / sqrtf((float) g);
+    for (int i = 0; i < g; ++i)
+        for (int j = 0; j < g; ++j) {
+            int a = i, b = j, s = 1, sign = 1;
+            while (s < g) { sign *= h4[a % 4][b % 4]; a /= 4; b /= 4; s *= 4; }
+            h[(int64_t) i * g + j] = (float) sign * norm;
+        }
+}
+void h3o_hadamard_sylvester(int g, float* h) {
+    const float norm = (float) (1.0 / sqrt((double) g));
+    for (int i = 0; i < g; ++i)
+        for (int j = 0; j < g; ++j) h[(int64_t) i * g + j] = (__builtin_popcount((unsigned) (i & j)) & 1) ? -norm : norm;
+}
+
+/* ---- quantizer: kernels/h3sycl.h:74-83; h3sycl.cpp:465-472, 556-573; reference.rs:68-70 ---- */
+static void quantize_row(const float* y, int64_t K, int8_t* q, float* s) {
+    float m = 0.0f;
+    for (int64_t i = 0; i < K; ++i) m = fmaxf(m, fabsf(y[i]));
+    const float sc = fmaxf(m / 127.0f, 1e-30f);
+    *s = sc;
+    for (int64_t i = 0; i < K; ++i) {
+        float v = rintf(y[i] / sc);
+        v = v < -128.0f ? -128.0f : v > 127.0f ? 127.0f : v;
+        q[i] = (int8_t) v;
+    }
+}
+void h3o_quantize_rows(const float* y, int64_t M, int64_t K, int8_t* q, float* s) {
+    for (int64_t r = 0; r < M; ++r) quantize_row(y + r * K, K, q + r * K, s + r);
+}
+
+/* ---- int8 GEMM + dequant epilogue: kernels/h3sycl.cpp:576-629, reference.rs:72-76 ----
+ * One weight scale: the row factor is fl(s_r * wscale[0]) (h3sycl.cpp:576), out = acc * factor. One per output:
+ * out = (acc * s_r) * wscale[n] (the post-op chain h3sycl.cpp:588-602). Then + bias[n], then the activation. */
+typedef struct {
+    const int8_t* q; const float* s; int64_t K; const int8_t* w; int64_t N; const float* ws; int64_t nws;
+    const float* bias; int act; void* out; int out_dt;
+} gemm_ctx;
+static void gemm_rows(void* p, int64_t r0, int64_t r1) {
+    const gemm_ctx* c = (const gemm_ctx*) p;
+    const int64_t K = c->K;
+    for (int64_t r = r0; r < r1; ++r) {
+        const int8_t* qr = c->q + r * K;
+        const float sr = c->s[r];
+        const float f1 = sr * c->ws[0];
+        for (int64_t n = 0; n < c->N; ++n) {
+            const int8_t* wr = c->w + n * K;
+            int32_t acc = 0;
+            for (int64_t k = 0; k < K; ++k) acc += (int32_t) qr[k] * (int32_t) wr[k];
+            float v = c->nws == 1 ? (float) acc * f1 : (float) acc * sr * c->ws[n];
+            if (c->bias) v = v + c->bias[n];
+            v = h3o_act(v, c->act);
+            h3o_store(c->out, c->out_dt, r * c->N + n, v);
+        }
+    }
+}
+int h3o_gemm_dequant(const int8_t* q, const float* s, int64_t M, int64_t K, const int8_t* w, int64_t N, const float* wscale,
+                     int64_t n_wscale, const float* bias, int act, void* out, int out_dt) {
+    if (M <= 0 || K <= 0 || N <= 0) return 0;
+    if (n_wscale != 1 && n_wscale != N) return fail("gemm_dequant: 1 or N weight scales");
+    gemm_ctx c = {q, s, K, w, N, wscale, n_wscale, bias, act, out, out_dt};
+    parallel_rows(M, gemm_rows, &c);
+    return 0;
+}
+
+/* ---- int8_linear: kernels/h3sycl.h:74-85; h3sycl.cpp:633-652 ---- */
+typedef struct { const void* x; int x_dt; int64_t K; int group; int8_t* q; float* s; } quant_ctx;
+static void quant_rows(void* p, int64_t r0, int64_t r1) {
+    const quant_ctx* c = (const quant_ctx*) p;
+    float* y = (float*) malloc((size_t) c->K * sizeof(float));
+    for (int64_t r = r0; r < r1; ++r) {
+        for (int64_t i = 0; i < c->K; ++i) y[i] = h3o_load(c->x, c->x_dt, r * c->K + i);
+        if (c->group > 0)
+            for (int64_t g0 = 0; g0 < c->K; g0 += c->group) h3o_rotate_group(y + g0, c->group, H3O_ROT_REGULAR);
+        quantize_row(y, c->K, c->q + r * c->K, c->s + r);
+    }
+    free(y);
+}
+static int is_pow4(int g) { return g > 0 && (g & (g - 1)) == 0 && (__builtin_ctz((unsigned) g) % 2) == 0; }
+int h3o_int8_linear(const void* x, int x_dt, int64_t M, int64_t K, const int8_t* w, int64_t N, const float* wscale,
+                    int64_t n_wscale, const float* bias, void* out, int out_dt, int group) {
+    if (M <= 0 || K <= 0 || N <= 0) return 0;
+    if (group > 0 && (group > 256 || K % group != 0 || !is_pow4(group)))
+        return fail("int8_linear: the ConvRot group must be a power of 4, at most 256, dividing K");
+    int8_t* q = (int8_t*) malloc((size_t) (M * K));
+    float* s = (float*) malloc((size_t) M * sizeof(float));
+    quant_ctx qc = {x, x_dt, K, group, q, s};
+    parallel_rows(M, quant_rows, &qc);
+    const int rc = h3o_gemm_dequant(q, s, M, K, w, N, wscale, n_wscale, bias, H3O_ACT_NONE, out, out_dt);
+    free(q);
+    free(s);
+    return rc;
+}
+
+/* ---- fused chains ---- */
+typedef struct {
+    const void* x; int x_dt; int64_t C; const float* w; float eps; const int32_t* rows; const void* scale;
+    const void* shift; int tab_dt; int h_dt; int rot; int group; int8_t* q; float* s;
+} nq_ctx;
+static void nq_rows(void* p, int64_t r0, int64_t r1) {
+    const nq_ctx* c = (const nq_ctx*) p;
+    const int64_t C = c->C;
+    float* y = (float*) malloc((size_t) C * sizeof(float));
+    for (int64_t r = r0; r < r1; ++r) {
+        for (int64_t i = 0; i < C; ++i) y[i] = h3o_load(c->x, c->x_dt, r * C + i);
+        const float inv = inv_root(h3o_canon_sum(y, C, vec_of(c->x_dt), 64, H3O_SUMSQ, 0.0f), C, c->eps);
+        const int64_t tr = c->rows ? c->rows[r] : 0;
+        for (int64_t i = 0; i < C; ++i) {
+            float v = y[i] * inv;
+            if (c->w) v = v * c->w[i];
+            if (c->scale && c->shift) {
+                const float sc = h3o_load(c->scale, c->tab_dt, tr * C + i), sh = h3o_load(c->shift, c->tab_dt, tr * C + i);
+                v = v * (1.0f + sc) + sh;
+            }
+            y[i] = h3o_round_to(v, c->h_dt);
+        }
+        if (c->rot != H3O_ROT_NONE)
+            for (int64_t g0 = 0; g0 < C; g0 += c->group) h3o_rotate_group(y + g0, c->group, c->rot);
+        quantize_row(y, C, c->q + r * C, c->s + r);
+    }
+    free(y);
+}
+int h3o_norm_quant(const void* x, int x_dt, int64_t M, int64_t C, const float* weight, float eps, const int32_t* rows,
+                   const void* scale, const void* shift, int tab_dt, int h_dt, int rot, int group, int8_t* q, float* s) {
+    if (M <= 0 || C <= 0) return 0;
+    if (!dt_ok(x_dt) || !dt_ok(h_dt) || !dt_ok(tab_dt)) return fail("norm_quant: unknown element type");
+    if (rot == H3O_ROT_REGULAR && (!is_pow4(group) || C % group != 0)) return fail("norm_quant: regular rotation needs g = 4^k dividing C");
+    if (rot == H3O_ROT_SYLVESTER && (group < 2 || (group & (group - 1)) != 0 || C % group != 0))
+        return fail("norm_quant: Sylvester rotation needs g = 2^k dividing C");
+    nq_ctx c = {x, x_dt, C, weight, eps, rows, scale, shift, tab_dt, h_dt, rot, group, q, s};
+    parallel_rows(M, nq_rows, &c);
+    return 0;
+}
+
+typedef struct {
+    const void* x; int x_dt; int64_t C; int norm; const float* w; const float* b; float eps; const int32_t* rows;
+    const void* scale; const void* shift; const void* gate; int tab_dt; int act; const void* res; int res_dt; void* out;
+    int out_dt;
+} nmag_ctx;
+static void nmag_rows(void* p, int64_t r0, int64_t r1) {
+    const nmag_ctx* c = (const nmag_ctx*) p;
+    const int64_t C = c->C;
+    const int V = vec_of(c->x_dt);
+    float* row = (float*) malloc((size_t) C * sizeof(float));
+    for (int64_t r = r0; r < r1; ++r) {
+        for (int64_t i = 0; i < C; ++i) row[i] = h3o_load(c->x, c->x_dt, r * C + i);
+        float mean = 0.0f, inv;
+        if (c->norm == H3O_NORM_LAYER) ln_stats(row, C, V, c->eps, &mean, &inv);
+        else inv = inv_root(h3o_canon_sum(row, C, V, 64, H3O_SUMSQ, 0.0f), C, c->eps);
+        const int64_t tr = c->rows ? c->rows[r] : 0;
+        for (int64_t i = 0; i < C; ++i) {
+            float v = c->norm == H3O_NORM_LAYER ? (row[i] - mean) * inv : row[i] * inv;
+            if (c->w) v = v * c->w[i];
+            if (c->b) v = v + c->b[i];
+            if (c->scale && c->shift) {
+                const float sc = h3o_load(c->scale, c->tab_dt, tr * C + i), sh = h3o_load(c->shift, c->tab_dt, tr * C + i);
+                v = v * (1.0f + sc) + sh;
+            }
+            v = h3o_act(v, c->act);
+            if (c->gate) v = v * h3o_load(c->gate, c->tab_dt, tr * C + i);
+            if (c->res) v = h3o_load(c->res, c->res_dt, r * C + i) + v;
+            h3o_store(c->out, c->out_dt, r * C + i, v);
+        }
+    }
+    free(row);
+}
+int h3o_norm_mod_act_gate(const void* x, int x_dt, int64_t M, int64_t C, int norm, const float* weight,
+                          const float* bias, float eps, const int32_t* rows, const void* scale, const void* shift,
+                          const void* gate, int tab_dt, int act, const void* res, int res_dt, void* out, int out_dt) {
+    if (M <= 0 || C <= 0) return 0;
+    if (!dt_ok(x_dt) || !dt_ok(tab_dt) || !dt_ok(res_dt) || !dt_ok(out_dt)) return fail("norm_mod_act_gate: unknown element type");
+    nmag_ctx c = {x, x_dt, C, norm, weight, bias, eps, rows, scale, shift, gate, tab_dt, act, res, res_dt, out, out_dt};
+    parallel_rows(M, nmag_rows, &c);
+    return 0;
+}
+
+/* ---- reference::compare: engine/h3-core/src/reference.rs:84-95 ---- */
+void h3o_compare(const float* a, const float* b, int64_t n, double* rel, double* cos) {
+    double d2 = 0, a2 = 0, b2 = 0, ab = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const double x = a[i], y = b[i];
+        d2 += (x - y) * (x - y);
+        a2 += x * x;
+        b2 += y * y;
+        ab += x * y;
+    }
+    *rel = sqrt(d2 / (b2 > 1e-300 ? b2 : 1e-300));
+    const double den = sqrt(a2) * sqrt(b2);
+    *cos = ab / (den > 1e-300 ? den : 1e-300);
+}

@@ -1,0 +1,245 @@
+// common.h - what every translation unit of libh3hip.so shares: the context, the error convention, and the
+// device-side helpers (element conversions, 16-byte vector access, cross-lane exchanges of a 64-wide wavefront).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/h3hip.h"
+
+#define H3S_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace h3 {
+
+// ---- host side -------------------------------------------------------------------------------------------------
+
+// the per-thread error message of h3s_last_error (kernels/h3sycl.cpp:40)
+void set_error(const std::string& msg);
+int fail(const std::string& msg);          // sets the message, returns -1
+
+struct Ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;          // kernels run here, in call order
+    bool own_stream = false;
+    hipStream_t copy_stream = nullptr;     // h3s_upload, made on first use
+    std::mutex copy_mu;
+    std::string name;
+    bool poison = false;                   // H3S_POISON: fresh buffers filled with 0xff bytes
+    // the allocation book (kernels/h3sycl.cpp:149-151): allocations and scratch counted against one cap
+    std::mutex mem_mu;
+    std::unordered_map<void*, size_t> mem;
+    size_t mem_used = 0, mem_cap = 0;
+    // scratch of h3s_int8_linear: the int8 activations and the row scales of one row chunk
+    int8_t* xq = nullptr; size_t xq_cap = 0;
+    float* rs = nullptr; size_t rs_cap = 0;
+
+    // A scratch buffer of at least n elements, counted against the cap; NULL with the reason on failure.
+    template <typename T> T* grow(T*& p, size_t& cap, size_t n);
+};
+
+// the context of an entry point: NULL with an error when ctx is NULL; makes its device current
+Ctx* ctx_of(void* ctx, const char* fn);
+// the status of the last launch on this thread, as an error naming fn
+int launched(const char* fn);
+
+// the quantizer of h3s_int8_linear (rownorm.hip): x [M, K] -> regular rotation per group (0: none) -> q, s
+int launch_quantize(Ctx* c, const void* x, int x_dt, int64_t M, int64_t K, int group, int8_t* q, float* s);
+
+inline bool aligned16(const void* p) { return ((uintptr_t) p & 15) == 0; }
+inline int elem_size(int dt) { return dt == H3S_F32 ? 4 : 2; }
+inline bool dt_ok(int dt) { return dt == H3S_F32 || dt == H3S_F16 || dt == H3S_BF16; }
+inline int vec_of(int dt) { return 16 / elem_size(dt); }   // elements in one 16-byte vector
+
+template <typename T> T* Ctx::grow(T*& p, size_t& cap, size_t n) {
+    if (n <= cap) return p;
+    const size_t want = n + (n >> 3);
+    std::lock_guard<std::mutex> l(mem_mu);
+    if (mem_used - cap * sizeof(T) + want * sizeof(T) > mem_cap) {
+        set_error("a scratch buffer of " + std::to_string((want * sizeof(T)) >> 20) + " MiB would pass the device memory cap (" +
+                  std::to_string(mem_used >> 20) + " of " + std::to_string(mem_cap >> 20) + " MiB in use)");
+        return nullptr;
+    }
+    if (p) { (void) hipStreamSynchronize(stream); (void) hipFree(p); }
+    mem_used -= cap * sizeof(T);
+    cap = 0;
+    void* q = nullptr;
+    if (hipMalloc(&q, want * sizeof(T)) != hipSuccess) {
+        p = nullptr;
+        set_error("the device refused a scratch buffer of " + std::to_string((want * sizeof(T)) >> 20) + " MiB");
+        return nullptr;
+    }
+    p = (T*) q;
+    cap = want;
+    mem_used += cap * sizeof(T);
+    return p;
+}
+
+// ---- device side -----------------------------------------------------------------------------------------------
+
+constexpr int kWave = 64;
+
+// bf16 <-> f32: widen by shifting; narrow with the hardware's round-to-nearest-even (finite values: the same bits
+// as kernels/h3sycl.cpp:42-49; a NaN stays a NaN)
+__device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    f2 v = {a, b};
+    bf2 r = __builtin_convertvector(v, bf2);
+    uint32_t u;
+    __builtin_memcpy(&u, &r, 4);
+    return u;
+}
+__device__ __forceinline__ float round_bf16(float v) { return bf16_lo(pack_bf16(v, 0.0f)); }
+__device__ __forceinline__ float f16_lo(uint32_t u) { _Float16 h; uint16_t b = (uint16_t) u; __builtin_memcpy(&h, &b, 2); return (float) h; }
+__device__ __forceinline__ float f16_hi(uint32_t u) { return f16_lo(u >> 16); }
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
+    _Float16 ha = (_Float16) a, hb = (_Float16) b;
+    uint16_t ua, ub;
+    __builtin_memcpy(&ua, &ha, 2);
+    __builtin_memcpy(&ub, &hb, 2);
+    return (uint32_t) ua | ((uint32_t) ub << 16);
+}
+__device__ __forceinline__ float round_f16(float v) { return (float) (_Float16) v; }
+
+// a 16-byte vector of element type DT as floats (V = 8 for 16-bit types, 4 for float32)
+template <int DT> struct Vec;
+template <> struct Vec<H3S_BF16> {
+    static constexpr int V = 8;
+    __device__ static __forceinline__ void unpack(const uint4& u, float* f) {
+        f[0] = bf16_lo(u.x); f[1] = bf16_hi(u.x); f[2] = bf16_lo(u.y); f[3] = bf16_hi(u.y);
+        f[4] = bf16_lo(u.z); f[5] = bf16_hi(u.z); f[6] = bf16_lo(u.w); f[7] = bf16_hi(u.w);
+    }
+    __device__ static __forceinline__ uint4 pack(const float* f) {
+        return make_uint4(pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]), pack_bf16(f[6], f[7]));
+    }
+    __device__ static __forceinline__ float round(float v) { return round_bf16(v); }
+};
+template <> struct Vec<H3S_F16> {
+    static constexpr int V = 8;
+    __device__ static __forceinline__ void unpack(const uint4& u, float* f) {
+        f[0] = f16_lo(u.x); f[1] = f16_hi(u.x); f[2] = f16_lo(u.y); f[3] = f16_hi(u.y);
+        f[4] = f16_lo(u.z); f[5] = f16_hi(u.z); f[6] = f16_lo(u.w); f[7] = f16_hi(u.w);
+    }
+    __device__ static __forceinline__ uint4 pack(const float* f) {
+        return make_uint4(pack_f16(f[0], f[1]), pack_f16(f[2], f[3]), pack_f16(f[4], f[5]), pack_f16(f[6], f[7]));
+    }
+    __device__ static __forceinline__ float round(float v) { return round_f16(v); }
+};
+template <> struct Vec<H3S_F32> {
+    static constexpr int V = 4;
+    __device__ static __forceinline__ void unpack(const uint4& u, float* f) {
+        f[0] = __uint_as_float(u.x); f[1] = __uint_as_float(u.y); f[2] = __uint_as_float(u.z); f[3] = __uint_as_float(u.w);
+    }
+    __device__ static __forceinline__ uint4 pack(const float* f) {
+        return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
+    }
+    __device__ static __forceinline__ float round(float v) { return v; }
+};
+
+// 8 consecutive float32 values (two 16-byte loads) and 8 table values of type TDT
+__device__ __forceinline__ void load_f32x(const float* p, float* f, int n) {
+#pragma unroll
+    for (int k = 0; k < n; k += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(p + k);
+        f[k] = v.x; f[k + 1] = v.y; f[k + 2] = v.z; f[k + 3] = v.w;
+    }
+}
+template <int TDT> __device__ __forceinline__ void load_tab(const void* p, int64_t i, float* f, int n) {
+    if constexpr (TDT == H3S_F32) {
+        load_f32x((const float*) p + i, f, n);
+    } else {
+        // n values of a 16-bit table: n / 8 16-byte loads, or one 8-byte load for n = 4
+        if (n == 4) {
+            const uint2 u = *reinterpret_cast<const uint2*>((const uint16_t*) p + i);
+            float g[8];
+            Vec<TDT>::unpack(make_uint4(u.x, u.y, 0, 0), g);
+            f[0] = g[0]; f[1] = g[1]; f[2] = g[2]; f[3] = g[3];
+        } else {
+#pragma unroll
+            for (int k = 0; k < n; k += 8) Vec<TDT>::unpack(*reinterpret_cast<const uint4*>((const uint16_t*) p + i + k), f + k);
+        }
+    }
+}
+
+// ---- cross-lane exchanges inside a 64-wide wavefront ----
+// value of lane (lane ^ OFF). 1, 2: quad permutes; 4: two row shifts, each for half of the lanes; 8: a row rotate;
+// 16: a swizzle inside each half of the wave; 32: a permute through the LDS crossbar.
+template <int OFF> __device__ __forceinline__ float xor_lane(float v) {
+    const int x = __float_as_int(v);
+    int r;
+    if constexpr (OFF == 1) r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);        // quad_perm [1,0,3,2]
+    else if constexpr (OFF == 2) r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    else if constexpr (OFF == 4) {
+        const int t = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0x5, false);                   // row_shl:4, lanes 0-3, 8-11
+        r = __builtin_amdgcn_update_dpp(t, x, 0x114, 0xF, 0xA, false);                             // row_shr:4, lanes 4-7, 12-15
+    } else if constexpr (OFF == 8) r = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);  // row_ror:8
+    else if constexpr (OFF == 16) r = __builtin_amdgcn_ds_swizzle(x, 0x401F);                     // xor 16 within 32
+    else {
+        static_assert(OFF == 32, "xor_lane: offsets 1..32");
+        r = __builtin_amdgcn_ds_bpermute((int) ((__lane_id() ^ 32u) << 2), x);
+    }
+    return __int_as_float(r);
+}
+
+// the canonical butterfly over the lanes of a wave (offsets L/2 .. 1); every lane ends with the same sum
+template <int L> __device__ __forceinline__ float wave_sum(float s) {
+    if constexpr (L >= 64) s = s + xor_lane<32>(s);
+    if constexpr (L >= 32) s = s + xor_lane<16>(s);
+    if constexpr (L >= 16) s = s + xor_lane<8>(s);
+    if constexpr (L >= 8) s = s + xor_lane<4>(s);
+    if constexpr (L >= 4) s = s + xor_lane<2>(s);
+    if constexpr (L >= 2) s = s + xor_lane<1>(s);
+    return s;
+}
+template <int L> __device__ __forceinline__ float wave_max(float m) {
+    if constexpr (L >= 64) m = fmaxf(m, xor_lane<32>(m));
+    if constexpr (L >= 32) m = fmaxf(m, xor_lane<16>(m));
+    if constexpr (L >= 16) m = fmaxf(m, xor_lane<8>(m));
+    if constexpr (L >= 8) m = fmaxf(m, xor_lane<4>(m));
+    if constexpr (L >= 4) m = fmaxf(m, xor_lane<2>(m));
+    if constexpr (L >= 2) m = fmaxf(m, xor_lane<1>(m));
+    return m;
+}
+
+// 1 / sqrt(mean + eps), each step correctly rounded (built with correctly rounded f32 division and square root)
+__device__ __forceinline__ float inv_root(float sum, float n, float eps) { return 1.0f / __builtin_sqrtf(sum / n + eps); }
+
+// rint(y / s) with y / s correctly rounded: q1 = y * r, e = y - q1 * s (exact, one fma), q = q1 + e * r, where
+// r = fl(1 / s) is the correctly rounded reciprocal (Markstein's division correction). Then round half to even.
+__device__ __forceinline__ float quant_code(float y, float s, float r) {
+    const float q1 = y * r;
+    const float e = __builtin_fmaf(-q1, s, y);
+    const float q = __builtin_fmaf(e, r, q1);
+    return fminf(fmaxf(__builtin_rintf(q), -128.0f), 127.0f);
+}
+// four codes (each in [-128, 127]) as the bytes of one word, lowest first
+__device__ __forceinline__ uint32_t pack_i8x4(float a, float b, float c, float d) {
+    const uint32_t ia = (uint32_t) (int) a & 0xffu, ib = (uint32_t) (int) b & 0xffu, ic = (uint32_t) (int) c & 0xffu,
+                   id = (uint32_t) (int) d & 0xffu;
+    return ia | (ib << 8) | (ic << 16) | (id << 24);
+}
+
+// pointwise activations (float32): SiLU g / (1 + e^-g) (kernels/h3sycl.cpp:1395); GELU-tanh
+// 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))) (engine/h3-core/src/audio.rs:440), evaluated as
+// v / (1 + e^(-2u)), u = sqrt(2/pi) (v + 0.044715 v^3), the same function: 0.5 (1 + tanh u) = 1 / (1 + e^(-2u)).
+__device__ __forceinline__ float act_silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+__device__ __forceinline__ float act_gelu_tanh(float v) {
+    // e^(-2u) = 2^(v * (A + B v^2)), A = -2 log2(e) sqrt(2/pi), B = A * 0.044715
+    const float A = -2.3022082f, B = -0.10294324f;
+    const float e = __builtin_amdgcn_exp2f(v * __builtin_fmaf(B, v * v, A));
+    return v * __builtin_amdgcn_rcpf(1.0f + e);
+}
+template <int ACT> __device__ __forceinline__ float act(float v) {
+    if constexpr (ACT == H3S_ACT_SILU) return act_silu(v);
+    else if constexpr (ACT == H3S_ACT_GELU_TANH) return act_gelu_tanh(v);
+    else return v;
+}
+
+}  // namespace h3

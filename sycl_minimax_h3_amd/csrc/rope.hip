@@ -1,0 +1,155 @@
+// rope.hip - h3s_rms_rope (kernels/h3sycl.cpp:1276-1376) and the fused pair h3s_qk_rms_rope: per-head RMS norm and
+// the rotary rotation of pairs (j, rot/2 + j), in place, q and k of a token in one wave.
+//
+// A head's D features are 16-byte chunks. A "slot" is one lane's share of a head: a rotated pair of chunks
+// (p, p + rot/2/V) - the lane then owns both values of each of its pairs, so the rotation needs no exchange - or
+// one passed-through chunk. A head takes P2 lanes (its slot count rounded up to a power of two), so a wave holds
+// 64 / P2 heads side by side; the head's sum of squares is the lane's own in chunk order, then an xor butterfly over
+// its P2 lanes: the canonical order of the CPU oracle. One wave per token: it reads the token's cos/sin row once
+// and the weights once, then every head of q and of k.
+#include "common.h"
+
+namespace h3 {
+
+constexpr int kUnits = 8;   // (tensor, head group) units whose loads are in flight together
+
+template <int XDT, int P2>
+__global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M, int H, int D, int64_t stride,
+                                                   const float* __restrict__ w0, const float* __restrict__ w1, float eps,
+                                                   const float* __restrict__ cs, int rot) {
+    constexpr int V = Vec<XDT>::V;
+    constexpr int HPW = kWave / P2;   // heads side by side in a wave
+    const int lane = threadIdx.x & 63;
+    const int64_t tok = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (tok >= M) return;
+    const int half = rot / 2, nrot = half / V, npass = (D - rot) / V, P = nrot + npass;
+    const int slot = lane % P2, hh = lane / P2;
+    const bool active = slot < P, rotated = slot < nrot;
+    const int off0 = rotated ? slot * V : rot + (slot - nrot) * V;   // this lane's chunk(s) inside the head
+    const int off1 = half + slot * V;
+
+    float co[V], si[V];
+    if (rotated) {
+        const float* c = cs + (tok * half + (int64_t) slot * V) * 2;
+#pragma unroll
+        for (int k = 0; k < 2 * V; k += 4) {
+            const float4 t = *reinterpret_cast<const float4*>(c + k);
+            co[k / 2] = t.x; si[k / 2] = t.y; co[k / 2 + 1] = t.z; si[k / 2 + 1] = t.w;
+        }
+    }
+    const int ngroups = (H + HPW - 1) / HPW;
+    const int ntens = x1 ? 2 : 1;
+    const int nunits = ntens * ngroups;
+    for (int u0 = 0; u0 < nunits; u0 += kUnits) {
+        uint4 ra[kUnits], rb[kUnits];
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            const int u = u0 + k, t = u / ngroups, head = (u % ngroups) * HPW + hh;
+            const bool ok = u < nunits && active && head < H;
+            const uint16_t* base = (const uint16_t*) (t ? x1 : x0) + (tok * stride + (int64_t) head * D) * (16 / V / 2);
+            ra[k] = ok ? *reinterpret_cast<const uint4*>(base + off0 * (16 / V / 2)) : make_uint4(0, 0, 0, 0);
+            rb[k] = ok && rotated ? *reinterpret_cast<const uint4*>(base + off1 * (16 / V / 2)) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            const int u = u0 + k;
+            if (u >= nunits) break;   // uniform across the wave
+            const int t = u / ngroups, head = (u % ngroups) * HPW + hh;
+            const bool ok = active && head < H;
+            float a[V], b[V];
+            Vec<XDT>::unpack(ra[k], a);
+            Vec<XDT>::unpack(rb[k], b);
+            float s = 0.0f;
+#pragma unroll
+            for (int e = 0; e < V; ++e) s = __builtin_fmaf(a[e], a[e], s);
+            if (rotated)
+#pragma unroll
+                for (int e = 0; e < V; ++e) s = __builtin_fmaf(b[e], b[e], s);
+            s = wave_sum<P2>(s);
+            if (!ok) continue;
+            const float inv = inv_root(s, (float) D, eps);
+            const float* w = t ? w1 : w0;
+            float wa[V];
+            load_f32x(w + off0, wa, V);
+            uint16_t* base = (uint16_t*) (t ? x1 : x0) + (tok * stride + (int64_t) head * D) * (16 / V / 2);
+            if (rotated) {
+                float wb[V], oa[V], ob[V];
+                load_f32x(w + off1, wb, V);
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const float A = a[e] * inv * wa[e], B = b[e] * inv * wb[e];
+                    oa[e] = A * co[e] - B * si[e];
+                    ob[e] = B * co[e] + A * si[e];
+                }
+                *reinterpret_cast<uint4*>(base + off0 * (16 / V / 2)) = Vec<XDT>::pack(oa);
+                *reinterpret_cast<uint4*>(base + off1 * (16 / V / 2)) = Vec<XDT>::pack(ob);
+            } else {
+                float oa[V];
+#pragma unroll
+                for (int e = 0; e < V; ++e) oa[e] = a[e] * inv * wa[e];
+                *reinterpret_cast<uint4*>(base + off0 * (16 / V / 2)) = Vec<XDT>::pack(oa);
+            }
+        }
+    }
+}
+
+static int pow2ceil(int n) { int p = 1; while (p < n) p *= 2; return p; }
+
+static int rope_launch(const char* fn, void* ctx, void* x0, void* x1, int x_dt, int64_t M, int64_t H, int64_t D,
+                       int64_t stride, const float* w0, const float* w1, float eps, const float* cs, int rot_dim) {
+    if (M <= 0 || H <= 0 || D <= 0) return 0;
+    if (rot_dim < 0 || rot_dim > D || rot_dim % 2 != 0 || (D - rot_dim) % 2 != 0)
+        return fail(std::string(fn) + ": rot_dim must be even, at most D, and leave an even remainder");
+    if (stride < H * D) return fail(std::string(fn) + ": the row stride is shorter than a row");
+    if (!dt_ok(x_dt)) return fail(std::string(fn) + ": unknown element type");
+    const int V = vec_of(x_dt);
+    const int64_t half = rot_dim / 2;
+    if (half % V != 0 || (D - rot_dim) % V != 0 || stride % V != 0)
+        return fail(std::string(fn) + ": rot_dim / 2, D - rot_dim and the stride must be whole 16-byte vectors (multiples of " +
+                    std::to_string(V) + ")");
+    const int P = (int) (half / V + (D - rot_dim) / V);
+    const int P2 = pow2ceil(P);
+    if (P2 > kWave) return fail(std::string(fn) + ": a head of more than 64 16-byte slots is not supported");
+    if (H > (1 << 24)) return fail(std::string(fn) + ": too many heads");
+    if (!w0 || (x1 && !w1)) return fail(std::string(fn) + ": the norm weight is required");
+    if (rot_dim > 0 && !cs) return fail(std::string(fn) + ": the rotation table is required");
+    for (const void* p : {(const void*) x0, (const void*) x1, (const void*) w0, (const void*) w1, (const void*) cs})
+        if (p && !aligned16(p)) return fail(std::string(fn) + ": tensors must be 16-byte aligned");
+    Ctx* c = ctx_of(ctx, fn);
+    if (!c) return -1;
+    const unsigned grid = (unsigned) ((M + 3) / 4);
+#define LP(XDT, PP) rope_kernel<XDT, PP><<<grid, 256, 0, c->stream>>>(x0, x1, M, (int) H, (int) D, stride, w0, w1, eps, cs, rot_dim)
+#define LD(XDT)                         \
+    switch (P2) {                       \
+        case 1: LP(XDT, 1); break;      \
+        case 2: LP(XDT, 2); break;      \
+        case 4: LP(XDT, 4); break;      \
+        case 8: LP(XDT, 8); break;      \
+        case 16: LP(XDT, 16); break;    \
+        case 32: LP(XDT, 32); break;    \
+        default: LP(XDT, 64); break;    \
+    }
+    switch (x_dt) {
+        case H3S_BF16: LD(H3S_BF16); break;
+        case H3S_F16: LD(H3S_F16); break;
+        default: LD(H3S_F32); break;
+    }
+#undef LD
+#undef LP
+    return launched(fn);
+}
+
+}  // namespace h3
+
+using namespace h3;
+
+H3S_EXPORT int h3s_rms_rope(void* ctx, void* x, int x_dt, int64_t M, int64_t H, int64_t D, int64_t stride, const float* weight,
+                            float eps, const float* cs, int rot_dim) try {
+    return rope_launch("h3s_rms_rope", ctx, x, nullptr, x_dt, M, H, D, stride, weight, nullptr, eps, cs, rot_dim);
+} catch (const std::exception& e) { return fail(e.what()); }
+
+H3S_EXPORT int h3s_qk_rms_rope(void* ctx, void* q, void* k, int x_dt, int64_t M, int64_t H, int64_t D, int64_t stride,
+                               const float* wq, const float* wk, float eps, const float* cs, int rot_dim) try {
+    if (!q || !k) return fail("h3s_qk_rms_rope: q and k are required");
+    return rope_launch("h3s_qk_rms_rope", ctx, q, k, x_dt, M, H, D, stride, wq, wk, eps, cs, rot_dim);
+} catch (const std::exception& e) { return fail(e.what()); }

@@ -1,0 +1,260 @@
+"""The kernels, with types and shapes checked on the way in (mirror of engine/h3-core/src/ops.rs).
+
+Each call queues work on the device's stream and returns; the result is there for the next call that uses it. The
+names, argument meanings and error behaviour follow ops.rs: a type or shape that does not fit raises ``Error``
+before anything is queued, and a failing library call raises ``Error`` with the library's message. The fused
+entry points of include/h3hip.h come after the reference's operations.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+from . import api as _api
+from .device import DType, Error, Tensor
+
+
+def _floats(t: Tensor, what: str, n: int) -> int:
+    """ops.rs:11-16."""
+    if t.dtype != DType.F32 or t.elements() < n:
+        raise Error(f"{what} must be float32 with at least {n} values, got {t.dtype} {t.shape}")
+    return t.ptr()
+
+
+def _row_table(t: Tensor, m: int) -> int:
+    """ops.rs:18-23."""
+    if t.dtype != DType.I32 or t.elements() != m:
+        raise Error(f"the row table must be int32 [{m}], got {t.dtype} {t.shape}")
+    return t.ptr()
+
+
+def _dev(t: Tensor):
+    if t.dev is None:
+        raise Error("the tensor has no device")
+    return t.dev
+
+
+@dataclass
+class Int8Linear:
+    """A linear layer with int8 weights (ops.rs:25-35)."""
+
+    weight: Tensor            # int8 [N, K]
+    scale: Tensor             # float32, 1 or N values
+    bias: Tensor | None = None
+    group: int | None = None  # ConvRot group size, when the weights were stored rotated
+
+    def inputs(self) -> int:
+        return self.weight.shape[1]
+
+    def outputs(self) -> int:
+        return self.weight.shape[0]
+
+    def forward(self, x: Tensor, out: Tensor) -> None:
+        """out = linear(x): x [M, K] in a float type, out [M, N] in out's type (ops.rs:46-83)."""
+        n, k = self.outputs(), self.inputs()
+        m = x.elements() // k
+        if self.weight.dtype != DType.I8 or self.scale.dtype != DType.F32:
+            raise Error("int8_linear: the weight must be int8 and its scale float32")
+        if x.elements() != m * k or out.elements() != m * n:
+            raise Error(f"int8_linear: x {x.shape} and out {out.shape} do not fit a [{n}, {k}] weight")
+        ns = self.scale.elements()
+        if ns != 1 and ns != n:
+            raise Error(f"int8_linear: {ns} weight scales for {n} outputs")
+        bias = _floats(self.bias, "the bias", n) if self.bias is not None else None
+        args = (x.ptr(), x.dtype.kernel_code(), m, k, self.weight.ptr(), n, self.scale.ptr(),
+                ns, bias, out.ptr(), out.dtype.kernel_code(), self.group or 0,)
+        dev = _dev(x)
+        dev.check(dev.api.int8_linear(dev.ctx, *args))
+
+
+@dataclass
+class Mod:
+    """How a block's tokens are modulated: the row table and the scale/shift tables (ops.rs:239-245)."""
+
+    rows: Tensor   # int32 [M]
+    scale: Tensor  # float32 [R, C]
+    shift: Tensor  # float32 [R, C]
+
+
+def rms_norm_mod(x: Tensor, weight: Tensor, eps: float, m: Mod | None, out: Tensor) -> None:
+    """Row-wise RMS norm of x [M, C], then * (1 + scale[row]) + shift[row] when m is given; out may be x (ops.rs:249-278)."""
+    c = weight.elements()
+    rows = x.elements() // c
+    if x.elements() != rows * c or out.elements() != x.elements():
+        raise Error(f"rms_norm: x {x.shape}, out {out.shape}, {c} features")
+    if m is None:
+        r = sc = sh = None
+    else:
+        r, sc, sh = _row_table(m.rows, rows), _floats(m.scale, "scale", c), _floats(m.shift, "shift", c)
+    args = (x.ptr(), x.dtype.kernel_code(), rows, c, _floats(weight, "the norm weight", c),
+            eps, r, sc, sh, out.ptr(), out.dtype.kernel_code(),)
+    dev = _dev(x)
+    dev.check(dev.api.rms_norm_mod(dev.ctx, *args))
+
+
+def layer_norm(x: Tensor, c: int, weight: Tensor | None, bias: Tensor | None, eps: float, out: Tensor) -> None:
+    """Layer norm of x [M, C] per row, optional weight and bias (ops.rs:281-294)."""
+    rows = x.elements() // max(c, 1)
+    if x.elements() != rows * c or out.elements() != x.elements():
+        raise Error(f"layer_norm: x {x.shape}, out {out.shape}, {c} features")
+    w = _floats(weight, "the norm weight", c) if weight is not None else None
+    b = _floats(bias, "the norm bias", c) if bias is not None else None
+    args = (x.ptr(), x.dtype.kernel_code(), rows, c, w, b, eps, out.ptr(), out.dtype.kernel_code(),)
+    dev = _dev(x)
+    dev.check(dev.api.layer_norm(dev.ctx, *args))
+
+
+@dataclass
+class Rows:
+    """Token rows of heads x dim features inside a wider buffer: row s at element offset + s * stride (ops.rs:298-326)."""
+
+    t: Tensor
+    offset: int
+    stride: int
+    tokens: int
+    heads: int
+    dim: int
+
+    def layout(self):
+        return (self.tokens, self.heads, self.dim, self.stride)
+
+    def ptr(self) -> int:
+        last = self.offset + (max(self.tokens, 1) - 1) * self.stride + self.heads * self.dim
+        if self.stride < self.heads * self.dim or last > self.t.elements():
+            raise Error(f"rows of {self.heads} x {self.dim} at offset {self.offset} with stride {self.stride} do not fit {self.t.shape}")
+        return self.t.ptr() + self.offset * self.t.dtype.size()
+
+
+def rms_rope(x: Rows, weight: Tensor, eps: float, cs: Tensor, rot_dim: int) -> None:
+    """Per-head RMS norm and the rotary rotation, in place; cs float32 [tokens, rot_dim/2, 2] (ops.rs:327-346)."""
+    args = (x.ptr(), x.t.dtype.kernel_code(), x.tokens, x.heads, x.dim, x.stride,
+            _floats(weight, "the norm weight", x.dim), eps,
+            _floats(cs, "the rotation table", x.tokens * rot_dim), rot_dim,)
+    dev = _dev(x.t)
+    dev.check(dev.api.rms_rope(dev.ctx, *args))
+
+
+def swiglu(x: Tensor, out: Tensor) -> None:
+    """out[r, i] = silu(x[r, i]) * x[r, C + i]: x [M, 2C], out [M, C] (ops.rs:349-360)."""
+    if not out.shape:
+        raise Error("swiglu: out has no shape")
+    c = out.shape[-1]
+    if x.elements() != out.elements() * 2 or c == 0:
+        raise Error(f"swiglu: x {x.shape} is not twice out {out.shape}")
+    args = (x.ptr(), x.dtype.kernel_code(), out.elements() // c, c, out.ptr(), out.dtype.kernel_code(),)
+    dev = _dev(x)
+    dev.check(dev.api.swiglu(dev.ctx, *args))
+
+
+def gate_add(x: Tensor, other: Tensor, rows: Tensor, gate: Tensor) -> None:
+    """x[r] += other[r] * gate[rows[r]], in place (ops.rs:363-385)."""
+    c = x.shape[-1]
+    m = x.elements() // max(c, 1)
+    if other.elements() != x.elements():
+        raise Error(f"gate_add: x {x.shape} and other {other.shape} differ")
+    args = (x.ptr(), x.dtype.kernel_code(), m, c, other.ptr(), other.dtype.kernel_code(),
+            _row_table(rows, m), _floats(gate, "the gate", c),)
+    dev = _dev(x)
+    dev.check(dev.api.gate_add(dev.ctx, *args))
+
+
+def add(x: Tensor, other: Tensor) -> None:
+    """x += other, in place (ops.rs:388-400)."""
+    c = x.shape[-1]
+    if other.elements() != x.elements():
+        raise Error(f"add: x {x.shape} and other {other.shape} differ")
+    args = (x.ptr(), x.dtype.kernel_code(), x.elements() // max(c, 1), c, other.ptr(),
+            other.dtype.kernel_code(), None, None,)
+    dev = _dev(x)
+    dev.check(dev.api.gate_add(dev.ctx, *args))
+
+
+# ---- fused entry points of include/h3hip.h ------------------------------------------------------------------------
+
+@dataclass
+class Tables:
+    """Modulation tables [R, C] (float32 or bfloat16) and an optional row table (None: every token uses row 0)."""
+
+    scale: Tensor | None = None
+    shift: Tensor | None = None
+    gate: Tensor | None = None
+    rows: Tensor | None = None
+
+    def dtype(self) -> int:
+        ts = [t for t in (self.scale, self.shift, self.gate) if t is not None]
+        if not ts:
+            return _api.F32
+        d = ts[0].dtype
+        if any(t.dtype != d for t in ts) or d not in (DType.F32, DType.BF16):
+            raise Error("tables: scale, shift and gate share one type, float32 or bfloat16")
+        return d.kernel_code()
+
+    def check(self, m: int, c: int) -> None:
+        for t in (self.scale, self.shift, self.gate):
+            if t is not None and (t.elements() < c or t.elements() % c):
+                raise Error(f"a table of {t.shape} for {c} features")
+        if self.rows is not None:
+            _row_table(self.rows, m)
+
+
+def _p(t: Tensor | None):
+    return t.ptr() if t is not None else None
+
+
+def norm_quant(x: Tensor, weight: Tensor | None, eps: float, tables: Tables | None, q: Tensor, s: Tensor,
+               rot: int = _api.ROT_NONE, group: int = 0, h_dtype: DType = DType.BF16) -> None:
+    """rms_norm_mod into a virtual h (h_dtype), then the int8 quantizer (optionally rotated): q int8 [M, C], s f32 [M]."""
+    c = x.shape[-1]
+    m = x.elements() // c
+    tb = tables or Tables()
+    tb.check(m, c)
+    if q.dtype != DType.I8 or q.elements() != m * c or s.dtype != DType.F32 or s.elements() != m:
+        raise Error(f"norm_quant: q {q.dtype} {q.shape} / s {s.dtype} {s.shape} for x {x.shape}")
+    w = _floats(weight, "the norm weight", c) if weight is not None else None
+    args = (x.ptr(), x.dtype.kernel_code(), m, c, w, eps, _p(tb.rows), _p(tb.scale), _p(tb.shift),
+            tb.dtype(), h_dtype.kernel_code(), rot, group, q.ptr(), s.ptr(),)
+    dev = _dev(x)
+    dev.check(dev.api.norm_quant(dev.ctx, *args))
+
+
+def norm_mod_act_gate(x: Tensor, norm: int, weight: Tensor | None, bias: Tensor | None, eps: float, tables: Tables | None,
+                      act: int, res: Tensor | None, out: Tensor) -> None:
+    """out = res + gate * act(norm(x) * (1 + scale) + shift), one pass."""
+    c = x.shape[-1]
+    m = x.elements() // c
+    tb = tables or Tables()
+    tb.check(m, c)
+    if out.elements() != x.elements() or (res is not None and res.elements() != x.elements()):
+        raise Error(f"norm_mod_act_gate: x {x.shape}, res {None if res is None else res.shape}, out {out.shape}")
+    w = _floats(weight, "the norm weight", c) if weight is not None else None
+    b = _floats(bias, "the norm bias", c) if bias is not None else None
+    args = (x.ptr(), x.dtype.kernel_code(), m, c, norm, w, b, eps, _p(tb.rows), _p(tb.scale),
+            _p(tb.shift), _p(tb.gate), tb.dtype(), act, _p(res),
+            res.dtype.kernel_code() if res is not None else _api.BF16, out.ptr(),
+            out.dtype.kernel_code(),)
+    dev = _dev(x)
+    dev.check(dev.api.norm_mod_act_gate(dev.ctx, *args))
+
+
+def qk_rms_rope(q: Rows, k: Rows, wq: Tensor, wk: Tensor, eps: float, cs: Tensor, rot_dim: int) -> None:
+    """rms_rope of q and of k in one launch (they share the layout and the rotation table)."""
+    if q.layout() != k.layout() or q.t.dtype != k.t.dtype:
+        raise Error("qk_rms_rope: q and k must have the same layout and type")
+    dev = _dev(q.t)
+    cs_p = _floats(cs, "the rotation table", q.tokens * rot_dim) if rot_dim else (cs.ptr() if cs is not None else None)
+    dev.check(dev.api.qk_rms_rope(dev.ctx, q.ptr(), k.ptr(), q.t.dtype.kernel_code(), q.tokens, q.heads, q.dim, q.stride,
+                                  _floats(wq, "the q norm weight", q.dim), _floats(wk, "the k norm weight", q.dim), eps,
+                                  cs_p, rot_dim))
+
+
+def int8_gemm_dequant(q: Tensor, s: Tensor, layer: Int8Linear, act: int, out: Tensor) -> None:
+    """out = act(dequant(q . W^T) + bias) from already quantized activations q int8 [M, K], s f32 [M]."""
+    n, k = layer.outputs(), layer.inputs()
+    m = q.elements() // k
+    if q.dtype != DType.I8 or q.elements() != m * k or s.elements() != m or out.elements() != m * n:
+        raise Error(f"int8_gemm_dequant: q {q.shape}, s {s.shape}, out {out.shape} for a [{n}, {k}] weight")
+    ns = layer.scale.elements()
+    bias = _floats(layer.bias, "the bias", n) if layer.bias is not None else None
+    args = (q.ptr(), _floats(s, "the row scales", m), m, k, layer.weight.ptr(), n,
+            layer.scale.ptr(), ns, bias, act, out.ptr(), out.dtype.kernel_code(),)
+    dev = _dev(q)
+    dev.check(dev.api.int8_gemm_dequant(dev.ctx, *args))

@@ -1,0 +1,313 @@
+"""GPU parity: every kernel of libh3hip.so, called through the C ABI (the Python mirror of engine/h3-core/src/ops.rs),
+against the CPU oracle on the same seeded inputs. Bit-exact where the arithmetic is +, -, *, /, sqrt and fma;
+BASELINE's tolerance (1 bf16 ulp on few elements, relative L2 < 1e-3) where it goes through exp or tanh."""
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from helpers import assert_bits_equal, assert_close_16, codes_close, new, up
+
+pytestmark = pytest.mark.gpu
+
+from sycl_minimax_h3_amd import DType, Error, ops  # noqa: E402
+
+DTS = {o.F32: DType.F32, o.F16: DType.F16, o.BF16: DType.BF16}
+
+
+def inputs(seed, n, dt, scale=1.0):
+    return o.to_dt(np.random.default_rng(seed).standard_normal(n).astype(np.float32) * scale, dt)
+
+
+def weight(seed, n):
+    return (1.0 + 0.1 * np.random.default_rng(seed).standard_normal(n)).astype(np.float32)
+
+
+# ---- context and memory (kernels/h3sycl.h:22-70) ----
+def test_context_and_memory(dev):
+    assert dev.mem_cap() > 0
+    used = dev.mem_used()
+    a = np.arange(1 << 20, dtype=np.uint8)
+    t = up(dev, a, "U8", [a.size])
+    assert dev.mem_used() == used + a.size
+    assert np.array_equal(t.to_numpy(), a)
+    t2 = new(dev, "U8", [a.size])
+    dev.check(dev.api.copy(dev.ctx, t2.ptr(), t.ptr(), a.size))
+    dev.wait()
+    assert np.array_equal(t2.to_numpy(), a)
+    # pinned upload beside the kernels
+    p = dev.api.alloc_host(dev.ctx, a.size)
+    assert p
+    import ctypes
+
+    ctypes.memmove(p, a.ctypes.data, a.size)
+    t3 = new(dev, "U8", [a.size])
+    dev.check(dev.api.upload(dev.ctx, t3.ptr(), p, a.size))
+    dev.check(dev.api.upload_wait(dev.ctx))
+    assert np.array_equal(t3.to_numpy(), a)
+    # a pageable source is refused (kernels/h3sycl.h:65-67)
+    assert dev.api.upload(dev.ctx, t3.ptr(), a.ctypes.data, a.size) == -1
+    dev.api.free_host(dev.ctx, p)
+    # the cap refuses, with a message, instead of asking the driver
+    assert not dev.api.alloc(dev.ctx, dev.mem_cap() + 1)
+    assert "cap" in dev.api.error()
+    assert dev.api.gpu_count() >= 1
+    name = dev.name()
+    assert name
+
+
+# ---- h3s_rms_norm_mod (kernels/h3sycl.cpp:766-810) ----
+@pytest.mark.parametrize("x_dt,out_dt", [(o.BF16, o.BF16), (o.BF16, o.F32), (o.F16, o.F16), (o.F32, o.F32), (o.F32, o.BF16)])
+@pytest.mark.parametrize("M,C", [(7, 4096), (33, 5376), (5, 64), (9, 520)])
+@pytest.mark.parametrize("mod", [False, True])
+def test_rms_norm_mod(dev, x_dt, out_dt, M, C, mod):
+    if C % (16 // (4 if x_dt == o.F32 else 2)):
+        pytest.skip("not whole vectors")
+    x = inputs(1, M * C, x_dt, 2.0)
+    w = weight(2, C)
+    R = 3
+    rows = (np.arange(M) % R).astype(np.int32) if mod else None
+    sc = (0.5 * np.random.default_rng(3).standard_normal((R, C))).astype(np.float32) if mod else None
+    sh = (0.5 * np.random.default_rng(4).standard_normal((R, C))).astype(np.float32) if mod else None
+    want = o.rms_norm_mod(x, x_dt, M, C, w, 1e-6, rows, sc, sh, out_dt)
+    xt = up(dev, x, DTS[x_dt], [M, C])
+    out = new(dev, DTS[out_dt], [M, C])
+    m = ops.Mod(up(dev, rows, "I32", [M]), up(dev, sc, "F32", [R, C]), up(dev, sh, "F32", [R, C])) if mod else None
+    ops.rms_norm_mod(xt, up(dev, w, "F32", [C]), 1e-6, m, out)
+    assert_bits_equal(out.to_numpy(), want, "rms_norm_mod")
+
+
+def test_rms_norm_in_place(dev):
+    M, C = 17, 4096
+    x = inputs(5, M * C, o.BF16)
+    w = weight(6, C)
+    want = o.rms_norm_mod(x, o.BF16, M, C, w, 1e-5)
+    xt = up(dev, x, "BF16", [M, C])
+    ops.rms_norm_mod(xt, up(dev, w, "F32", [C]), 1e-5, None, xt)
+    assert_bits_equal(xt.to_numpy(), want, "rms_norm_mod in place")
+
+
+# ---- h3s_layer_norm (kernels/h3sycl.cpp:1248-1274) ----
+@pytest.mark.parametrize("affine", [False, True])
+@pytest.mark.parametrize("x_dt,out_dt,C", [(o.BF16, o.F32, 4096), (o.BF16, o.BF16, 1024), (o.F32, o.F32, 260)])
+def test_layer_norm(dev, affine, x_dt, out_dt, C):
+    M = 11
+    x = o.to_dt(np.random.default_rng(7).standard_normal(M * C).astype(np.float32) * 3 + 1, x_dt)
+    w = weight(8, C) if affine else None
+    b = (0.1 * np.random.default_rng(9).standard_normal(C)).astype(np.float32) if affine else None
+    want = o.layer_norm(x, x_dt, M, C, w, b, 1e-5, out_dt)
+    out = new(dev, DTS[out_dt], [M, C])
+    ops.layer_norm(up(dev, x, DTS[x_dt], [M, C]), C, up(dev, w, "F32", [C]) if affine else None,
+                   up(dev, b, "F32", [C]) if affine else None, 1e-5, out)
+    assert_bits_equal(out.to_numpy(), want, "layer_norm")
+
+
+# ---- h3s_gate_add, h3s_swiglu (kernels/h3sycl.cpp:1378-1431) ----
+@pytest.mark.parametrize("x_dt,o_dt", [(o.BF16, o.BF16), (o.BF16, o.F32), (o.F32, o.BF16)])
+@pytest.mark.parametrize("gated", [False, True])
+def test_gate_add(dev, x_dt, o_dt, gated):
+    M, C, R = 19, 1536, 4
+    x = inputs(10, M * C, x_dt)
+    other = inputs(11, M * C, o_dt)
+    rows = (np.arange(M) % R).astype(np.int32)
+    gate = (0.5 * np.random.default_rng(12).standard_normal((R, C))).astype(np.float32)
+    want = o.gate_add(x, x_dt, M, C, other, o_dt, rows if gated else None, gate if gated else None)
+    xt = up(dev, x, DTS[x_dt], [M, C])
+    if gated:
+        ops.gate_add(xt, up(dev, other, DTS[o_dt], [M, C]), up(dev, rows, "I32", [M]), up(dev, gate, "F32", [R, C]))
+    else:
+        ops.add(xt, up(dev, other, DTS[o_dt], [M, C]))
+    assert_bits_equal(xt.to_numpy(), want, "gate_add")
+
+
+@pytest.mark.parametrize("x_dt,out_dt", [(o.BF16, o.BF16), (o.F16, o.F16), (o.F32, o.F32)])
+def test_swiglu(dev, x_dt, out_dt):
+    M, C = 23, 2048
+    x = inputs(13, M * 2 * C, x_dt, 3.0)
+    want = o.swiglu(x, x_dt, M, C, out_dt)
+    out = new(dev, DTS[out_dt], [M, C])
+    ops.swiglu(up(dev, x, DTS[x_dt], [M, 2 * C]), out)
+    got = out.to_numpy()
+    if out_dt == o.F32:
+        rel, _ = o.compare(got.ravel(), want)
+        assert rel < 1e-6
+        assert np.allclose(got.ravel(), want, rtol=2e-6, atol=1e-7)
+    else:
+        assert_close_16(got, want, out_dt, "swiglu", max_frac=2e-2)
+
+
+# ---- h3s_rms_rope / h3s_qk_rms_rope (kernels/h3sycl.cpp:1276-1376) ----
+def cs_table(seed, M, rot):
+    ang = np.random.default_rng(seed).uniform(-50, 50, (M, rot // 2))
+    return np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32).ravel()
+
+
+@pytest.mark.parametrize("x_dt", [o.BF16, o.F16, o.F32])
+@pytest.mark.parametrize("H,D,rot,pad", [(32, 128, 128, 0), (4, 64, 48, 0), (3, 128, 0, 64), (5, 128, 96, 8), (2, 64, 64, 0)])
+def test_rms_rope(dev, x_dt, H, D, rot, pad):
+    M = 13
+    stride = H * D + pad
+    x = inputs(14, M * stride, x_dt)
+    w = weight(15, D)
+    cs = cs_table(16, M, rot) if rot else np.zeros(4, dtype=np.float32)
+    want = o.rms_rope(x, x_dt, M, H, D, stride, w, 1e-5, cs if rot else None, rot)
+    xt = up(dev, x, DTS[x_dt], [M * stride])
+    ops.rms_rope(ops.Rows(xt, 0, stride, M, H, D), up(dev, w, "F32", [D]), 1e-5, up(dev, cs, "F32", [cs.size]), rot)
+    assert_bits_equal(xt.to_numpy(), want, "rms_rope")
+
+
+def test_qk_rms_rope_in_a_qkv_buffer(dev):
+    """q and k inside the qkv linear's output, stride 3 H D (engine/h3-core/src/dit.rs:345-348)."""
+    M, H, D, rot = 37, 32, 128, 128
+    w_ = H * D
+    qkv = inputs(17, M * 3 * w_, o.BF16)
+    wq, wk = weight(18, D), weight(19, D)
+    cs = cs_table(20, M, rot)
+    want = o.rms_rope(qkv, o.BF16, M, H, D, 3 * w_, wq, 1e-5, cs, rot)
+    want = o.rms_rope(want[w_:], o.BF16, M, H, D, 3 * w_, wk, 1e-5, cs, rot)
+    t = up(dev, qkv, "BF16", [M, 3 * w_])
+    ops.qk_rms_rope(ops.Rows(t, 0, 3 * w_, M, H, D), ops.Rows(t, w_, 3 * w_, M, H, D), up(dev, wq, "F32", [D]),
+                    up(dev, wk, "F32", [D]), 1e-5, up(dev, cs, "F32", [cs.size]), rot)
+    got = t.to_numpy().ravel()
+    assert_bits_equal(got[w_:], want, "qk_rms_rope")
+    # q as rms_rope leaves it, v untouched
+    q_only = o.rms_rope(qkv, o.BF16, M, H, D, 3 * w_, wq, 1e-5, cs, rot)
+    g3 = got.reshape(M, 3, w_)
+    assert_bits_equal(g3[:, 0], q_only.reshape(M, 3, w_)[:, 0], "q")
+    assert_bits_equal(g3[:, 2], qkv.reshape(M, 3, w_)[:, 2], "v")
+
+
+# ---- h3s_norm_quant: rms_norm_mod -> bf16 h -> quantizer (configs 1, 4, 5a) ----
+@pytest.mark.parametrize("rot,group", [(o.ROT_NONE, 0), (o.ROT_SYLVESTER, 128), (o.ROT_SYLVESTER, 16), (o.ROT_SYLVESTER, 512),
+                                       (o.ROT_REGULAR, 256), (o.ROT_REGULAR, 64), (o.ROT_REGULAR, 16), (o.ROT_REGULAR, 4)])
+@pytest.mark.parametrize("x_dt,C", [(o.BF16, 4096), (o.BF16, 5376), (o.F32, 1024)])
+def test_norm_quant(dev, rot, group, x_dt, C):
+    if group and C % group:
+        pytest.skip("group does not divide C")
+    if rot == o.ROT_SYLVESTER and group > 64 * (16 // (4 if x_dt == o.F32 else 2)):
+        pytest.skip("group longer than a wave's vectors")
+    M = 21
+    x = o.to_dt(np.random.default_rng(21).standard_normal((M, C)).astype(np.float32)
+                * np.where(np.random.default_rng(22).random(C) < 0.01, 20.0, 1.0).astype(np.float32), x_dt).ravel()
+    w = weight(23, C)
+    want_q, want_s = o.norm_quant(x, x_dt, M, C, w, 1e-6, rot=rot, group=group, h_dt=o.BF16)
+    q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+    ops.norm_quant(up(dev, x, DTS[x_dt], [M, C]), up(dev, w, "F32", [C]), 1e-6, None, q, s, rot=rot, group=group,
+                   h_dtype=DType.BF16)
+    assert_bits_equal(s.to_numpy(), want_s, "scales")
+    codes_close(q.to_numpy(), want_q, "codes")
+
+
+@pytest.mark.parametrize("tab_dt", [o.F32, o.BF16])
+@pytest.mark.parametrize("with_rows", [False, True])
+@pytest.mark.parametrize("h_dt", [o.BF16, o.F32, o.F16])
+def test_norm_quant_modulated(dev, tab_dt, with_rows, h_dt):
+    M, C, R = 29, 4096, 3
+    x = inputs(24, M * C, o.BF16)
+    w = weight(25, C)
+    rows = (np.arange(M) % R).astype(np.int32) if with_rows else None
+    nt = R if with_rows else 1
+    sc = o.to_dt(0.5 * np.random.default_rng(26).standard_normal(nt * C).astype(np.float32), tab_dt)
+    sh = o.to_dt(0.5 * np.random.default_rng(27).standard_normal(nt * C).astype(np.float32), tab_dt)
+    want_q, want_s = o.norm_quant(x, o.BF16, M, C, w, 1e-6, rows, sc, sh, tab_dt, h_dt)
+    q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+    tb = ops.Tables(scale=up(dev, sc, DTS[tab_dt], [nt, C]), shift=up(dev, sh, DTS[tab_dt], [nt, C]),
+                    rows=up(dev, rows, "I32", [M]) if with_rows else None)
+    ops.norm_quant(up(dev, x, "BF16", [M, C]), up(dev, w, "F32", [C]), 1e-6, tb, q, s, h_dtype=DTS[h_dt])
+    assert_bits_equal(s.to_numpy(), want_s, "scales")
+    codes_close(q.to_numpy(), want_q, "codes")
+
+
+def test_norm_quant_edge_rows(dev):
+    """A zero row (scale 1e-30, codes 0), a constant row, huge and tiny rows, and a row count not a multiple of 4."""
+    M, C = 6, 4096
+    x = np.random.default_rng(28).standard_normal((M, C)).astype(np.float32)
+    x[0] = 0.0
+    x[1] = 3.0
+    x[2] *= 1e30
+    x[3] *= 1e-30
+    xb = o.to_bf16(x).ravel()
+    w = weight(29, C)
+    want_q, want_s = o.norm_quant(xb, o.BF16, M, C, w, 1e-6, h_dt=o.BF16)
+    q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+    ops.norm_quant(up(dev, xb, "BF16", [M, C]), up(dev, w, "F32", [C]), 1e-6, None, q, s)
+    assert_bits_equal(s.to_numpy(), want_s, "scales")
+    codes_close(q.to_numpy(), want_q, "codes")
+    assert s.to_numpy()[0] == np.float32(1e-30) and not q.to_numpy()[0].any()
+
+
+# ---- h3s_norm_mod_act_gate (config 2's chain) ----
+@pytest.mark.parametrize("norm", [o.NORM_LAYER, o.NORM_RMS])
+@pytest.mark.parametrize("act", [o.ACT_GELU_TANH, o.ACT_SILU, o.ACT_NONE])
+@pytest.mark.parametrize("tab_dt", [o.BF16, o.F32])
+def test_norm_mod_act_gate(dev, norm, act, tab_dt):
+    M, C = 40, 4096
+    x = inputs(30, M * C, o.BF16)
+    res = inputs(31, M * C, o.BF16)
+    tabs = [o.to_dt(0.5 * np.random.default_rng(32 + i).standard_normal(C).astype(np.float32), tab_dt) for i in range(3)]
+    w = weight(35, C) if norm == o.NORM_RMS else None
+    want = o.norm_mod_act_gate(x, o.BF16, M, C, norm, w, None, 1e-5, None, tabs[0], tabs[1], tabs[2], tab_dt, act, res,
+                               o.BF16, o.BF16)
+    out = new(dev, "BF16", [M, C])
+    tb = ops.Tables(scale=up(dev, tabs[0], DTS[tab_dt], [1, C]), shift=up(dev, tabs[1], DTS[tab_dt], [1, C]),
+                    gate=up(dev, tabs[2], DTS[tab_dt], [1, C]))
+    ops.norm_mod_act_gate(up(dev, x, "BF16", [M, C]), norm, up(dev, w, "F32", [C]) if w is not None else None, None, 1e-5, tb,
+                          act, up(dev, res, "BF16", [M, C]), out)
+    if act == o.ACT_NONE:
+        assert_bits_equal(out.to_numpy(), want, "norm_mod_act_gate")
+    else:
+        assert_close_16(out.to_numpy(), want, o.BF16, "norm_mod_act_gate", max_frac=5e-3)
+
+
+# ---- h3s_int8_linear and h3s_int8_gemm_dequant (kernels/h3sycl.cpp:404-652) ----
+@pytest.mark.parametrize("M,K,N", [(1, 64, 5), (300, 256, 300), (257, 4096, 129), (64, 1024, 512)])
+@pytest.mark.parametrize("group", [0, 4, 16, 64, 256])
+@pytest.mark.parametrize("per_n,bias,out_dt", [(False, False, o.BF16), (True, True, o.BF16), (True, False, o.F32)])
+def test_int8_linear(dev, M, K, N, group, per_n, bias, out_dt):
+    if group and K % group:
+        pytest.skip("group does not divide K")
+    rng = np.random.default_rng(M * 7 + K + N + group)
+    x = o.to_bf16((0.7 * rng.standard_normal(M * K)).astype(np.float32))
+    w = rng.integers(-127, 128, N * K, dtype=np.int8)
+    ws = rng.uniform(0.005, 0.02, N if per_n else 1).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    want = o.int8_linear(x, o.BF16, M, K, w, N, ws, b, out_dt, group)
+    layer = ops.Int8Linear(up(dev, w, "I8", [N, K]), up(dev, ws, "F32", [ws.size]), up(dev, b, "F32", [N]) if bias else None,
+                           group or None)
+    out = new(dev, DTS[out_dt], [M, N])
+    layer.forward(up(dev, x, "BF16", [M, K]), out)
+    assert_bits_equal(out.to_numpy(), want, "int8_linear")
+
+
+@pytest.mark.parametrize("act", [o.ACT_NONE, o.ACT_SILU])
+def test_int8_gemm_dequant(dev, act):
+    M, K, N = 515, 4096, 770
+    rng = np.random.default_rng(40)
+    q = rng.integers(-128, 128, M * K, dtype=np.int8)
+    s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    w = rng.integers(-127, 128, N * K, dtype=np.int8)
+    ws = rng.uniform(0.005, 0.02, N).astype(np.float32)
+    want = o.gemm_dequant(q, s, M, K, w, N, ws, None, act, o.BF16)
+    layer = ops.Int8Linear(up(dev, w, "I8", [N, K]), up(dev, ws, "F32", [N]))
+    out = new(dev, "BF16", [M, N])
+    ops.int8_gemm_dequant(up(dev, q, "I8", [M, K]), up(dev, s, "F32", [M]), layer, act, out)
+    if act == o.ACT_NONE:
+        assert_bits_equal(out.to_numpy(), want, "gemm")
+    else:
+        assert_close_16(out.to_numpy(), want, o.BF16, "gemm silu", max_frac=5e-3)
+
+
+# ---- errors through the ABI on the device ----
+def test_errors_are_reported(dev):
+    M, C = 4, 4096
+    xt = new(dev, "BF16", [M, C])
+    q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+    with pytest.raises(Error, match="aligned"):
+        dev.check(dev.api.norm_quant(dev.ctx, xt.ptr() + 2, 2, M, C - 8, None, 1e-6, None, None, None, 0, 2, 0, 0, q.ptr(), s.ptr()))
+    with pytest.raises(Error, match="group"):
+        dev.check(dev.api.int8_linear(dev.ctx, xt.ptr(), 2, M, C, q.ptr(), 8, s.ptr(), 1, None, xt.ptr(), 2, 128))
+    with pytest.raises(Error, match="rot_dim"):
+        dev.check(dev.api.rms_rope(dev.ctx, xt.ptr(), 2, M, 32, 128, 4096, s.ptr(), 1e-5, s.ptr(), 127))
+    with pytest.raises(Error, match="not implemented"):
+        dev.check(dev.api.attention(dev.ctx, xt.ptr(), xt.ptr(), xt.ptr(), 2, M, 32, 128, 4096, xt.ptr(), 2))
+    assert dev.api.rms_norm_mod(dev.ctx, xt.ptr(), 2, 0, C, s.ptr(), 1e-6, None, None, None, xt.ptr(), 2) == 0
+    dev.wait()

@@ -1,0 +1,293 @@
+"""Pins the CPU oracle (oracle/h3oracle.c) against the reference's own known answers and against what the mathematics
+fixes: closed forms, brute force, invariants. CPU only."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+
+
+def f32_bits(u):
+    return np.frombuffer(np.uint32(u).tobytes(), dtype=np.float32)[0]
+
+
+# ---- element types: engine/h3-core/src/dtype.rs:137-155 ----
+def test_bf16_round_trip_and_ties(oracle):
+    L = oracle.lib()
+    for v in [0.0, 1.0, -1.0, 0.5, 3.140625, -1234.0, 1e-20]:
+        r = L.h3o_bf16_to_f32(L.h3o_f32_to_bf16(v))
+        assert abs(r - v) <= abs(v) * 0.004
+    # ties go to even (dtype.rs:144-145)
+    assert L.h3o_f32_to_bf16(f32_bits(0x3F808000)) == 0x3F80
+    assert L.h3o_f32_to_bf16(f32_bits(0x3F818000)) == 0x3F82
+    # inf truncated, not rounded (dtype.rs:61-63)
+    assert L.h3o_f32_to_bf16(float("inf")) == 0x7F80
+    # the numpy restatement in oracle.py agrees with the C one on every pattern class
+    x = np.random.default_rng(0).standard_normal(100000).astype(np.float32) * 1000
+    ref = np.array([L.h3o_f32_to_bf16(float(v)) for v in x[:2000]], dtype=np.uint16)
+    assert np.array_equal(o.to_bf16(x[:2000]), ref)
+
+
+def test_f16_values(oracle):
+    L = oracle.lib()
+    assert L.h3o_f16_to_f32(0x3C00) == 1.0
+    assert L.h3o_f16_to_f32(0xC000) == -2.0
+    assert L.h3o_f16_to_f32(0x0001) == pytest.approx(5.9604645e-08, rel=1e-7)
+    assert L.h3o_f16_to_f32(0x7C00) == float("inf")
+    assert L.h3o_f16_to_f32(0) == 0.0
+    # f32 -> f16 agrees with numpy's IEEE conversion (round to nearest even) on random and subnormal values
+    x = np.concatenate([np.random.default_rng(1).standard_normal(5000) * 100, np.linspace(-1e-5, 1e-5, 999)]).astype(np.float32)
+    mine = np.array([L.h3o_f32_to_f16(float(v)) for v in x], dtype=np.uint16)
+    assert np.array_equal(mine, x.astype(np.float16).view(np.uint16))
+
+
+# ---- seeded inputs: engine/h3-core/src/rng.rs ----
+def test_rng_published_vectors(oracle):
+    # xoshiro256** from state {1, 2, 3, 4}: the published first outputs of the algorithm
+    r = oracle.Rng(state=[1, 2, 3, 4])
+    assert [r.next_u64() for _ in range(4)] == [11520, 0, 1509978240, 1215971899390074240]
+    # splitmix64 seeded with 0: its published first output is the first state word
+    assert oracle.Rng(0).state[0] == 0xE220A8397B1DCDAF
+
+
+def test_rng_uniform_and_normal_moments(oracle):
+    r = oracle.Rng(3)
+    u = np.array([r.uniform() for _ in range(20000)])
+    assert 0.0 <= u.min() and u.max() < 1.0 and abs(u.mean() - 0.5) < 0.01
+    z = oracle.normal(5, 200000)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1.0) < 0.01
+    # Box-Muller from two uniforms, restated in float64: the draws agree to float32 rounding
+    r1, r2 = oracle.Rng(11), oracle.Rng(11)
+    for _ in range(100):
+        a, b = r2.uniform(), r2.uniform()
+        want = math.sqrt(-2.0 * math.log(max(a, 1e-7))) * math.cos(2 * math.pi * b)
+        assert abs(r1.normal() - want) < 1e-5 * max(1.0, abs(want))
+
+
+# ---- rotations: engine/h3-core/src/reference.rs:4-23, 101-112; kernels/h3sycl.cpp:184-213, 433-459 ----
+@pytest.mark.parametrize("g", [4, 16, 64, 256])
+def test_regular_hadamard_orthonormal_and_symmetric(oracle, g):
+    h = oracle.hadamard(g, oracle.ROT_REGULAR).astype(np.float64)
+    assert np.abs(h @ h.T - np.eye(g)).max() < 1e-5
+    assert np.array_equal(h, h.T)
+
+
+def test_regular_hadamard_closed_form(oracle):
+    h4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=np.float64)
+    want = np.kron(np.kron(h4, h4), h4) / 8.0
+    # the digit of lowest weight is the innermost Kronecker factor
+    assert np.allclose(oracle.hadamard(64, oracle.ROT_REGULAR), want, atol=1e-7)
+
+
+@pytest.mark.parametrize("g", [2, 8, 128, 512])
+def test_sylvester_closed_form_and_involution(oracle, g):
+    h2 = np.array([[1, 1], [1, -1]], dtype=np.float64)
+    want = np.array([[1.0]])
+    for _ in range(int(math.log2(g))):
+        want = np.kron(want, h2)
+    want /= math.sqrt(g)
+    h = oracle.hadamard(g, oracle.ROT_SYLVESTER).astype(np.float64)
+    assert np.allclose(h, want, atol=1e-7)
+    assert np.abs(h @ h - np.eye(g)).max() < 1e-5        # symmetric and orthonormal: its own inverse
+
+
+@pytest.mark.parametrize("kind,g", [(o.ROT_REGULAR, 4), (o.ROT_REGULAR, 16), (o.ROT_REGULAR, 256), (o.ROT_SYLVESTER, 2),
+                                    (o.ROT_SYLVESTER, 32), (o.ROT_SYLVESTER, 128)])
+def test_butterfly_equals_dense_product(oracle, kind, g):
+    rng = np.random.default_rng(g)
+    h = oracle.hadamard(g, kind).astype(np.float64)
+    for _ in range(20):
+        x = rng.standard_normal(g).astype(np.float32) * rng.choice([1.0, 20.0])
+        got = oracle.rotate_group(x, kind).astype(np.float64)
+        want = x.astype(np.float64) @ h
+        assert np.abs(got - want).max() <= 4e-6 * max(1.0, np.abs(x).sum() / math.sqrt(g))
+    # a transposed or sign-flipped matrix would fail this: a unit vector picks out one row of H
+    for i in [0, 1, g - 1]:
+        e = np.zeros(g, dtype=np.float32)
+        e[i] = 1.0
+        assert np.allclose(oracle.rotate_group(e, kind), h[i], atol=1e-7)
+
+
+# ---- quantizer: kernels/h3sycl.h:74-83, engine/h3-core/src/reference.rs:68-70 ----
+def test_quantizer_invariants(oracle):
+    rng = np.random.default_rng(2)
+    M, K = 64, 512
+    y = rng.standard_normal((M, K)).astype(np.float32) * rng.uniform(1e-3, 1e3, (M, 1)).astype(np.float32)
+    y[5] = 0.0
+    q, s = oracle.quantize_rows(y, M, K)
+    q = q.reshape(M, K).astype(np.int32)
+    assert s[5] == np.float32(1e-30) and not q[5].any()
+    nz = [r for r in range(M) if r != 5]
+    assert (np.abs(q[nz]).max(axis=1) == 127).all()
+    assert np.array_equal(s[nz], np.maximum(np.abs(y[nz]).max(axis=1) / np.float32(127), np.float32(1e-30)))
+    err = np.abs(y - q * s[:, None])
+    assert (err <= s[:, None] * 0.5 * (1 + 1e-5)).all()
+
+
+def test_quantizer_ties_to_even(oracle):
+    # s = 127 / 127 = 1: values k + 0.5 are exact ties
+    y = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5]], dtype=np.float32)
+    q, s = oracle.quantize_rows(y, 1, 8)
+    assert s[0] == 1.0
+    assert list(q) == [127, 0, 2, 2, 0, -2, -2, 126]
+
+
+def test_int8_linear_matches_a_plain_linear_within_quantization(oracle):
+    """engine/h3-core/src/reference.rs:114-131, on the oracle."""
+    m, k, n = 3, 64, 5
+    r = oracle.Rng(7)
+    x = np.array([r.normal() for _ in range(m * k)], dtype=np.float32)
+    w = np.array([(r.next_u64() % 255) - 127 for _ in range(n * k)], dtype=np.int8)
+    ws = np.array([0.01], dtype=np.float32)
+    got = oracle.int8_linear(x, oracle.F32, m, k, w, n, ws, out_dt=oracle.F32)
+    want = (x.reshape(m, k).astype(np.float64) @ w.reshape(n, k).T.astype(np.float64) * 0.01).astype(np.float32)
+    rel, cos = oracle.compare(got, want.ravel())
+    assert rel < 0.02 and cos > 0.999
+
+
+def test_gemm_dequant_brute_force(oracle):
+    rng = np.random.default_rng(4)
+    M, K, N = 7, 128, 9
+    q = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    s = rng.uniform(0.001, 0.1, M).astype(np.float32)
+    acc = q.astype(np.int64) @ w.astype(np.int64).T
+    bias = rng.standard_normal(N).astype(np.float32)
+    # N scales: (acc * s) * ws[n] + b, each step rounded to float32
+    ws = rng.uniform(0.005, 0.02, N).astype(np.float32)
+    want = (acc.astype(np.float32) * s[:, None]) * ws[None, :] + bias[None, :]
+    got = oracle.gemm_dequant(q.ravel(), s, M, K, w.ravel(), N, ws, bias, out_dt=oracle.F32).reshape(M, N)
+    assert np.array_equal(got, want.astype(np.float32))
+    # one scale: acc * fl(s * ws0)
+    ws1 = np.array([0.0123], dtype=np.float32)
+    want1 = acc.astype(np.float32) * (s * ws1[0])[:, None]
+    got1 = oracle.gemm_dequant(q.ravel(), s, M, K, w.ravel(), N, ws1, None, out_dt=oracle.F32).reshape(M, N)
+    assert np.array_equal(got1, want1.astype(np.float32))
+
+
+# ---- the canonical reduction ----
+def test_canon_sum_is_a_sum(oracle):
+    rng = np.random.default_rng(5)
+    for n, V, L in [(4096, 8, 64), (5376, 8, 64), (100, 4, 64), (128, 8, 8), (17, 8, 64)]:
+        x = rng.standard_normal(n).astype(np.float32)
+        exact = math.fsum(float(v) for v in x)
+        got = oracle.canon_sum(x, V, L, oracle.SUM)
+        assert abs(got - exact) <= 1e-6 * math.fsum(abs(float(v)) for v in x)
+        exact2 = math.fsum(float(v) * float(v) for v in x)
+        got2 = oracle.canon_sum(x, V, L, oracle.SUMSQ)
+        assert abs(got2 - exact2) <= 1e-6 * exact2
+    # the order is the one stated: with L = 2, V = 1, lanes hold the even and the odd positions
+    x = np.array([1e8, 1.0, -1e8, 1.0], dtype=np.float32)
+    # lane 0: 1e8 + -1e8 = 0; lane 1: 1 + 1 = 2; total 2 (a sequential sum would give 1)
+    assert oracle.canon_sum(x, 1, 2, oracle.SUM) == 2.0
+
+
+# ---- the norms: kernels/h3sycl.cpp:766-810, 1248-1274 ----
+def test_rms_norm_invariants(oracle):
+    rng = np.random.default_rng(6)
+    M, C = 16, 1024
+    x = rng.standard_normal((M, C)).astype(np.float32) * 3
+    w = np.full(C, 0.5, dtype=np.float32)
+    y = oracle.rms_norm_mod(x, oracle.F32, M, C, w, 1e-6).reshape(M, C)
+    assert np.allclose(np.sqrt((y.astype(np.float64) ** 2).mean(axis=1)), 0.5, rtol=1e-5)
+    # against a float64 restatement
+    want = x / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6) * 0.5
+    assert np.abs(y - want).max() < 1e-5
+    # the modulation: rows pick table rows
+    rows = np.array([i % 3 for i in range(M)], dtype=np.int32)
+    sc = rng.standard_normal((3, C)).astype(np.float32)
+    sh = rng.standard_normal((3, C)).astype(np.float32)
+    ym = oracle.rms_norm_mod(x, oracle.F32, M, C, w, 1e-6, rows, sc, sh).reshape(M, C)
+    assert np.allclose(ym, y * (1 + sc[rows]) + sh[rows], atol=1e-5)
+
+
+def test_layer_norm_invariants(oracle):
+    rng = np.random.default_rng(7)
+    M, C = 8, 2048
+    x = (rng.standard_normal((M, C)) * 4 + 10).astype(np.float32)
+    x[3] = 7.0
+    y = oracle.layer_norm(x, oracle.F32, M, C, None, None, 1e-5).reshape(M, C)
+    assert np.abs(y[3]).max() == 0.0                              # a constant row goes to zero
+    ok = [r for r in range(M) if r != 3]
+    assert np.abs(y[ok].mean(axis=1)).max() < 1e-5
+    assert np.abs(y[ok].var(axis=1) - 1).max() < 1e-3
+    w = rng.standard_normal(C).astype(np.float32)
+    b = rng.standard_normal(C).astype(np.float32)
+    yw = oracle.layer_norm(x, oracle.F32, M, C, w, b, 1e-5).reshape(M, C)
+    assert np.array_equal(yw, (y * w + b).astype(np.float32))
+
+
+# ---- rotary: kernels/h3sycl.cpp:1276-1376 ----
+def test_rms_rope_invariants(oracle):
+    rng = np.random.default_rng(8)
+    M, H, D, rot = 5, 3, 64, 48
+    stride = H * D + 16
+    x = rng.standard_normal(M * stride).astype(np.float32)
+    w = np.ones(D, dtype=np.float32)
+    ang = rng.uniform(-10, 10, (M, rot // 2))
+    cs = np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32).ravel()
+    y = oracle.rms_rope(x, oracle.F32, M, H, D, stride, w, 1e-5, cs, rot)
+    ident = np.stack([np.ones((M, rot // 2)), np.zeros((M, rot // 2))], -1).astype(np.float32).ravel()
+    n = oracle.rms_rope(x, oracle.F32, M, H, D, stride, w, 1e-5, ident, rot)     # zero angle: only the norm
+    n0 = oracle.rms_rope(x, oracle.F32, M, H, D, stride, w, 1e-5, None, 0)        # rot_dim 0: only the norm
+    assert np.array_equal(n, n0)
+    X, Y, N0 = (a.reshape(M, stride)[:, : H * D].reshape(M, H, D) for a in (x, y, n0))
+    assert np.array_equal(y.reshape(M, stride)[:, H * D:], x.reshape(M, stride)[:, H * D:])   # the gap is untouched
+    rms = np.sqrt((X.astype(np.float64) ** 2).mean(-1, keepdims=True) + 1e-5)
+    assert np.allclose(N0, X / rms, atol=1e-5)
+    h = rot // 2
+    # each pair keeps its length, and the angle is the table's
+    la = np.hypot(Y[..., :h], Y[..., h:rot])
+    lb = np.hypot(N0[..., :h], N0[..., h:rot])
+    assert np.allclose(la, lb, atol=1e-5)
+    a, b = N0[..., :h], N0[..., h:rot]
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    assert np.allclose(Y[..., :h], a * c - b * s, atol=1e-5)
+    assert np.allclose(Y[..., h:rot], b * c + a * s, atol=1e-5)
+    assert np.array_equal(Y[..., rot:], N0[..., rot:])              # features from rot_dim on: only normalized
+
+
+# ---- activations: kernels/h3sycl.cpp:1395; engine/h3-core/src/audio.rs:440 ----
+def test_activation_closed_forms(oracle):
+    for v in np.linspace(-12, 12, 97):
+        v = float(np.float32(v))
+        gelu = 0.5 * v * (1 + math.tanh(math.sqrt(2 / math.pi) * (v + 0.044715 * v ** 3)))
+        silu = v / (1 + math.exp(-v))
+        assert abs(oracle.act(v, oracle.ACT_GELU_TANH) - gelu) <= 2e-6 * max(1.0, abs(gelu))
+        assert abs(oracle.act(v, oracle.ACT_SILU) - silu) <= 2e-6 * max(1.0, abs(silu))
+    # GELU-tanh, not the erf form: at 1.0 they differ in the 4th digit
+    assert abs(oracle.act(1.0, oracle.ACT_GELU_TANH) - 0.8411920) < 1e-6
+
+
+def test_fused_chains_are_compositions(oracle):
+    """norm_quant = rms_norm_mod into bf16, then the quantizer; norm_mod_act_gate = norm, modulate, act, gate_add."""
+    rng = np.random.default_rng(9)
+    M, C = 12, 1024
+    x = oracle.to_bf16(rng.standard_normal((M, C)).astype(np.float32))
+    w = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    rows = np.zeros(M, dtype=np.int32)
+    sc = (0.5 * rng.standard_normal((1, C))).astype(np.float32)
+    sh = (0.5 * rng.standard_normal((1, C))).astype(np.float32)
+    h = oracle.rms_norm_mod(x, oracle.BF16, M, C, w, 1e-6, rows, sc, sh)
+    q, s = oracle.norm_quant(x, oracle.BF16, M, C, w, 1e-6, rows, sc, sh, oracle.F32, oracle.BF16)
+    q2, s2 = oracle.quantize_rows(oracle.from_bf16(h), M, C)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+    # with a rotation: quantize(rotate(h)) group by group
+    q3, s3 = oracle.norm_quant(x, oracle.BF16, M, C, w, 1e-6, rows, sc, sh, oracle.F32, oracle.BF16, oracle.ROT_SYLVESTER, 128)
+    hr = np.concatenate([oracle.rotate_group(g, oracle.ROT_SYLVESTER) for g in oracle.from_bf16(h).reshape(-1, 128)])
+    q4, s4 = oracle.quantize_rows(hr, M, C)
+    assert np.array_equal(q3, q4) and np.array_equal(s3, s4)
+    # norm_mod_act_gate with act NONE, no gate and res = 0 rows equals rms_norm_mod into float32
+    out = oracle.norm_mod_act_gate(x, oracle.BF16, M, C, oracle.NORM_RMS, w, None, 1e-6, rows, sc, sh, None, oracle.F32,
+                                   oracle.ACT_NONE, None, oracle.BF16, oracle.F32)
+    h32 = oracle.rms_norm_mod(x, oracle.BF16, M, C, w, 1e-6, rows, sc, sh, out_dt=oracle.F32)
+    assert np.array_equal(out, h32)
+    # and gate_add of the activation equals the fused residual
+    res = oracle.to_bf16(rng.standard_normal((M, C)).astype(np.float32))
+    gate = (0.5 * rng.standard_normal((1, C))).astype(np.float32)
+    y = np.array([oracle.act(float(v), oracle.ACT_GELU_TANH) for v in h32], dtype=np.float32)
+    want = oracle.gate_add(res, oracle.BF16, M, C, y, oracle.F32, rows, gate)
+    got = oracle.norm_mod_act_gate(x, oracle.BF16, M, C, oracle.NORM_RMS, w, None, 1e-6, rows, sc, sh, gate, oracle.F32,
+                                   oracle.ACT_GELU_TANH, res, oracle.BF16, oracle.BF16)
+    assert np.array_equal(got, want.ravel())
