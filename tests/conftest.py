@@ -17,6 +17,7 @@ def oracle():
     from oracle import oracle as o
 
     o.lib()
+    o.set_threads(min(8, os.cpu_count() or 1))
     return o
 
 
