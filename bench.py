@@ -63,6 +63,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of kernel keys to time (default all)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also time a plain device copy of 1 GiB (the attainable HBM rate; the known-size kernel that "
+                         "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the per-token kernels shard "
@@ -150,6 +153,14 @@ def main() -> int:
     O5 = T(out5)
     run("cfg5b_int8_gemm_silu_47104x16384", lambda: ops.int8_gemm_dequant(Q4, S4, layer, A.ACT_SILU, O5), 5)
 
+    copy = None
+    if args.copy_probe:
+        src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev_t).fill_(1.0)
+        dst = torch.empty_like(src)
+        ms_c = timed(lambda: dst.copy_(src), 20, 3)
+        copy = {"bytes": 2 * src.numel() * 2, "ms": round(ms_c, 4), "GB/s": round(2 * src.numel() * 2 / (ms_c * 1e-3) / 1e9, 1)}
+        del src, dst
+
     per = {}
     for k, ms in kernels.items():
         gbs = B[k] / (ms * 1e-3) / 1e9
@@ -180,6 +191,8 @@ def main() -> int:
         "kernels": per,
         "device": dev.name(),
     }
+    if copy:
+        line["copy_probe"] = copy
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(x2, r2, tab)
     print(json.dumps(line), flush=True)

@@ -364,15 +364,15 @@ int h3o_gate_add(void* x, int x_dt, int64_t M, int64_t C, const void* other, int
 
 /* ---- rotations ---- */
 /* regular: one base-4 digit at a time, low digit first; for the four values x0..x3 that differ only in that digit,
- * t = ((x0 + x1) + x2) + x3 and y_a = t - 2 x_(3-a) (kernels/h3sycl.cpp:408-412, 433-459); then * 1/sqrt(g), a power
- * of two. Sylvester: h = 1, 2, ..., g/2, (a, b) -> (a + b, a - b); then * fl(1/sqrt(g)). */
+ * t = (x0 + x1) + (x2 + x3) and y_a = t - 2 x_(3-a) (kernels/h3sycl.cpp:408-412, 433-459; the pairwise sum is the
+ * association of the reference's cross-lane digits, h3sycl.cpp:444-453); then * 1/sqrt(g), a power of two. Sylvester: h = 1, 2, ..., g/2, (a, b) -> (a + b, a - b); then * fl(1/sqrt(g)). */
 void h3o_rotate_group(float* y, int g, int kind) {
     if (kind == H3O_ROT_REGULAR) {
         for (int d = 1; d < g; d *= 4)
             for (int i = 0; i < g; ++i) {
                 if ((i / d) % 4 != 0) continue;
                 const float x0 = y[i], x1 = y[i + d], x2 = y[i + 2 * d], x3 = y[i + 3 * d];
-                const float t = x0 + x1 + x2 + x3;
+                const float t = (x0 + x1) + (x2 + x3);
                 y[i] = t - 2.0f * x3;
                 y[i + d] = t - 2.0f * x2;
                 y[i + 2 * d] = t - 2.0f * x1;

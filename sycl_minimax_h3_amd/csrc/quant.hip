@@ -1,0 +1,63 @@
+// quant.hip - the entry points of the row quantizer: h3s_norm_quant (rms_norm_mod -> the reference's bf16
+// scratch h -> int8_linear's quantizer, in one pass) and launch_quantize (h3s_int8_linear's quantizer). The kernel
+// is quant_impl.h, instantiated per input type in quant_bf16.hip, quant_f16.hip and quant_f32.hip.
+#include <cmath>
+
+#include "quant_impl.h"
+
+namespace h3 {
+
+template <int XDT> int quant_launch(Ctx*, const char*, QuantArgs, int, int, int, bool);
+extern template int quant_launch<H3S_BF16>(Ctx*, const char*, QuantArgs, int, int, int, bool);
+extern template int quant_launch<H3S_F16>(Ctx*, const char*, QuantArgs, int, int, int, bool);
+extern template int quant_launch<H3S_F32>(Ctx*, const char*, QuantArgs, int, int, int, bool);
+
+static int dispatch(Ctx* c, const char* fn, int x_dt, const QuantArgs& A, int rot, int hdt, int tab, bool norm) {
+    switch (x_dt) {
+        case H3S_BF16: return quant_launch<H3S_BF16>(c, fn, A, rot, hdt, tab, norm);
+        case H3S_F16: return quant_launch<H3S_F16>(c, fn, A, rot, hdt, tab, norm);
+        default: return quant_launch<H3S_F32>(c, fn, A, rot, hdt, tab, norm);
+    }
+}
+
+static bool is_pow2(int g) { return g > 0 && (g & (g - 1)) == 0; }
+
+int launch_quantize(Ctx* c, const void* x, int x_dt, int64_t M, int64_t K, int group, int8_t* q, float* s) {
+    if (K % vec_of(x_dt) != 0) return fail("h3s_int8_linear: K must be whole 16-byte vectors");
+    if (group > 0 && K % kSeg != 0) return fail("h3s_int8_linear: a rotated row must be a multiple of 64 features");
+    QuantArgs A{x, M, K, nullptr, 0.0f, nullptr, nullptr, nullptr, group, group > 0 ? (float) (1.0 / std::sqrt((double) group)) : 1.0f,
+                q, s, 0};
+    return dispatch(c, "h3s_int8_linear", x_dt, A, group > 0 ? H3S_ROT_REGULAR : H3S_ROT_NONE, H3S_F32, TAB_NONE, false);
+}
+
+}  // namespace h3
+
+using namespace h3;
+
+H3S_EXPORT int h3s_norm_quant(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, const float* weight, float eps,
+                              const int32_t* rows, const void* scale, const void* shift, int tab_dt, int h_dt, int rot,
+                              int group, int8_t* q, float* s) try {
+    if (M <= 0 || C <= 0) return 0;
+    const char* fn = "h3s_norm_quant";
+    if (!dt_ok(x_dt) || !dt_ok(h_dt) || !dt_ok(tab_dt)) return fail(std::string(fn) + ": unknown element type");
+    const int V = vec_of(x_dt);
+    if (C % V != 0) return fail(std::string(fn) + ": C must be a multiple of " + std::to_string(V) + " (whole 16-byte vectors per row)");
+    for (const void* p : {x, (const void*) weight, scale, shift, (const void*) q})
+        if (p && !aligned16(p)) return fail(std::string(fn) + ": tensors must be 16-byte aligned");
+    if (!q || !s) return fail(std::string(fn) + ": q and s are required");
+    if (rot == H3S_ROT_SYLVESTER) {
+        if (!is_pow2(group) || group < 2 || group > 512 || C % group != 0 || (group > 64 && C % 64 != 0))
+            return fail(std::string(fn) + ": a Sylvester group is a power of 2 dividing C, at most 512");
+    } else if (rot == H3S_ROT_REGULAR) {
+        if (!is_pow2(group) || (__builtin_ctz((unsigned) group) & 1) || group < 4 || group > 256 || C % group != 0)
+            return fail(std::string(fn) + ": a regular group is a power of 4 dividing C, at most 256");
+    } else if (rot != H3S_ROT_NONE) return fail(std::string(fn) + ": unknown rotation");
+    if (scale && shift && tab_dt != H3S_F32 && tab_dt != H3S_BF16) return fail(std::string(fn) + ": tables are float32 or bfloat16");
+    if (rot != H3S_ROT_NONE && C % kSeg != 0) return fail(std::string(fn) + ": a rotated row must be a multiple of 64 features");
+    Ctx* c = ctx_of(ctx, fn);
+    if (!c) return -1;
+    const int tab = !(scale && shift) ? TAB_NONE : tab_dt == H3S_BF16 ? TAB_BF16 : TAB_F32;
+    QuantArgs A{x, M, C, weight, eps, rows, scale, shift, group, rot != H3S_ROT_NONE ? (float) (1.0 / std::sqrt((double) group)) : 1.0f,
+                q, s, 0};
+    return dispatch(c, fn, x_dt, A, rot, h_dt, tab, true);
+} catch (const std::exception& e) { return fail(e.what()); }

@@ -241,152 +241,6 @@ __global__ __launch_bounds__(256) void norm_mod_act_gate_kernel(
     }
 }
 
-// ---- rotations of the values a wave holds (group of G features = G / V consecutive lanes' chunks) ----
-// Sylvester: stages h = 1, 2, ..., G/2, (a, b) -> (a + b, a - b): inside the chunk while h < V, then across lanes
-// (lane ^ h/V): the lower lane of a pair forms a + b and the upper one a - b, both as fma(+-1, own, partner), which
-// is exactly that sum or difference. Then * fl(1 / sqrt(G)).
-template <int G, int V, int OFF> __device__ __forceinline__ void sylvester_cross(float (&v)[V], int lane) {
-    if constexpr (OFF * V < G && OFF < kWave) {
-        const float sg = (lane & OFF) ? -1.0f : 1.0f;
-#pragma unroll
-        for (int e = 0; e < V; ++e) {
-            const float p = xor_lane<OFF>(v[e]);
-            v[e] = __builtin_fmaf(sg, v[e], p);
-        }
-        sylvester_cross<G, V, OFF * 2>(v, lane);
-    }
-}
-template <int G, int V> __device__ __forceinline__ void sylvester(float (&v)[V], int lane) {
-#pragma unroll
-    for (int h = 1; h < V && h < G; h *= 2)
-#pragma unroll
-        for (int e = 0; e < V; ++e)
-            if (!(e & h)) {
-                const float a = v[e], b2 = v[e + h];
-                v[e] = a + b2;
-                v[e + h] = a - b2;
-            }
-    sylvester_cross<G, V, 1>(v, lane);
-    const float c = (float) (1.0 / __builtin_sqrt((double) G));
-#pragma unroll
-    for (int e = 0; e < V; ++e) v[e] = v[e] * c;
-}
-
-// Regular (h4 per base-4 digit, kernels/h3sycl.cpp:433-459): digit strides d = 1, 4, 16, ... < G; for the four
-// values x0..x3 differing in that digit, t = ((x0 + x1) + x2) + x3 and y_a = t - 2 x_(3-a); then * 1/sqrt(G) (a
-// power of two). Values of one digit group are inside the chunk (4d <= V), split over a lane pair (V = 8, d = 4),
-// or in four lanes (d >= V), gathered from lane l ^ ((a ^ b) d / V).
-template <int V> __device__ __forceinline__ void regular_digit(float (&v)[V], int lane, int d) {
-    if (4 * d <= V) {
-#pragma unroll
-        for (int e = 0; e < V; ++e) {
-            if ((e / d) % 4 != 0) continue;
-            const float x0 = v[e], x1 = v[e + d], x2 = v[e + 2 * d], x3 = v[e + 3 * d];
-            const float t = x0 + x1 + x2 + x3;
-            v[e] = t - 2.0f * x3; v[e + d] = t - 2.0f * x2; v[e + 2 * d] = t - 2.0f * x1; v[e + 3 * d] = t - 2.0f * x0;
-        }
-    } else if (d < V) {
-        // V = 8, d = 4: lane pair (l, l ^ 1); values e0 and e0 + 4 of each
-        const bool upper = lane & 1;
-#pragma unroll
-        for (int e0 = 0; e0 < V / 2; ++e0) {
-            const float o0 = v[e0], o1 = v[e0 + V / 2];
-            const float p0 = xor_lane<1>(o0), p1 = xor_lane<1>(o1);
-            const float a = upper ? p0 : o0, b = upper ? p1 : o1, c = upper ? o0 : p0, dd = upper ? o1 : p1;
-            const float t = a + b + c + dd;
-            v[e0] = t - 2.0f * p1;
-            v[e0 + V / 2] = t - 2.0f * p0;
-        }
-    } else {
-        const int ls = d / V, a = (lane / ls) & 3;
-#pragma unroll
-        for (int e = 0; e < V; ++e) {
-            float xb[4];
-#pragma unroll
-            for (int bb = 0; bb < 4; ++bb) {
-                const int src = lane ^ ((a ^ bb) * ls);
-                xb[bb] = __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v[e])));
-            }
-            const float t = xb[0] + xb[1] + xb[2] + xb[3];
-            v[e] = t - 2.0f * xb[3 - a];
-        }
-    }
-}
-template <int G, int V> __device__ __forceinline__ void regular(float (&v)[V], int lane) {
-    for (int d = 1; d < G; d *= 4) regular_digit<V>(v, lane, d);
-    const float c = (float) (1.0 / __builtin_sqrt((double) G));
-#pragma unroll
-    for (int e = 0; e < V; ++e) v[e] = v[e] * c;
-}
-
-// ---- h3s_norm_quant (NORM) and the quantizer of h3s_int8_linear (!NORM: x quantized as it is) ----
-template <int XDT, int CPL, int ROT, int G, bool NORM = true>
-__global__ __launch_bounds__(256) void norm_quant_kernel(const void* __restrict__ x, int64_t M, int64_t C,
-                                                         const float* __restrict__ w, float eps,
-                                                         const int32_t* __restrict__ rows, const void* __restrict__ scale,
-                                                         const void* __restrict__ shift, int tab_dt, int h_dt,
-                                                         int8_t* __restrict__ q, float* __restrict__ s) {
-    constexpr int V = Vec<XDT>::V;
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= M) return;
-    RowRegs<XDT, CPL> R;
-    R.load(x, row, C, lane);
-    const float inv = NORM ? inv_root(R.sumsq(lane), (float) C, eps) : 1.0f;
-    const int64_t tr = rows ? (int64_t) rows[row] * C : 0;
-    float m = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        // (rows past the end hold zeros: they take part in the cross-lane rotation stages and add nothing)
-        const bool ok = R.valid(lane, j);
-        const int64_t i = (lane + (int64_t) kWave * j) * V;
-        float* o = R.v[j];
-        if (NORM && ok) {
-            if (w) {
-                float wv[V];
-                load_f32x(w + i, wv, V);
-#pragma unroll
-                for (int e = 0; e < V; ++e) o[e] = o[e] * inv * wv[e];
-            } else {
-#pragma unroll
-                for (int e = 0; e < V; ++e) o[e] = o[e] * inv;
-            }
-            if (scale && shift) {
-                float sc[V], sh[V];
-                load_tab_rt<V>(scale, tab_dt, tr + i, sc);
-                load_tab_rt<V>(shift, tab_dt, tr + i, sh);
-#pragma unroll
-                for (int e = 0; e < V; ++e) o[e] = o[e] * (1.0f + sc[e]) + sh[e];
-            }
-#pragma unroll
-            for (int e = 0; e < V; ++e) o[e] = round_rt(o[e], h_dt);
-        }
-        if constexpr (ROT == H3S_ROT_SYLVESTER) sylvester<G, V>(R.v[j], lane);
-        else if constexpr (ROT == H3S_ROT_REGULAR) regular<G, V>(R.v[j], lane);
-        if (ok)
-#pragma unroll
-            for (int e = 0; e < V; ++e) m = fmaxf(m, fabsf(o[e]));
-    }
-    m = wave_max<kWave>(m);
-    const float sc = fmaxf(m / 127.0f, 1e-30f);
-    const float r = 1.0f / sc;
-    if (lane == 0) s[row] = sc;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        if (!R.valid(lane, j)) continue;
-        const int64_t i = (lane + (int64_t) kWave * j) * V;
-        const float* o = R.v[j];
-        if constexpr (V == 8) {
-            *reinterpret_cast<uint2*>(q + row * C + i) =
-                make_uint2(pack_i8x4(quant_code(o[0], sc, r), quant_code(o[1], sc, r), quant_code(o[2], sc, r), quant_code(o[3], sc, r)),
-                           pack_i8x4(quant_code(o[4], sc, r), quant_code(o[5], sc, r), quant_code(o[6], sc, r), quant_code(o[7], sc, r)));
-        } else {
-            *reinterpret_cast<uint32_t*>(q + row * C + i) =
-                pack_i8x4(quant_code(o[0], sc, r), quant_code(o[1], sc, r), quant_code(o[2], sc, r), quant_code(o[3], sc, r));
-        }
-    }
-}
-
 // ---- host: shapes, preconditions, instantiation ----
 static const char* cpl_error = "rows longer than 16 x 64 16-byte vectors (8192 16-bit or 4096 float32 features) are not supported";
 
@@ -489,77 +343,3 @@ H3S_EXPORT int h3s_norm_mod_act_gate(void* ctx, const void* x, int x_dt, int64_t
     return launched("h3s_norm_mod_act_gate");
 } catch (const std::exception& e) { return fail(e.what()); }
 
-static bool is_pow2(int g) { return g > 0 && (g & (g - 1)) == 0; }
-
-H3S_EXPORT int h3s_norm_quant(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, const float* weight, float eps,
-                              const int32_t* rows, const void* scale, const void* shift, int tab_dt, int h_dt, int rot,
-                              int group, int8_t* q, float* s) try {
-    if (M <= 0 || C <= 0) return 0;
-    int cpl;
-    if (row_checks("h3s_norm_quant", x_dt, h_dt, C, {x, weight, scale, shift, q}, &cpl)) return -1;
-    if (!dt_ok(tab_dt)) return fail("h3s_norm_quant: unknown element type");
-    if (!q || !s) return fail("h3s_norm_quant: q and s are required");
-    const int V = vec_of(x_dt);
-    if (rot == H3S_ROT_SYLVESTER) {
-        if (!is_pow2(group) || group < 2 || group > V * kWave || C % group != 0)
-            return fail("h3s_norm_quant: a Sylvester group is a power of 2 dividing C, at most 64 vectors");
-    } else if (rot == H3S_ROT_REGULAR) {
-        if (!is_pow2(group) || (__builtin_ctz((unsigned) group) & 1) || group < 4 || group > 256 || C % group != 0)
-            return fail("h3s_norm_quant: a regular group is a power of 4 dividing C, at most 256");
-    } else if (rot != H3S_ROT_NONE) return fail("h3s_norm_quant: unknown rotation");
-    Ctx* c = ctx_of(ctx, "h3s_norm_quant");
-    if (!c) return -1;
-#define LK(XDT, CPL, ROT, G)                                                                                             \
-    norm_quant_kernel<XDT, CPL, ROT, G><<<grid_rows(M), 256, 0, c->stream>>>(x, M, C, weight, eps, rows, scale, shift, \
-                                                                              tab_dt, h_dt, q, s)
-#define LG(XDT, CPL, ROT)                             \
-    switch (group) {                                  \
-        case 2: LK(XDT, CPL, ROT, 2); break;          \
-        case 4: LK(XDT, CPL, ROT, 4); break;          \
-        case 8: LK(XDT, CPL, ROT, 8); break;          \
-        case 16: LK(XDT, CPL, ROT, 16); break;        \
-        case 32: LK(XDT, CPL, ROT, 32); break;        \
-        case 64: LK(XDT, CPL, ROT, 64); break;        \
-        case 128: LK(XDT, CPL, ROT, 128); break;      \
-        case 256: LK(XDT, CPL, ROT, 256); break;      \
-        default: LK(XDT, CPL, ROT, 512); break;       \
-    }
-#define L(XDT, CPL)                                                        \
-    if (rot == H3S_ROT_SYLVESTER) { LG(XDT, CPL, H3S_ROT_SYLVESTER); }     \
-    else if (rot == H3S_ROT_REGULAR) {                                     \
-        switch (group) {                                                   \
-            case 4: LK(XDT, CPL, H3S_ROT_REGULAR, 4); break;               \
-            case 16: LK(XDT, CPL, H3S_ROT_REGULAR, 16); break;             \
-            case 64: LK(XDT, CPL, H3S_ROT_REGULAR, 64); break;             \
-            default: LK(XDT, CPL, H3S_ROT_REGULAR, 256); break;            \
-        }                                                                  \
-    } else { LK(XDT, CPL, H3S_ROT_NONE, 1); }
-    H3_DT_SWITCH(x_dt, cpl, L)
-#undef L
-#undef LG
-#undef LK
-    return launched("h3s_norm_quant");
-} catch (const std::exception& e) { return fail(e.what()); }
-
-namespace h3 {
-// the quantizer of h3s_int8_linear: x [M, K] (any type) -> regular rotation per group (0: none) -> q, s
-int launch_quantize(Ctx* c, const void* x, int x_dt, int64_t M, int64_t K, int group, int8_t* q, float* s) {
-    int cpl;
-    if (row_checks("h3s_int8_linear", x_dt, x_dt, K, {x, q}, &cpl)) return -1;
-#define LK(XDT, CPL, ROT, G)                                                                                           \
-    norm_quant_kernel<XDT, CPL, ROT, G, false><<<grid_rows(M), 256, 0, c->stream>>>(x, M, K, nullptr, 0.0f, nullptr,  \
-                                                                                     nullptr, nullptr, H3S_F32, H3S_F32, q, s)
-#define L(XDT, CPL)                                                    \
-    switch (group) {                                                   \
-        case 0: LK(XDT, CPL, H3S_ROT_NONE, 1); break;                  \
-        case 4: LK(XDT, CPL, H3S_ROT_REGULAR, 4); break;               \
-        case 16: LK(XDT, CPL, H3S_ROT_REGULAR, 16); break;             \
-        case 64: LK(XDT, CPL, H3S_ROT_REGULAR, 64); break;             \
-        default: LK(XDT, CPL, H3S_ROT_REGULAR, 256); break;            \
-    }
-    H3_DT_SWITCH(x_dt, cpl, L)
-#undef L
-#undef LK
-    return launched("h3s_int8_linear");
-}
-}  // namespace h3
