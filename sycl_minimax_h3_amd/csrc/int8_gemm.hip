@@ -31,15 +31,23 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(const int8_t* __restrict__
     const int wm = wave >> 1, wn = wave & 1;
     const int64_t m0 = (int64_t) (blockIdx.x / tiles_n) * kBM, n0 = (int64_t) (blockIdx.x % tiles_n) * kBN;
 
-    // global -> register staging: thread t moves 16-byte pieces t + 256 i (i < 4) of each 256 x 64 tile
+    // global -> register staging: thread t moves 16-byte pieces t + 256 i (i < 4) of each 256 x 64 tile; rows past
+    // M or N read the last row again (their products land in rows / columns that are not stored)
+    const int8_t* pa[4];
+    const int8_t* pb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int id = tid + 256 * i, r = id >> 2, c16 = id & 3;
+        const int64_t ma = m0 + r < M ? m0 + r : M - 1, nb = n0 + r < N ? n0 + r : N - 1;
+        pa[i] = A + ma * K + c16 * 16;
+        pb[i] = W + nb * K + c16 * 16;
+    }
     uint4 ga[4], gb[4];
     auto gload = [&](int64_t k0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int id = tid + 256 * i, r = id >> 2, c16 = id & 3;
-            const int64_t ma = m0 + r, nb = n0 + r;
-            ga[i] = ma < M ? *reinterpret_cast<const uint4*>(A + ma * K + k0 + c16 * 16) : make_uint4(0, 0, 0, 0);
-            gb[i] = nb < N ? *reinterpret_cast<const uint4*>(W + nb * K + k0 + c16 * 16) : make_uint4(0, 0, 0, 0);
+            ga[i] = *reinterpret_cast<const uint4*>(pa[i] + k0);
+            gb[i] = *reinterpret_cast<const uint4*>(pb[i] + k0);
         }
     };
     auto sstore = [&]() {

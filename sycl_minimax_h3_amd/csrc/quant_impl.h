@@ -183,11 +183,13 @@ __global__ __launch_bounds__(256) void quant_kernel(QuantArgs A) {
     // ---- the row, chunk c = lane + 64 j ----
     uint4 raw[CPL];
     {
+        // every lane loads (a chunk past the row's end reads the last one again and is never used): no branch
+        // between the loads, so all of them are in flight together
         const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * (16 / V));
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int64_t c = lane + (int64_t) kWave * j;
-            raw[j] = c < nch ? p[c] : make_uint4(0, 0, 0, 0);
+            raw[j] = p[c < nch ? c : nch - 1];
         }
     }
     float v[CPL][V];

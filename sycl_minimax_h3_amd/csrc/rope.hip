@@ -44,11 +44,13 @@ __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M
         uint4 ra[kUnits], rb[kUnits];
 #pragma unroll
         for (int k = 0; k < kUnits; ++k) {
-            const int u = u0 + k, t = u / ngroups, head = (u % ngroups) * HPW + hh;
-            const bool ok = u < nunits && active && head < H;
+            // every lane loads from a valid place (idle lanes and units past the end read head 0 / the last unit
+            // again, and their values are never used): no branch between the loads
+            const int u = u0 + k < nunits ? u0 + k : nunits - 1, t = u / ngroups, h0 = (u % ngroups) * HPW + hh;
+            const int head = active && h0 < H ? h0 : 0;
             const uint16_t* base = (const uint16_t*) (t ? x1 : x0) + (tok * stride + (int64_t) head * D) * (16 / V / 2);
-            ra[k] = ok ? *reinterpret_cast<const uint4*>(base + off0 * (16 / V / 2)) : make_uint4(0, 0, 0, 0);
-            rb[k] = ok && rotated ? *reinterpret_cast<const uint4*>(base + off1 * (16 / V / 2)) : make_uint4(0, 0, 0, 0);
+            ra[k] = *reinterpret_cast<const uint4*>(base + (active ? off0 : 0) * (16 / V / 2));
+            rb[k] = *reinterpret_cast<const uint4*>(base + (rotated ? off1 : 0) * (16 / V / 2));
         }
 #pragma unroll
         for (int k = 0; k < kUnits; ++k) {
@@ -60,11 +62,13 @@ __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M
             Vec<XDT>::unpack(ra[k], a);
             Vec<XDT>::unpack(rb[k], b);
             float s = 0.0f;
+            if (ok) {
 #pragma unroll
-            for (int e = 0; e < V; ++e) s = __builtin_fmaf(a[e], a[e], s);
-            if (rotated)
+                for (int e = 0; e < V; ++e) s = __builtin_fmaf(a[e], a[e], s);
+                if (rotated)
 #pragma unroll
-                for (int e = 0; e < V; ++e) s = __builtin_fmaf(b[e], b[e], s);
+                    for (int e = 0; e < V; ++e) s = __builtin_fmaf(b[e], b[e], s);
+            }
             s = wave_sum<P2>(s);
             if (!ok) continue;
             const float inv = inv_root(s, (float) D, eps);

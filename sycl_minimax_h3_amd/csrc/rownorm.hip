@@ -19,10 +19,12 @@ template <int XDT, int CPL> struct RowRegs {
         nch = C / V;
         const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(x) + row * C * (16 / V));
         uint4 raw[CPL];
+        // every lane loads (a chunk past the row's end reads the last one again and is never used): no branch
+        // between the loads, so all of them are in flight together
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int64_t c = lane + (int64_t) kWave * j;
-            raw[j] = c < nch ? p[c] : make_uint4(0, 0, 0, 0);
+            raw[j] = p[c < nch ? c : nch - 1];
         }
 #pragma unroll
         for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(raw[j], v[j]);
@@ -179,7 +181,7 @@ __global__ __launch_bounds__(256) void norm_mod_act_gate_kernel(
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int64_t c = lane + (int64_t) kWave * j;
-            if constexpr (V == 8) rraw[j] = c < R.nch ? rp[c] : make_uint4(0, 0, 0, 0);
+            if constexpr (V == 8) rraw[j] = rp[c < R.nch ? c : R.nch - 1];
         }
     }
     float mean = 0.0f, inv;
