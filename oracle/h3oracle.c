@@ -176,17 +176,26 @@ void h3o_choose(uint64_t seed, int64_t n, int64_t k, int64_t* out) {
     free(idx);
 }
 
-/* ---- canonical reduction ---- */
+/* ---- canonical reduction ----
+ * L lane partials, L a power of two up to 512. Up to 64 lanes (one wavefront): the xor butterfly with offsets
+ * L/2, ..., 1. Beyond: that butterfly inside each group of 64 lanes first, then the same butterfly over the L/64
+ * group sums (offsets L/128, ..., 1). */
 static float butterfly(float* p, int L) {
-    float tmp[64];
+    float tmp[512];
     for (int off = L / 2; off >= 1; off /= 2) {
         for (int l = 0; l < L; ++l) tmp[l] = p[l] + p[l ^ off];
         memcpy(p, tmp, (size_t) L * sizeof(float));
     }
     return p[0];
 }
+static float canon_combine(float* p, int L) {
+    if (L <= 64) return butterfly(p, L);
+    float w[8];
+    for (int g = 0; g < L / 64; ++g) w[g] = butterfly(p + 64 * g, 64);
+    return butterfly(w, L / 64);
+}
 float h3o_canon_sum(const float* x, int64_t n, int V, int L, int kind, float mean) {
-    float p[64];
+    float p[512];
     for (int l = 0; l < L; ++l) p[l] = 0.0f;
     for (int64_t i = 0; i < n; ++i) {
         const int l = (int) ((i / V) % L);
@@ -195,7 +204,12 @@ float h3o_canon_sum(const float* x, int64_t n, int V, int L, int kind, float mea
         else if (kind == H3O_SUMSQ) p[l] = fmaf(v, v, p[l]);
         else { const float d = v - mean; p[l] = fmaf(d, d, p[l]); }
     }
-    return butterfly(p, L);
+    return canon_combine(p, L);
+}
+/* lanes per row of n values in 16-byte chunks of V: 64 below 256 chunks, 256 up to 1024, 512 up to 2048 */
+int h3o_row_lanes(int64_t n, int V) {
+    const int64_t nch = n / V;
+    return nch < 256 ? 64 : nch <= 1024 ? 256 : 512;
 }
 
 /* 1 / sqrt(mean + eps), each step correctly rounded (the reference's sycl::rsqrt, h3sycl.cpp:779, 1264) */
@@ -212,7 +226,7 @@ static void rmsn_rows(void* p, int64_t r0, int64_t r1) {
     float* row = (float*) malloc((size_t) C * sizeof(float));
     for (int64_t r = r0; r < r1; ++r) {
         for (int64_t i = 0; i < C; ++i) row[i] = h3o_load(c->x, c->x_dt, r * C + i);
-        const float inv = inv_root(h3o_canon_sum(row, C, vec_of(c->x_dt), 64, H3O_SUMSQ, 0.0f), C, c->eps);
+        const float inv = inv_root(h3o_canon_sum(row, C, vec_of(c->x_dt), h3o_row_lanes(C, vec_of(c->x_dt)), H3O_SUMSQ, 0.0f), C, c->eps);
         for (int64_t i = 0; i < C; ++i) {
             float v = row[i] * inv * c->w[i];
             if (c->rows) {
@@ -239,8 +253,9 @@ typedef struct {
     const void* x; int x_dt; int64_t C; const float* w; const float* b; float eps; void* out; int out_dt;
 } ln_ctx;
 static void ln_stats(const float* row, int64_t C, int V, float eps, float* mean, float* inv) {
-    *mean = h3o_canon_sum(row, C, V, 64, H3O_SUM, 0.0f) / (float) C;
-    *inv = inv_root(h3o_canon_sum(row, C, V, 64, H3O_SUMSQ_DIFF, *mean), C, eps);
+    const int L = h3o_row_lanes(C, V);
+    *mean = h3o_canon_sum(row, C, V, L, H3O_SUM, 0.0f) / (float) C;
+    *inv = inv_root(h3o_canon_sum(row, C, V, L, H3O_SUMSQ_DIFF, *mean), C, eps);
 }
 static void ln_rows(void* p, int64_t r0, int64_t r1) {
     const ln_ctx* c = (const ln_ctx*) p;
@@ -496,7 +511,7 @@ static void nq_rows(void* p, int64_t r0, int64_t r1) {
     float* y = (float*) malloc((size_t) C * sizeof(float));
     for (int64_t r = r0; r < r1; ++r) {
         for (int64_t i = 0; i < C; ++i) y[i] = h3o_load(c->x, c->x_dt, r * C + i);
-        const float inv = inv_root(h3o_canon_sum(y, C, vec_of(c->x_dt), 64, H3O_SUMSQ, 0.0f), C, c->eps);
+        const float inv = inv_root(h3o_canon_sum(y, C, vec_of(c->x_dt), h3o_row_lanes(C, vec_of(c->x_dt)), H3O_SUMSQ, 0.0f), C, c->eps);
         const int64_t tr = c->rows ? c->rows[r] : 0;
         for (int64_t i = 0; i < C; ++i) {
             float v = y[i] * inv;
@@ -539,7 +554,7 @@ static void nmag_rows(void* p, int64_t r0, int64_t r1) {
         for (int64_t i = 0; i < C; ++i) row[i] = h3o_load(c->x, c->x_dt, r * C + i);
         float mean = 0.0f, inv;
         if (c->norm == H3O_NORM_LAYER) ln_stats(row, C, V, c->eps, &mean, &inv);
-        else inv = inv_root(h3o_canon_sum(row, C, V, 64, H3O_SUMSQ, 0.0f), C, c->eps);
+        else inv = inv_root(h3o_canon_sum(row, C, V, h3o_row_lanes(C, V), H3O_SUMSQ, 0.0f), C, c->eps);
         const int64_t tr = c->rows ? c->rows[r] : 0;
         for (int64_t i = 0; i < C; ++i) {
             float v = c->norm == H3O_NORM_LAYER ? (row[i] - mean) * inv : row[i] * inv;

@@ -10,8 +10,13 @@
  *
  *   the row's n values are cut into chunks of V consecutive values; chunk c belongs to lane c % L;
  *   each lane accumulates its values in increasing index order, starting from +0.0f;
- *   the L lane partials are then combined by an xor butterfly with offsets L/2, L/4, ..., 1
- *   (partial[l] = partial[l] + partial[l ^ off]), which leaves the same value in every lane; lane 0's is the sum.
+ *   up to L = 64 (one wavefront), the L lane partials are then combined by an xor butterfly with offsets
+ *   L/2, L/4, ..., 1 (partial[l] = partial[l] + partial[l ^ off]), which leaves the same value in every lane;
+ *   lane 0's is the sum. For L = 128 .. 512 (several wavefronts on one row) that butterfly runs inside each group
+ *   of 64 lanes, and the L/64 group sums are then combined by the same butterfly.
+ *
+ * Rows of the row-wise operations (norms, fused chains) use L = h3o_row_lanes(n, V): 64 lanes below 256 chunks,
+ * 256 up to 1024 chunks, 512 up to 2048.
  *
  * Squares are accumulated with a fused multiply-add (acc = fma(x, x, acc)). Everything else is written out
  * operation by operation and must be compiled with -ffp-contract=off.
@@ -67,6 +72,8 @@ void h3o_choose(uint64_t seed, int64_t n, int64_t k, int64_t* out);
 
 /* ---- canonical reduction (see the header comment) ---- */
 float h3o_canon_sum(const float* x, int64_t n, int V, int L, int kind, float mean);
+/* lanes per row of n values in chunks of V (see the header comment) */
+int h3o_row_lanes(int64_t n, int V);
 
 /* ---- the reference's operations (kernels/h3sycl.h) ---- */
 /* kernels/h3sycl.h:96-101, 162-163; kernels/h3sycl.cpp:766-810 */

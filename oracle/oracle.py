@@ -48,6 +48,7 @@ _SIGS = {
     "h3o_fill_uniform": (None, [u64, f32, f32, i64, vp]),
     "h3o_choose": (None, [u64, i64, i64, vp]),
     "h3o_canon_sum": (f32, [vp, i64, i32, i32, i32, f32]),
+    "h3o_row_lanes": (i32, [i64, i32]),
     "h3o_rms_norm_mod": (i32, [vp, i32, i64, i64, vp, f32, vp, vp, vp, vp, i32]),
     "h3o_layer_norm": (i32, [vp, i32, i64, i64, vp, vp, f32, vp, i32]),
     "h3o_rms_rope": (i32, [vp, i32, i64, i64, i64, i64, vp, f32, vp, i32]),
@@ -188,6 +189,11 @@ def choose(seed: int, n: int, k: int) -> np.ndarray:
 def canon_sum(x: np.ndarray, V: int, L: int, kind: int = SUM, mean: float = 0.0) -> float:
     x = np.ascontiguousarray(x, dtype=np.float32)
     return float(lib().h3o_canon_sum(_p(x), x.size, V, L, kind, mean))
+
+
+def row_lanes(n: int, V: int) -> int:
+    """Lanes per row of the row-wise operations' canonical order."""
+    return int(lib().h3o_row_lanes(n, V))
 
 
 # ---- operations ----------------------------------------------------------------------------------------------

@@ -1,0 +1,220 @@
+// chain_impl.h - the row chain kernel behind h3s_rms_norm_mod, h3s_layer_norm (kernels/h3sycl.cpp:766-810,
+// 1248-1274) and the fused h3s_norm_mod_act_gate, instantiated per input type in chain_bf16.hip, chain_f16.hip and
+// chain_f32.hip.
+//
+// What it computes for each row (the oracle's h3o_norm_mod_act_gate; rms_norm_mod and layer_norm are the cases
+// with no activation, gate or residual):
+//   RMS:    n = x * inv,             inv = 1 / sqrt(sum x^2 / C + eps)
+//   LAYER:  n = (x - mean) * inv,    mean = sum x / C, inv = 1 / sqrt(sum (x - mean)^2 / C + eps)
+//   v = n [* w] [+ b] [* (1 + scale[t]) + shift[t]];  v = act(v) [* gate[t]];  out = [res +] v
+// with t = rows[r] (table row 0 when rows is NULL), everything in float32 and one rounding to out's type. The sums
+// follow the canonical order of rowcore.h. The row layout, the canonical sums and the stores are rowcore.h's; every
+// load of the row (x, the residual, the weights, the table rows) is issued before the first value is used.
+#pragma once
+
+#include "rowcore.h"
+
+namespace h3 {
+
+struct ChainArgs {
+    const void* x;
+    int64_t M, C;
+    int norm;                 // H3S_NORM_RMS or H3S_NORM_LAYER
+    const float* w;           // NULL: no weight
+    const float* b;           // NULL: no bias
+    float eps;
+    const int32_t* rows;      // NULL: table row 0 for every token
+    const void* scale;        // scale and shift: both or neither
+    const void* shift;
+    const void* gate;         // NULL: 1
+    int tab_dt;
+    int act;
+    const void* res;          // NULL: no residual
+    int res_dt;
+    void* out;
+    int out_dt;
+};
+
+template <int XDT, int CPL, int F>
+__global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift) {
+    constexpr int V = Vec<XDT>::V;
+    constexpr bool DYN = F & ROW_DYN;
+    constexpr bool TW = DYN || (F & ROW_TAB32), RW = DYN || (F & ROW_RES32);   // wide storage of tables, residual
+    __shared__ float red[2][8];
+    const bool has_w = DYN ? A.w != nullptr : (F & ROW_W) != 0;
+    const bool has_b = DYN ? A.b != nullptr : (F & ROW_B) != 0;
+    const bool has_tab = DYN ? A.scale != nullptr : (F & ROW_TAB) != 0;
+    const bool has_gate = DYN ? A.gate != nullptr : (F & ROW_GATE) != 0;
+    const bool has_res = DYN ? A.res != nullptr : (F & ROW_RES) != 0;
+    const int tab_dt = (!DYN && (F & ROW_TAB32)) ? H3S_F32 : A.tab_dt;
+    const int res_dt = (!DYN && (F & ROW_RES32)) ? H3S_F32 : A.res_dt;
+    const RowPos P = row_pos(lshift, A.M);
+    const int L = 1 << lshift;
+    const int64_t row = P.row, C = A.C, nch = C / V;
+
+    // chunk j of this lane, clamped into the row (a clamped chunk is loaded and never used)
+    int64_t cc[CPL];
+    bool ok[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int64_t c = P.t + (int64_t) L * j;
+        ok[j] = c < nch;
+        cc[j] = ok[j] ? c : nch - 1;
+    }
+
+    // ---- every load of the row, in flight together: the table row index first, then the row and the residual
+    // (HBM), then the weights and table rows (small, cache resident) ----
+    const int64_t tr = (has_tab || has_gate) && A.rows ? (int64_t) A.rows[row] * C : 0;
+    uint4 xr[CPL];
+    {
+        const uint4* xp = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * (16 / V));
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) xr[j] = xp[cc[j]];
+    }
+    Raw<V, RW> rr[CPL];
+    Raw<V, true> wr[CPL], br[CPL];
+    Raw<V, TW> sr[CPL], hr[CPL], gr[CPL];
+    if (has_res)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) fetch(rr[j], A.res, res_dt, row * C + cc[j] * V);
+    if (has_w)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) fetch(wr[j], A.w, H3S_F32, cc[j] * V);
+    if (has_b)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) fetch(br[j], A.b, H3S_F32, cc[j] * V);
+    if (has_tab) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            fetch(sr[j], A.scale, tab_dt, tr + cc[j] * V);
+            fetch(hr[j], A.shift, tab_dt, tr + cc[j] * V);
+        }
+    }
+    if (has_gate)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) fetch(gr[j], A.gate, tab_dt, tr + cc[j] * V);
+
+    // ---- row statistics ----
+    float v[CPL][V];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(xr[j], v[j]);
+    float mean = 0.0f, inv;
+    if (A.norm == H3S_NORM_LAYER) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+            if (ok[j])
+#pragma unroll
+                for (int e = 0; e < V; ++e) s = s + v[j][e];
+        mean = row_sum(s, red[0], P.W) / (float) C;
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+            if (ok[j])
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const float d = v[j][e] - mean;
+                    q = __builtin_fmaf(d, d, q);
+                }
+        inv = inv_root(row_sum(q, red[1], P.W), (float) C, A.eps);
+    } else {
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+            if (ok[j])
+#pragma unroll
+                for (int e = 0; e < V; ++e) q = __builtin_fmaf(v[j][e], v[j][e], q);
+        inv = inv_root(row_sum(q, red[0], P.W), (float) C, A.eps);
+    }
+
+    // ---- the chain, one chunk at a time ----
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        float o[V], f[V], g[V];
+        if (A.norm == H3S_NORM_LAYER) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) o[e] = (v[j][e] - mean) * inv;
+        } else {
+#pragma unroll
+            for (int e = 0; e < V; ++e) o[e] = v[j][e] * inv;
+        }
+        if (has_w) {
+            decode(wr[j], H3S_F32, f);
+#pragma unroll
+            for (int e = 0; e < V; ++e) o[e] = o[e] * f[e];
+        }
+        if (has_b) {
+            decode(br[j], H3S_F32, f);
+#pragma unroll
+            for (int e = 0; e < V; ++e) o[e] = o[e] + f[e];
+        }
+        if (has_tab) {
+            decode(sr[j], tab_dt, f);
+            decode(hr[j], tab_dt, g);
+#pragma unroll
+            for (int e = 0; e < V; ++e) o[e] = o[e] * (1.0f + f[e]) + g[e];
+        }
+        if (A.act == H3S_ACT_GELU_TANH) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) o[e] = act_gelu_tanh(o[e]);
+        } else if (A.act == H3S_ACT_SILU) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) o[e] = act_silu(o[e]);
+        }
+        if (has_gate) {
+            decode(gr[j], tab_dt, f);
+#pragma unroll
+            for (int e = 0; e < V; ++e) o[e] = o[e] * f[e];
+        }
+        if (has_res) {
+            decode(rr[j], res_dt, f);
+#pragma unroll
+            for (int e = 0; e < V; ++e) o[e] = f[e] + o[e];
+        }
+        if (P.live && ok[j]) store_chunk<V>(A.out, A.out_dt, row * C + cc[j] * V, o);
+    }
+}
+
+// The feature masks compiled exactly (16-bit inputs): h3s_rms_norm_mod without and with its float32 tables,
+// h3s_layer_norm without and with weight and bias, and the AdaLN chain with 16-bit tables, gate and residual.
+// Every other call shape runs the ROW_DYN instantiation.
+constexpr int kChainW = ROW_W, kChainWTab32 = ROW_W | ROW_TAB | ROW_TAB32, kChainNone = 0, kChainWB = ROW_W | ROW_B,
+              kChainTabGateRes = ROW_TAB | ROW_GATE | ROW_RES;
+
+inline int chain_features(const ChainArgs& A) {
+    const bool t16 = A.tab_dt != H3S_F32, r16 = A.res_dt != H3S_F32;
+    const int f = (A.w ? ROW_W : 0) | (A.b ? ROW_B : 0) | (A.scale ? ROW_TAB | (t16 ? 0 : ROW_TAB32) : 0) |
+                  (A.gate ? ROW_GATE : 0) | (A.res ? ROW_RES | (r16 ? 0 : ROW_RES32) : 0);
+    if (A.gate && !A.scale && !t16) return ROW_DYN;   // a float32 gate alone has no exact mask
+    return f;
+}
+
+// Launches the chain for one input type; the plan comes from row_plan.
+template <int XDT> int chain_launch(Ctx* c, const char* fn, const ChainArgs& A, RowPlan p) {
+    const RowLaunch R = row_launch(A.M, p);
+    int f = chain_features(A);
+    if (XDT == H3S_F32 || !(f == kChainW || f == kChainWTab32 || f == kChainNone || f == kChainWB || f == kChainTabGateRes))
+        f = ROW_DYN;
+#define H3_CHAIN_F(CC, FF) row_chain_kernel<XDT, CC, FF><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift)
+#define H3_CHAIN_CPL(CC)                                                    \
+    if (p.cpl == CC) {                                                      \
+        if constexpr (XDT != H3S_F32) {                                     \
+            if (f == kChainW) { H3_CHAIN_F(CC, kChainW); return launched(fn); }                     \
+            if (f == kChainWTab32) { H3_CHAIN_F(CC, kChainWTab32); return launched(fn); }           \
+            if (f == kChainNone) { H3_CHAIN_F(CC, kChainNone); return launched(fn); }               \
+            if (f == kChainWB) { H3_CHAIN_F(CC, kChainWB); return launched(fn); }                   \
+            if (f == kChainTabGateRes) { H3_CHAIN_F(CC, kChainTabGateRes); return launched(fn); }   \
+        }                                                                   \
+        H3_CHAIN_F(CC, ROW_DYN);                                            \
+        return launched(fn);                                                \
+    }
+    H3_CHAIN_CPL(1)
+    H3_CHAIN_CPL(2)
+    H3_CHAIN_CPL(3)
+    H3_CHAIN_CPL(4)
+#undef H3_CHAIN_CPL
+#undef H3_CHAIN_F
+    return fail(std::string(fn) + ": no kernel for this row length");
+}
+
+}  // namespace h3

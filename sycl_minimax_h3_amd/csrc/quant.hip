@@ -7,27 +7,32 @@
 
 namespace h3 {
 
-template <int XDT> int quant_launch(Ctx*, const char*, QuantArgs, int, int, int, bool);
-extern template int quant_launch<H3S_BF16>(Ctx*, const char*, QuantArgs, int, int, int, bool);
-extern template int quant_launch<H3S_F16>(Ctx*, const char*, QuantArgs, int, int, int, bool);
-extern template int quant_launch<H3S_F32>(Ctx*, const char*, QuantArgs, int, int, int, bool);
+template <int XDT> int quant_launch(Ctx*, const char*, const QuantArgs&, RowPlan);
+extern template int quant_launch<H3S_BF16>(Ctx*, const char*, const QuantArgs&, RowPlan);
+extern template int quant_launch<H3S_F16>(Ctx*, const char*, const QuantArgs&, RowPlan);
+extern template int quant_launch<H3S_F32>(Ctx*, const char*, const QuantArgs&, RowPlan);
 
-static int dispatch(Ctx* c, const char* fn, int x_dt, const QuantArgs& A, int rot, int hdt, int tab, bool norm) {
+static int dispatch(Ctx* c, const char* fn, int x_dt, const QuantArgs& A, RowPlan p) {
     switch (x_dt) {
-        case H3S_BF16: return quant_launch<H3S_BF16>(c, fn, A, rot, hdt, tab, norm);
-        case H3S_F16: return quant_launch<H3S_F16>(c, fn, A, rot, hdt, tab, norm);
-        default: return quant_launch<H3S_F32>(c, fn, A, rot, hdt, tab, norm);
+        case H3S_BF16: return quant_launch<H3S_BF16>(c, fn, A, p);
+        case H3S_F16: return quant_launch<H3S_F16>(c, fn, A, p);
+        default: return quant_launch<H3S_F32>(c, fn, A, p);
     }
 }
 
 static bool is_pow2(int g) { return g > 0 && (g & (g - 1)) == 0; }
+static float inv_sqrt_group(int g) { return (float) (1.0 / std::sqrt((double) g)); }
+static const char* too_long = ": rows longer than 2048 16-byte vectors (16384 16-bit or 8192 float32 features) are not supported";
 
 int launch_quantize(Ctx* c, const void* x, int x_dt, int64_t M, int64_t K, int group, int8_t* q, float* s) {
-    if (K % vec_of(x_dt) != 0) return fail("h3s_int8_linear: K must be whole 16-byte vectors");
-    if (group > 0 && K % kSeg != 0) return fail("h3s_int8_linear: a rotated row must be a multiple of 64 features");
-    QuantArgs A{x, M, K, nullptr, 0.0f, nullptr, nullptr, nullptr, group, group > 0 ? (float) (1.0 / std::sqrt((double) group)) : 1.0f,
-                q, s, 0};
-    return dispatch(c, "h3s_int8_linear", x_dt, A, group > 0 ? H3S_ROT_REGULAR : H3S_ROT_NONE, H3S_F32, TAB_NONE, false);
+    const char* fn = "h3s_int8_linear";
+    const int V = vec_of(x_dt);
+    if (K % V != 0) return fail(std::string(fn) + ": K must be whole 16-byte vectors");
+    const RowPlan p = row_plan(K / V);
+    if (!p.L) return fail(std::string(fn) + too_long);
+    const QuantArgs A{x, M, K, false, nullptr, 0.0f, nullptr, nullptr, nullptr, H3S_F32, H3S_F32,
+                      group > 0 ? H3S_ROT_REGULAR : H3S_ROT_NONE, group, group > 0 ? inv_sqrt_group(group) : 1.0f, q, s};
+    return dispatch(c, fn, x_dt, A, p);
 }
 
 }  // namespace h3
@@ -44,20 +49,22 @@ H3S_EXPORT int h3s_norm_quant(void* ctx, const void* x, int x_dt, int64_t M, int
     if (C % V != 0) return fail(std::string(fn) + ": C must be a multiple of " + std::to_string(V) + " (whole 16-byte vectors per row)");
     for (const void* p : {x, (const void*) weight, scale, shift, (const void*) q})
         if (p && !aligned16(p)) return fail(std::string(fn) + ": tensors must be 16-byte aligned");
-    if (!q || !s) return fail(std::string(fn) + ": q and s are required");
+    if (!x || !q || !s) return fail(std::string(fn) + ": x, q and s are required");
+    // a group of G features spans G / V lanes of one wavefront
     if (rot == H3S_ROT_SYLVESTER) {
-        if (!is_pow2(group) || group < 2 || group > 512 || C % group != 0 || (group > 64 && C % 64 != 0))
-            return fail(std::string(fn) + ": a Sylvester group is a power of 2 dividing C, at most 512");
+        if (!is_pow2(group) || group < 2 || group > 64 * V || C % group != 0)
+            return fail(std::string(fn) + ": a Sylvester group is a power of 2 dividing C, at most " + std::to_string(64 * V));
     } else if (rot == H3S_ROT_REGULAR) {
         if (!is_pow2(group) || (__builtin_ctz((unsigned) group) & 1) || group < 4 || group > 256 || C % group != 0)
             return fail(std::string(fn) + ": a regular group is a power of 4 dividing C, at most 256");
     } else if (rot != H3S_ROT_NONE) return fail(std::string(fn) + ": unknown rotation");
-    if (scale && shift && tab_dt != H3S_F32 && tab_dt != H3S_BF16) return fail(std::string(fn) + ": tables are float32 or bfloat16");
-    if (rot != H3S_ROT_NONE && C % kSeg != 0) return fail(std::string(fn) + ": a rotated row must be a multiple of 64 features");
+    const bool mod = scale && shift;
+    if (mod && tab_dt != H3S_F32 && tab_dt != H3S_BF16) return fail(std::string(fn) + ": tables are float32 or bfloat16");
+    const RowPlan p = row_plan(C / V);
+    if (!p.L) return fail(std::string(fn) + too_long);
     Ctx* c = ctx_of(ctx, fn);
     if (!c) return -1;
-    const int tab = !(scale && shift) ? TAB_NONE : tab_dt == H3S_BF16 ? TAB_BF16 : TAB_F32;
-    QuantArgs A{x, M, C, weight, eps, rows, scale, shift, group, rot != H3S_ROT_NONE ? (float) (1.0 / std::sqrt((double) group)) : 1.0f,
-                q, s, 0};
-    return dispatch(c, fn, x_dt, A, rot, h_dt, tab, true);
+    const QuantArgs A{x, M, C, true, weight, eps, rows, mod ? scale : nullptr, mod ? shift : nullptr, tab_dt, h_dt, rot,
+                      rot != H3S_ROT_NONE ? group : 0, rot != H3S_ROT_NONE ? inv_sqrt_group(group) : 1.0f, q, s};
+    return dispatch(c, fn, x_dt, A, p);
 } catch (const std::exception& e) { return fail(e.what()); }

@@ -1,20 +1,19 @@
 // quant_impl.h - the row quantizer kernel behind h3s_norm_quant and h3s_int8_linear, instantiated per input type in
-// quant_bf16.hip, quant_f16.hip and quant_f32.hip (so the three compile in parallel).
+// quant_bf16.hip, quant_f16.hip and quant_f32.hip.
 //
 // What it computes (the oracle's h3o_norm_quant / h3o_int8_linear quantizer):
-//   NORM:  h = round_to_h_dt(x * inv_rms * w [* (1 + scale[t]) + shift[t]])     rms_norm_mod into the reference's
+//   NORM:  h = round_to_h_dt(x * inv_rms [* w] [* (1 + scale[t]) + shift[t]])  rms_norm_mod into the reference's
 //          scratch h (engine/h3-core/src/dit.rs:340-342, kernels/h3sycl.cpp:766-810)
 //   !NORM: h = x                                                               (h3s_int8_linear's own input)
-//   y = h . H per group of G features (none, regular h4^(x)k, or Sylvester H2^(x)k; normalized by fl(1/sqrt(G)))
+//   y = h . H per group of G features (none, regular h4^(x)k, or Sylvester H2^(x)k), then * fl(1/sqrt(G))
 //   s = max(max|y| / 127, 1e-30); q = rint(y / s)                               (kernels/h3sycl.cpp:465-472)
 //
-// Layout: one 64-wide wavefront per token row. The row is read through 16-byte loads, lane l holding chunks l,
-// l + 64, ... (each load instruction of the wave covers 1 KiB of consecutive bytes); the sum of squares is the
-// lane's own in chunk order, then an xor butterfly over the 64 lanes (the oracle's canonical order). With a
-// rotation, h goes through LDS (as h's bits) so that each lane then owns 64 consecutive features, a "segment": the
-// butterfly stages inside a segment run in the lane's registers, and only stages across segments exchange values
-// (DPP within a quad / row, LDS crossbar beyond). The codes go back through LDS to the chunk layout, so every global
-// store is coalesced as well.
+// Layout: rowcore.h's. A rotation group of G features is G/V consecutive chunks, so it lives in G/V consecutive
+// lanes (G/V <= 64: one wavefront) at the same chunk slot of each: its butterfly stages inside a chunk run in the
+// lane's registers, and the stages across chunks exchange values between lanes (DPP inside a row of 16 lanes, the
+// LDS crossbar beyond), with no staging through memory. A group's chunks are all inside the row or all past it, so
+// lanes that hold a clamped copy of the last chunk only ever exchange with each other. The group size is a runtime
+// value: each possible stage is compiled once and runs when the group is large enough.
 //
 // Quantization: q = rint(y / s) with y / s correctly rounded, formed as Markstein's corrected quotient from
 // r = fl(1 / s) (one IEEE division per row), then rounded to nearest-even by adding 1.5 * 2^23, whose low byte is
@@ -22,12 +21,9 @@
 // never binds and is not evaluated.
 #pragma once
 
-#include "common.h"
+#include "rowcore.h"
 
 namespace h3 {
-
-constexpr int kSeg = 64;   // features a lane owns in the segment layout
-enum { TAB_NONE = 0, TAB_F32 = 1, TAB_BF16 = 2 };
 
 __device__ __forceinline__ float code_of(float y, float s, float r) {
     const float q1 = y * r;
@@ -42,394 +38,282 @@ __device__ __forceinline__ uint32_t bytes4(float a, float b, float c, float d) {
     return lo | hi;
 }
 
-// the value of lane (lane ^ OFF): quad permutes, two half-row shifts, a row rotate, a swizzle; beyond, the LDS
-// crossbar. No initial value: every lane's source is valid, or (xor 4) overwritten by the second half.
-template <int OFF> __device__ __forceinline__ float xl(float v) {
+// the value held by lane (lane ^ X) of the wavefront: quad permutes (1, 2, 3), two half-row shifts (4), a row
+// rotate (8), a swizzle inside each half of the wave (other X < 32), the LDS crossbar (X >= 32)
+template <int X> __device__ __forceinline__ float lane_xor(float v) {
+    static_assert(X > 0 && X < 64, "lane_xor: 1 .. 63");
     const int x = __float_as_int(v);
     int r;
-    if constexpr (OFF == 1) r = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true);
-    else if constexpr (OFF == 2) r = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);
-    else if constexpr (OFF == 4) {
-        const int t = __builtin_amdgcn_mov_dpp(x, 0x104, 0xF, 0xF, true);      // row_shl:4, right for lanes 0-3, 8-11
-        r = __builtin_amdgcn_update_dpp(t, x, 0x114, 0xF, 0xA, false);          // row_shr:4 for lanes 4-7, 12-15
-    } else if constexpr (OFF == 8) r = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true);   // row_ror:8
-    else if constexpr (OFF == 16) r = __builtin_amdgcn_ds_swizzle(x, 0x401F);                // xor 16 in 32
-    else r = __builtin_amdgcn_ds_bpermute((int) ((__lane_id() ^ (unsigned) OFF) << 2), x);
+    if constexpr (X == 1) r = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true);          // quad_perm [1,0,3,2]
+    else if constexpr (X == 2) r = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);     // quad_perm [2,3,0,1]
+    else if constexpr (X == 3) r = __builtin_amdgcn_mov_dpp(x, 0x1B, 0xF, 0xF, true);     // quad_perm [3,2,1,0]
+    else if constexpr (X == 4) {
+        const int t = __builtin_amdgcn_mov_dpp(x, 0x104, 0xF, 0xF, true);                  // row_shl:4, lanes 0-3, 8-11
+        r = __builtin_amdgcn_update_dpp(t, x, 0x114, 0xF, 0xA, false);                      // row_shr:4, lanes 4-7, 12-15
+    } else if constexpr (X == 8) r = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true);  // row_ror:8
+    else if constexpr (X < 32) r = __builtin_amdgcn_ds_swizzle(x, 0x1F | (X << 10));      // and 0x1f, xor X
+    else r = __builtin_amdgcn_ds_bpermute((int) ((__lane_id() ^ (unsigned) X) << 2), x);
     return __int_as_float(r);
 }
-template <int B> __device__ __forceinline__ float quad_lane(float v) {      // lane (lane & ~3) | B
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), B | (B << 2) | (B << 4) | (B << 6), 0xF, 0xF, true));
-}
 
-// Sylvester stage across segments: lane ^ OFF pairs; the lower lane forms a + b and the upper a - b, both as
-// fma(+-1, own, partner), which is exactly that sum or difference
-template <int OFF> __device__ __forceinline__ void syl_cross(float (&v)[kSeg], int lane) {
-    const float sg = (lane & OFF) ? -1.0f : 1.0f;
+// ---- Sylvester: stages h = 1, 2, ..., G/2 in order, (a, b) -> (a + b, a - b) for the pair h apart ----
+template <int V, int H> __device__ __forceinline__ void syl_in(float (&v)[V]) {
 #pragma unroll
-    for (int e = 0; e < kSeg; ++e) v[e] = __builtin_fmaf(sg, v[e], xl<OFF>(v[e]));
-}
-// one in-lane Sylvester stage: pairs H apart
-template <int H> __device__ __forceinline__ void syl_stage(float (&v)[kSeg]) {
-#pragma unroll
-    for (int e = 0; e < kSeg; ++e)
+    for (int e = 0; e < V; ++e)
         if (!(e & H)) {
             const float a = v[e], b = v[e + H];
             v[e] = a + b;
             v[e + H] = a - b;
         }
 }
-// one in-lane regular digit: quads D apart
-template <int D> __device__ __forceinline__ void reg_digit(float (&v)[kSeg]) {
+// the pair S lanes apart: the lower lane keeps a + b, the upper a - b, both as fma(+-1, own, partner), which is
+// exactly that sum or difference
+template <int V, int S> __device__ __forceinline__ void syl_x(float (&v)[V], int lane) {
+    const float sg = (lane & S) ? -1.0f : 1.0f;
 #pragma unroll
-    for (int e = 0; e < kSeg; ++e) {
+    for (int e = 0; e < V; ++e) v[e] = __builtin_fmaf(sg, v[e], lane_xor<S>(v[e]));
+}
+template <int V> __device__ __forceinline__ void sylvester(float (&v)[V], int lane, int G) {
+    if (G > 1) syl_in<V, 1>(v);
+    if (G > 2) syl_in<V, 2>(v);
+    if constexpr (V == 8)
+        if (G > 4) syl_in<V, 4>(v);
+    if (G > V) syl_x<V, 1>(v, lane);
+    if (G > 2 * V) syl_x<V, 2>(v, lane);
+    if (G > 4 * V) syl_x<V, 4>(v, lane);
+    if (G > 8 * V) syl_x<V, 8>(v, lane);
+    if (G > 16 * V) syl_x<V, 16>(v, lane);
+    if (G > 32 * V) syl_x<V, 32>(v, lane);
+}
+
+// ---- regular: one base-4 digit at a time, low digit first (kernels/h3sycl.cpp:433-459); for the four values
+// x0..x3 that differ in that digit, t = (x0 + x1) + (x2 + x3) and y_a = t - 2 x_(3-a) ----
+// the digit of stride D inside the lane (4 D <= V)
+template <int V, int D> __device__ __forceinline__ void reg_in(float (&v)[V]) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
         if ((e / D) % 4 != 0) continue;
         const float x0 = v[e], x1 = v[e + D], x2 = v[e + 2 * D], x3 = v[e + 3 * D];
         const float t = (x0 + x1) + (x2 + x3);
         v[e] = t - 2.0f * x3; v[e + D] = t - 2.0f * x2; v[e + 2 * D] = t - 2.0f * x1; v[e + 3 * D] = t - 2.0f * x0;
     }
 }
-// Sylvester stages h = 1, 2, ..., G/2 in order (the oracle's): below 64 inside the lane, then across segments
-template <int G> __device__ __forceinline__ void sylvester_seg(float (&v)[kSeg], int lane) {
-    if constexpr (G > 1) syl_stage<1>(v);
-    if constexpr (G > 2) syl_stage<2>(v);
-    if constexpr (G > 4) syl_stage<4>(v);
-    if constexpr (G > 8) syl_stage<8>(v);
-    if constexpr (G > 16) syl_stage<16>(v);
-    if constexpr (G > 32) syl_stage<32>(v);
-    if constexpr (G > 64) syl_cross<1>(v, lane);
-    if constexpr (G > 128) syl_cross<2>(v, lane);
-    if constexpr (G > 256) syl_cross<4>(v, lane);
-}
-// regular (h4 per base-4 digit, kernels/h3sycl.cpp:433-459): for the four values x0..x3 differing in one digit,
-// t = (x0 + x1) + (x2 + x3) (the association of the reference's cross-lane butterfly, h3sycl.cpp:444-453) and
-// y_a = t - 2 x_(3-a); digits d = 1, 4, 16 inside the lane, d = 64 (G = 256) across the quad of lanes holding the
-// group's four segments: two butterfly adds and the quad mirror (lane a reads lane 3 - a)
-template <int G> __device__ __forceinline__ void regular_seg(float (&v)[kSeg], int lane) {
-    if constexpr (G > 1) reg_digit<1>(v);
-    if constexpr (G > 4) reg_digit<4>(v);
-    if constexpr (G > 16) reg_digit<16>(v);
-    if constexpr (G > kSeg) {
+// the digit of stride 4 with V = 8: x0, x1 at e and e + 4 of an even lane, x2, x3 at e and e + 4 of the odd lane
+// beside it. Each lane forms its own pair sum and its partner's from the partner's values (the same additions, so
+// the same bits), t = own + other (equal to (x0 + x1) + (x2 + x3) in both lanes), and the mirror value x_(3-a)
+// is the partner's value at the other half of the chunk.
+__device__ __forceinline__ void reg_mixed(float (&v)[8]) {
+    float p[8];
 #pragma unroll
-        for (int e = 0; e < kSeg; ++e) {
-            const float p = v[e] + xl<1>(v[e]);                  // x0 + x1 (lanes 0, 1), x2 + x3 (lanes 2, 3)
-            const float t = p + xl<2>(p);
-            const float m = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[e]), 0x1B, 0xF, 0xF, true));   // quad_perm [3,2,1,0]
-            v[e] = t - 2.0f * m;
-        }
+    for (int e = 0; e < 8; ++e) p[e] = lane_xor<1>(v[e]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float t = (v[r] + v[r + 4]) + (p[r] + p[r + 4]);
+        v[r] = t - 2.0f * p[r + 4];
+        v[r + 4] = t - 2.0f * p[r];
     }
 }
-// the rotation: for a group size fixed at compile time (GF), a straight-line sequence of stages; otherwise one
-// switch on the runtime size (more registers: the cases' allocations add up)
-template <int ROT, int GF> __device__ __forceinline__ void rotate_seg(float (&v)[kSeg], int lane, int G) {
-    if constexpr (GF != 0) {
-        if constexpr (ROT == H3S_ROT_SYLVESTER) sylvester_seg<GF>(v, lane);
-        else regular_seg<GF>(v, lane);
-    } else if constexpr (ROT == H3S_ROT_SYLVESTER) {
-        switch (G) {
-            case 2: sylvester_seg<2>(v, lane); break;
-            case 4: sylvester_seg<4>(v, lane); break;
-            case 8: sylvester_seg<8>(v, lane); break;
-            case 16: sylvester_seg<16>(v, lane); break;
-            case 32: sylvester_seg<32>(v, lane); break;
-            case 64: sylvester_seg<64>(v, lane); break;
-            case 128: sylvester_seg<128>(v, lane); break;
-            case 256: sylvester_seg<256>(v, lane); break;
-            default: sylvester_seg<512>(v, lane); break;
-        }
+// the digit whose four values sit in lanes S apart (a = (lane / S) % 4): the own pair x_a + x_(a^1), the other pair
+// from the lanes 2S away, and the mirror x_(3-a) from the lane 3S away
+template <int V, int S> __device__ __forceinline__ void reg_x(float (&v)[V]) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+        const float pv = v[e] + lane_xor<S>(v[e]);
+        const float t = pv + lane_xor<2 * S>(pv);
+        v[e] = t - 2.0f * lane_xor<3 * S>(v[e]);
+    }
+}
+template <int V> __device__ __forceinline__ void regular(float (&v)[V], int G) {
+    if (G > 1) reg_in<V, 1>(v);
+    if constexpr (V == 8) {
+        if (G > 4) reg_mixed(v);
+        if (G > 16) reg_x<8, 2>(v);
+        if (G > 64) reg_x<8, 8>(v);
     } else {
-        switch (G) {
-            case 4: regular_seg<4>(v, lane); break;
-            case 16: regular_seg<16>(v, lane); break;
-            case 64: regular_seg<64>(v, lane); break;
-            default: regular_seg<256>(v, lane); break;
-        }
+        if (G > 4) reg_x<4, 1>(v);
+        if (G > 16) reg_x<4, 4>(v);
+        if (G > 64) reg_x<4, 16>(v);
     }
 }
-
-// LDS: the row as 16-byte units with a 16-byte pad after each segment's units (segment reads: lanes 144 or 272 bytes
-// apart, no bank conflicts); codes: 64 bytes a segment plus 16 of pad
-template <int EB> struct Lds {
-    static constexpr int UPS = kSeg * EB / 16;
-    __device__ static __forceinline__ int unit(int u) { return (u + u / UPS) * 16; }
-    static constexpr int bytes_for(int64_t C) { return (int) ((C * EB / 16 + C / kSeg) * 16); }
-};
 
 struct QuantArgs {
     const void* x;
     int64_t M, C;
+    bool norm;               // false: quantize x itself (h3s_int8_linear)
     const float* w;          // NULL: 1
     float eps;
     const int32_t* rows;     // NULL: table row 0
-    const void* scale;
+    const void* scale;       // scale and shift: both or neither
     const void* shift;
+    int tab_dt;
+    int h_dt;
+    int rot;                 // H3S_ROT_NONE, H3S_ROT_REGULAR or H3S_ROT_SYLVESTER
     int group;
     float cg;                // fl(1 / sqrt(group))
     int8_t* q;
     float* s;
-    int lds_bytes;           // per wave
 };
 
-template <int XDT, int CPL, int ROT, int HDT, int TAB, bool NORM, int GF = 0>
-__global__ __launch_bounds__(256) void quant_kernel(QuantArgs A) {
+// ROTATED: a rotation runs (its kind, A.rot, and group size at run time); F: the side inputs (ROW_W, ROW_TAB,
+// ROW_TAB32 or ROW_DYN, as in rowcore.h)
+template <int XDT, int CPL, bool ROTATED, int F>
+__global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift) {
     constexpr int V = Vec<XDT>::V;
-    constexpr int ST = NORM ? HDT : XDT;                     // the type of the values that are quantized
-    constexpr int EB = ST == H3S_F32 ? 4 : 2;
-    extern __shared__ __attribute__((aligned(16))) char lds_all[];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int64_t row = (int64_t) blockIdx.x * (blockDim.x >> 6) + wv;
-    if (row >= A.M) return;
-    const int64_t C = A.C, nch = C / V;
+    constexpr bool DYN = F & ROW_DYN;
+    constexpr bool TW = DYN || (F & ROW_TAB32);
+    __shared__ float red[2][8];
+    const bool has_w = DYN ? A.w != nullptr : (F & ROW_W) != 0;
+    const bool has_tab = DYN ? A.scale != nullptr : (F & ROW_TAB) != 0;
+    const int tab_dt = (!DYN && (F & ROW_TAB32)) ? H3S_F32 : A.tab_dt;
+    const RowPos P = row_pos(lshift, A.M);
+    const int L = 1 << lshift, lane = (int) (threadIdx.x & 63);
+    const int64_t row = P.row, C = A.C, nch = C / V;
+    int64_t cc[CPL];
+    bool ok[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int64_t c = P.t + (int64_t) L * j;
+        ok[j] = c < nch;
+        cc[j] = ok[j] ? c : nch - 1;
+    }
 
-    // ---- the row, chunk c = lane + 64 j ----
-    uint4 raw[CPL];
+    // ---- every load of the row, in flight together ----
+    const int64_t tr = has_tab && A.rows ? (int64_t) A.rows[row] * C : 0;
+    uint4 xr[CPL];
     {
-        // every lane loads (a chunk past the row's end reads the last one again and is never used): no branch
-        // between the loads, so all of them are in flight together
-        const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * (16 / V));
+        const uint4* xp = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * (16 / V));
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int64_t c = lane + (int64_t) kWave * j;
-            raw[j] = p[c < nch ? c : nch - 1];
-        }
+        for (int j = 0; j < CPL; ++j) xr[j] = xp[cc[j]];
     }
-    float v[CPL][V];
-    // packed words of the values in ST when they go to LDS as 16-bit (EB == 2)
-    uint32_t pk[CPL][V / 2];
+    Raw<V, true> wr[CPL];
+    Raw<V, TW> sr[CPL], hr[CPL];
+    if (has_w)
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(raw[j], v[j]);
-    if constexpr (!NORM && EB == 2) {
+        for (int j = 0; j < CPL; ++j) fetch(wr[j], A.w, H3S_F32, cc[j] * V);
+    if (has_tab) {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            pk[j][0] = raw[j].x; pk[j][1] = raw[j].y;
-            if constexpr (V == 8) { pk[j][2] = raw[j].z; pk[j][3] = raw[j].w; }
+            fetch(sr[j], A.scale, tab_dt, tr + cc[j] * V);
+            fetch(hr[j], A.shift, tab_dt, tr + cc[j] * V);
         }
     }
 
-    if constexpr (NORM) {
+    float v[CPL][V];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(xr[j], v[j]);
+
+    // ---- rms_norm_mod into h's type ----
+    if (A.norm) {
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < CPL; ++j)
-            if (lane + (int64_t) kWave * j < nch)
+            if (ok[j])
 #pragma unroll
                 for (int e = 0; e < V; ++e) ss = __builtin_fmaf(v[j][e], v[j][e], ss);
-        const float inv = inv_root(wave_sum<kWave>(ss), (float) C, A.eps);
-        const int64_t tr = A.rows ? (int64_t) A.rows[row] * C : 0;
+        const float inv = inv_root(row_sum(ss, red[0], P.W), (float) C, A.eps);
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            const int64_t i = (lane + (int64_t) kWave * j) * V;
-            if (i >= C) continue;
-            float* o = v[j];
-            float wv_[V];
-            if (A.w) load_f32x(A.w + i, wv_, V);
-            else
+            float f[V], g[V];
+            if (has_w) {
+                decode(wr[j], H3S_F32, f);
 #pragma unroll
-                for (int e = 0; e < V; ++e) wv_[e] = 1.0f;
+                for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * inv * f[e];
+            } else {
 #pragma unroll
-            for (int e = 0; e < V; ++e) o[e] = o[e] * inv * wv_[e];
-            if constexpr (TAB != TAB_NONE) {
-                float sc[V], sh[V];
-                if constexpr (TAB == TAB_BF16) {
-                    load_tab<H3S_BF16>(A.scale, tr + i, sc, V);
-                    load_tab<H3S_BF16>(A.shift, tr + i, sh, V);
-                } else {
-                    load_f32x((const float*) A.scale + tr + i, sc, V);
-                    load_f32x((const float*) A.shift + tr + i, sh, V);
-                }
-#pragma unroll
-                for (int e = 0; e < V; ++e) o[e] = o[e] * (1.0f + sc[e]) + sh[e];
+                for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * inv;
             }
-            // round to h's type, two values a conversion
-            if constexpr (HDT != H3S_F32) {
+            if (has_tab) {
+                decode(sr[j], tab_dt, f);
+                decode(hr[j], tab_dt, g);
+#pragma unroll
+                for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * (1.0f + f[e]) + g[e];
+            }
+            if (A.h_dt == H3S_BF16) {
 #pragma unroll
                 for (int e = 0; e < V; e += 2) {
-                    const uint32_t p2 = HDT == H3S_BF16 ? pack_bf16(o[e], o[e + 1]) : pack_f16(o[e], o[e + 1]);
-                    pk[j][e / 2] = p2;
-                    if constexpr (ROT == H3S_ROT_NONE) {
-                        if constexpr (HDT == H3S_BF16) { o[e] = bf16_lo(p2); o[e + 1] = bf16_hi(p2); }
-                        else { o[e] = f16_lo(p2); o[e + 1] = f16_hi(p2); }
-                    }
+                    const uint32_t p = pack_bf16(v[j][e], v[j][e + 1]);
+                    v[j][e] = bf16_lo(p);
+                    v[j][e + 1] = bf16_hi(p);
+                }
+            } else if (A.h_dt == H3S_F16) {
+#pragma unroll
+                for (int e = 0; e < V; e += 2) {
+                    const uint32_t p = pack_f16(v[j][e], v[j][e + 1]);
+                    v[j][e] = f16_lo(p);
+                    v[j][e + 1] = f16_hi(p);
                 }
             }
         }
     }
 
+    // ---- the block rotation, then the row's absolute maximum ----
     float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        if constexpr (ROTATED) {
+            if (A.rot == H3S_ROT_SYLVESTER) sylvester<V>(v[j], lane, A.group);
+            else regular<V>(v[j], A.group);
+#pragma unroll
+            for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * A.cg;
+        }
+        if (ok[j])
+#pragma unroll
+            for (int e = 0; e < V; ++e) m = fmaxf(m, fabsf(v[j][e]));
+    }
+    m = row_max(m, red[1], P.W);
+    const float sc = fmaxf(m / 127.0f, 1e-30f), r = 1.0f / sc;
+    if (P.live && P.t == 0) A.s[row] = sc;
+
+    // ---- the codes, V bytes a chunk ----
     int8_t* qrow = A.q + row * C;
-    if constexpr (ROT == H3S_ROT_NONE) {
 #pragma unroll
-        for (int j = 0; j < CPL; ++j)
-            if (lane + (int64_t) kWave * j < nch)
-#pragma unroll
-                for (int e = 0; e < V; ++e) m = fmaxf(m, fabsf(v[j][e]));
-        m = wave_max<kWave>(m);
-        const float sc = fmaxf(m / 127.0f, 1e-30f), r = 1.0f / sc;
-        if (lane == 0) A.s[row] = sc;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int64_t c = lane + (int64_t) kWave * j;
-            if (c >= nch) continue;
-            const float* o = v[j];
-            if constexpr (V == 8)
-                *reinterpret_cast<uint2*>(qrow + c * 8) =
-                    make_uint2(bytes4(code_of(o[0], sc, r), code_of(o[1], sc, r), code_of(o[2], sc, r), code_of(o[3], sc, r)),
-                               bytes4(code_of(o[4], sc, r), code_of(o[5], sc, r), code_of(o[6], sc, r), code_of(o[7], sc, r)));
-            else
-                *reinterpret_cast<uint32_t*>(qrow + c * 4) =
-                    bytes4(code_of(o[0], sc, r), code_of(o[1], sc, r), code_of(o[2], sc, r), code_of(o[3], sc, r));
-        }
-    } else {
-        using L = Lds<EB>;
-        char* lds = lds_all + wv * A.lds_bytes;
-        // ---- chunk layout -> LDS, in ST's bits ----
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int64_t c = lane + (int64_t) kWave * j;
-            if (c >= nch) continue;
-            const int64_t e0 = c * V;
-            if constexpr (EB == 2) {
-                char* a = lds + L::unit((int) (e0 / 8)) + (int) (e0 % 8) * 2;
-                if constexpr (V == 8) *reinterpret_cast<uint4*>(a) = make_uint4(pk[j][0], pk[j][1], pk[j][2], pk[j][3]);
-                else *reinterpret_cast<uint2*>(a) = make_uint2(pk[j][0], pk[j][1]);
-            } else {
-#pragma unroll
-                for (int k = 0; k < V; k += 4)
-                    *reinterpret_cast<float4*>(lds + L::unit((int) ((e0 + k) / 4))) = make_float4(v[j][k], v[j][k + 1], v[j][k + 2], v[j][k + 3]);
-            }
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        // ---- segments: lane l owns features 64 (it 64 + l) .. + 63, it < SI ----
-        const int nseg = (int) (C / kSeg);
-        constexpr int SI = (CPL * V + kSeg - 1) / kSeg;
-        static_assert(SI <= 2, "at most two segment passes");
-        // a lane past the row's segments works on a copy of the last one (its results are not used); groups never
-        // mix such lanes with real ones (a group's segments are all in the row or all past it)
-        auto load_rotate = [&](float (&y)[kSeg], int it) {
-            const int sg = it * kWave + lane, sgc = sg < nseg ? sg : nseg - 1;
-            if constexpr (EB == 2) {
-                uint4 raw_[kSeg / 8];
-#pragma unroll
-                for (int u = 0; u < kSeg / 8; ++u) raw_[u] = *reinterpret_cast<const uint4*>(lds + L::unit(sgc * (kSeg / 8) + u));
-#pragma unroll
-                for (int u = 0; u < kSeg / 8; ++u) Vec<ST>::unpack(raw_[u], y + 8 * u);
-            } else {
-#pragma unroll
-                for (int u = 0; u < kSeg / 4; ++u) {
-                    const float4 b = *reinterpret_cast<const float4*>(lds + L::unit(sgc * (kSeg / 4) + u));
-                    y[4 * u] = b.x; y[4 * u + 1] = b.y; y[4 * u + 2] = b.z; y[4 * u + 3] = b.w;
-                }
-            }
-            rotate_seg<ROT, GF>(y, lane, A.group);
-            float mm = 0.0f;
-#pragma unroll
-            for (int e = 0; e < kSeg; ++e) {
-                y[e] = y[e] * A.cg;
-                mm = fmaxf(mm, fabsf(y[e]));
-            }
-            if (sg < nseg) m = fmaxf(m, mm);
-        };
-        float y0[kSeg], y1[SI > 1 ? kSeg : 1];
-        load_rotate(y0, 0);
-        if constexpr (SI > 1) load_rotate(y1, 1);
-        m = wave_max<kWave>(m);
-        const float sc = fmaxf(m / 127.0f, 1e-30f), r = 1.0f / sc;
-        if (lane == 0) A.s[row] = sc;
-        asm volatile("" ::: "memory");
-        // ---- codes: segments -> LDS -> 8-byte pieces of the chunk layout -> global ----
-        auto put_codes = [&](const float (&y)[kSeg], int it) {
-            const int sg = it * kWave + lane;
-            if (sg >= nseg) return;
-#pragma unroll
-            for (int u = 0; u < kSeg / 16; ++u) {
-                const float* yy = y + 16 * u;
-                *reinterpret_cast<uint4*>(lds + sg * 80 + 16 * u) =
-                    make_uint4(bytes4(code_of(yy[0], sc, r), code_of(yy[1], sc, r), code_of(yy[2], sc, r), code_of(yy[3], sc, r)),
-                               bytes4(code_of(yy[4], sc, r), code_of(yy[5], sc, r), code_of(yy[6], sc, r), code_of(yy[7], sc, r)),
-                               bytes4(code_of(yy[8], sc, r), code_of(yy[9], sc, r), code_of(yy[10], sc, r), code_of(yy[11], sc, r)),
-                               bytes4(code_of(yy[12], sc, r), code_of(yy[13], sc, r), code_of(yy[14], sc, r), code_of(yy[15], sc, r)));
-            }
-        };
-        put_codes(y0, 0);
-        if constexpr (SI > 1) put_codes(y1, 1);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        const int64_t npieces = C / 8;                       // piece p (features 8p .. 8p + 7) at 80 (p / 8) + 8 (p % 8)
-#pragma unroll
-        for (int k = 0; k < (CPL * V) / 8 + 1; ++k) {
-            const int64_t p = lane + (int64_t) kWave * k;
-            if (p < npieces) *reinterpret_cast<uint2*>(qrow + p * 8) = *reinterpret_cast<const uint2*>(lds + (p / 8) * 80 + (p % 8) * 8);
+    for (int j = 0; j < CPL; ++j) {
+        if (!(P.live && ok[j])) continue;
+        const float* o = v[j];
+        const uint32_t b0 = bytes4(code_of(o[0], sc, r), code_of(o[1], sc, r), code_of(o[2], sc, r), code_of(o[3], sc, r));
+        if constexpr (V == 8) {
+            const uint32_t b1 = bytes4(code_of(o[4], sc, r), code_of(o[5], sc, r), code_of(o[6], sc, r), code_of(o[7], sc, r));
+            st_nt(qrow + cc[j] * 8, make_uint2(b0, b1));
+        } else {
+            st_nt(qrow + cc[j] * 4, b0);
         }
     }
 }
 
-// Launches the kernel for one input type. Checks shapes it cannot take.
-template <int XDT>
-int quant_launch(Ctx* c, const char* fn, QuantArgs A, int rot, int hdt, int tab, bool norm) {
-    constexpr int V = Vec<XDT>::V;
-    const int64_t per_lane = (A.C / V + kWave - 1) / kWave;
-    const int cpl = per_lane <= 2 ? 2 : per_lane <= 8 ? 8 : per_lane <= 16 ? 16 : 0;
-    if (!cpl)
-        return fail(std::string(fn) + ": rows longer than 16 x 64 16-byte vectors (8192 16-bit or 4096 float32 features) are not supported");
-    const int st = norm ? hdt : XDT;
-    const int eb = st == H3S_F32 ? 4 : 2;
-    A.lds_bytes = rot == H3S_ROT_NONE ? 0 : (eb == 2 ? Lds<2>::bytes_for(A.C) : Lds<4>::bytes_for(A.C));
-    int wpb = 4;                                          // waves a block, within 64 KiB of LDS
-    while (wpb > 1 && (size_t) A.lds_bytes * wpb > 64 * 1024) wpb /= 2;
-    if ((size_t) A.lds_bytes * wpb > 64 * 1024) return fail(std::string(fn) + ": a rotated row of this length does not fit the LDS");
-    const unsigned grid = (unsigned) ((A.M + wpb - 1) / wpb);
-    const size_t shm = (size_t) A.lds_bytes * wpb;
-#define QK(CPL, ROT, HDT, TAB, NRM) quant_kernel<XDT, CPL, ROT, HDT, TAB, NRM><<<grid, 64 * wpb, shm, c->stream>>>(A)
-#define QF(CPL, ROT, TAB, G) quant_kernel<XDT, CPL, ROT, XDT, TAB, true, G><<<grid, 64 * wpb, shm, c->stream>>>(A)
-    // compile-time group sizes for the common cases: 16-bit x and h of the same type, CPL 8 or 16
-    if constexpr (XDT != H3S_F32) {
-        const bool syl = rot == H3S_ROT_SYLVESTER && (A.group == 64 || A.group == 128 || A.group == 256);
-        const bool reg = rot == H3S_ROT_REGULAR && A.group == 256;
-        if (norm && hdt == XDT && (cpl == 8 || cpl == 16) && (syl || reg)) {
-#define QFG(CPL, TAB)                                                              \
-    if (reg) QF(CPL, H3S_ROT_REGULAR, TAB, 256);                                   \
-    else if (A.group == 64) QF(CPL, H3S_ROT_SYLVESTER, TAB, 64);                   \
-    else if (A.group == 128) QF(CPL, H3S_ROT_SYLVESTER, TAB, 128);                 \
-    else QF(CPL, H3S_ROT_SYLVESTER, TAB, 256);
-#define QFT(CPL)                                          \
-    if (tab == TAB_BF16) { QFG(CPL, TAB_BF16) }           \
-    else if (tab == TAB_F32) { QFG(CPL, TAB_F32) }        \
-    else { QFG(CPL, TAB_NONE) }
-            if (cpl == 8) { QFT(8) }
-            else { QFT(16) }
-#undef QFT
-#undef QFG
-            return launched(fn);
-        }
-        if (!norm && reg && (cpl == 8 || cpl == 16)) {
-            if (cpl == 8) quant_kernel<XDT, 8, H3S_ROT_REGULAR, H3S_F32, TAB_NONE, false, 256><<<grid, 64 * wpb, shm, c->stream>>>(A);
-            else quant_kernel<XDT, 16, H3S_ROT_REGULAR, H3S_F32, TAB_NONE, false, 256><<<grid, 64 * wpb, shm, c->stream>>>(A);
-            return launched(fn);
-        }
-    }
-#define QT(CPL, ROT, HDT)                                          \
-    if (tab == TAB_BF16) QK(CPL, ROT, HDT, TAB_BF16, true);        \
-    else if (tab == TAB_F32) QK(CPL, ROT, HDT, TAB_F32, true);     \
-    else QK(CPL, ROT, HDT, TAB_NONE, true)
-#define QH(CPL, ROT)                                       \
-    if (hdt == H3S_BF16) { QT(CPL, ROT, H3S_BF16); }       \
-    else if (hdt == H3S_F16) { QT(CPL, ROT, H3S_F16); }    \
-    else { QT(CPL, ROT, H3S_F32); }
-#define QR(CPL)                                                                                   \
-    if (norm) {                                                                                   \
-        if (rot == H3S_ROT_SYLVESTER) { QH(CPL, H3S_ROT_SYLVESTER) }                               \
-        else if (rot == H3S_ROT_REGULAR) { QH(CPL, H3S_ROT_REGULAR) }                              \
-        else { QH(CPL, H3S_ROT_NONE) }                                                             \
-    } else {                                                                                      \
-        if (rot == H3S_ROT_REGULAR) QK(CPL, H3S_ROT_REGULAR, H3S_F32, TAB_NONE, false);           \
-        else QK(CPL, H3S_ROT_NONE, H3S_F32, TAB_NONE, false);                                     \
-    }
-    if (cpl == 2) { QR(2) }
-    else if (cpl == 8) { QR(8) }
-    else { QR(16) }
-#undef QR
-#undef QH
-#undef QT
-#undef QF
-#undef QK
+// The side-input masks compiled exactly for 16-bit inputs: none (h3s_int8_linear's quantizer), the weight
+// (configs 1 and 4), the weight with 16-bit or float32 tables (config 5's front pass, the DiT's AdaLN). Every other
+// call shape runs the ROW_DYN instantiation.
+constexpr int kQuantNone = 0, kQuantW = ROW_W, kQuantWTab = ROW_W | ROW_TAB, kQuantWTab32 = ROW_W | ROW_TAB | ROW_TAB32;
+
+// Launches the kernel for one input type; the plan comes from row_plan.
+template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, RowPlan p) {
+    const RowLaunch R = row_launch(A.M, p);
+    int f = (A.w ? ROW_W : 0) | (A.scale ? ROW_TAB | (A.tab_dt == H3S_F32 ? ROW_TAB32 : 0) : 0);
+    if (XDT == H3S_F32 || !(f == kQuantNone || f == kQuantW || f == kQuantWTab || f == kQuantWTab32)) f = ROW_DYN;
+    const bool rotated = A.rot != H3S_ROT_NONE;
+#define H3_QUANT_F(CC, RR, FF) quant_kernel<XDT, CC, RR, FF><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift)
+#define H3_QUANT_R(CC, RR)                                                                           \
+    if constexpr (XDT != H3S_F32) {                                                                  \
+        if (f == kQuantNone) { H3_QUANT_F(CC, RR, kQuantNone); return launched(fn); }               \
+        if (f == kQuantW) { H3_QUANT_F(CC, RR, kQuantW); return launched(fn); }                     \
+        if (f == kQuantWTab) { H3_QUANT_F(CC, RR, kQuantWTab); return launched(fn); }               \
+        if (f == kQuantWTab32) { H3_QUANT_F(CC, RR, kQuantWTab32); return launched(fn); }           \
+    }                                                                                                \
+    H3_QUANT_F(CC, RR, ROW_DYN);                                                                     \
     return launched(fn);
+#define H3_QUANT_CPL(CC)                           \
+    if (p.cpl == CC) {                             \
+        if (rotated) { H3_QUANT_R(CC, true) }      \
+        else { H3_QUANT_R(CC, false) }             \
+    }
+    H3_QUANT_CPL(1)
+    H3_QUANT_CPL(2)
+    H3_QUANT_CPL(3)
+    H3_QUANT_CPL(4)
+#undef H3_QUANT_CPL
+#undef H3_QUANT_R
+#undef H3_QUANT_F
+    return fail(std::string(fn) + ": no kernel for this row length");
 }
 
 }  // namespace h3

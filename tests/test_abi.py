@@ -75,7 +75,7 @@ def test_arguments_are_checked_before_the_device(api):
     assert "aligned" in api.error()
     assert api.rms_norm_mod(None, p, 7, 4, 4096, p, 1e-6, None, None, None, p, 2) == -1
     assert "element type" in api.error()
-    assert api.rms_norm_mod(None, p, 2, 4, 16384, p, 1e-6, None, None, None, p, 2) == -1
+    assert api.rms_norm_mod(None, p, 2, 4, 16392, p, 1e-6, None, None, None, p, 2) == -1
     assert "not supported" in api.error()
     assert api.gate_add(None, p, 2, 4, 4096, p, 2, None, p) == -1
     assert "row table" in api.error()

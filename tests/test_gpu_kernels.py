@@ -57,8 +57,16 @@ def test_context_and_memory(dev):
 
 
 # ---- h3s_rms_norm_mod (kernels/h3sycl.cpp:766-810) ----
+# row lengths that reach every launch plan (lanes per row x chunks per lane) for 16-bit and float32 rows
+ROW_SHAPES = [(7, 4096), (33, 5376), (5, 64), (9, 520), (6, 1536), (4, 2040), (5, 2048), (3, 8192), (3, 8200), (2, 16384)]
+
+
+def too_long(C, x_dt):
+    return C // (16 // (4 if x_dt == o.F32 else 2)) > 2048
+
+
 @pytest.mark.parametrize("x_dt,out_dt", [(o.BF16, o.BF16), (o.BF16, o.F32), (o.F16, o.F16), (o.F32, o.F32), (o.F32, o.BF16)])
-@pytest.mark.parametrize("M,C", [(7, 4096), (33, 5376), (5, 64), (9, 520)])
+@pytest.mark.parametrize("M,C", ROW_SHAPES)
 @pytest.mark.parametrize("mod", [False, True])
 def test_rms_norm_mod(dev, x_dt, out_dt, M, C, mod):
     if C % (16 // (4 if x_dt == o.F32 else 2)):
@@ -72,8 +80,8 @@ def test_rms_norm_mod(dev, x_dt, out_dt, M, C, mod):
     xt = up(dev, x, DTS[x_dt], [M, C])
     out = new(dev, DTS[out_dt], [M, C])
     m = ops.Mod(up(dev, rows, "I32", [M]), up(dev, sc, "F32", [R, C]), up(dev, sh, "F32", [R, C])) if mod else None
-    if C // (16 // (4 if x_dt == o.F32 else 2)) > 16 * 64:
-        # rows are held in registers, at most 16 16-byte vectors per lane: longer ones are refused, with the reason
+    if too_long(C, x_dt):
+        # rows are held in registers, at most 2048 16-byte vectors a row: longer ones are refused, with the reason
         with pytest.raises(Error, match="not supported"):
             ops.rms_norm_mod(xt, up(dev, w, "F32", [C]), 1e-6, m, out)
         return
@@ -94,7 +102,8 @@ def test_rms_norm_in_place(dev):
 
 # ---- h3s_layer_norm (kernels/h3sycl.cpp:1248-1274) ----
 @pytest.mark.parametrize("affine", [False, True])
-@pytest.mark.parametrize("x_dt,out_dt,C", [(o.BF16, o.F32, 4096), (o.BF16, o.BF16, 1024), (o.F32, o.F32, 260)])
+@pytest.mark.parametrize("x_dt,out_dt,C", [(o.BF16, o.F32, 4096), (o.BF16, o.BF16, 1024), (o.F32, o.F32, 260), (o.F32, o.BF16, 4096),
+                                           (o.BF16, o.BF16, 16384), (o.F16, o.F32, 5376)])
 def test_layer_norm(dev, affine, x_dt, out_dt, C):
     M = 11
     x = o.to_dt(np.random.default_rng(7).standard_normal(M * C).astype(np.float32) * 3 + 1, x_dt)
@@ -185,7 +194,8 @@ def test_qk_rms_rope_in_a_qkv_buffer(dev):
 # ---- h3s_norm_quant: rms_norm_mod -> bf16 h -> quantizer (configs 1, 4, 5a) ----
 @pytest.mark.parametrize("rot,group", [(o.ROT_NONE, 0), (o.ROT_SYLVESTER, 128), (o.ROT_SYLVESTER, 16), (o.ROT_SYLVESTER, 512),
                                        (o.ROT_REGULAR, 256), (o.ROT_REGULAR, 64), (o.ROT_REGULAR, 16), (o.ROT_REGULAR, 4)])
-@pytest.mark.parametrize("x_dt,C", [(o.BF16, 4096), (o.BF16, 5376), (o.F32, 1024)])
+@pytest.mark.parametrize("x_dt,C", [(o.BF16, 4096), (o.BF16, 5376), (o.F32, 1024), (o.BF16, 1024), (o.BF16, 16384), (o.F32, 4096),
+                                    (o.F16, 2048)])
 def test_norm_quant(dev, rot, group, x_dt, C):
     if group and C % group:
         pytest.skip("group does not divide C")
@@ -245,8 +255,8 @@ def test_norm_quant_edge_rows(dev):
 @pytest.mark.parametrize("norm", [o.NORM_LAYER, o.NORM_RMS])
 @pytest.mark.parametrize("act", [o.ACT_GELU_TANH, o.ACT_SILU, o.ACT_NONE])
 @pytest.mark.parametrize("tab_dt", [o.BF16, o.F32])
-def test_norm_mod_act_gate(dev, norm, act, tab_dt):
-    M, C = 40, 4096
+@pytest.mark.parametrize("M,C", [(40, 4096), (9, 1024), (5, 16384)])
+def test_norm_mod_act_gate(dev, norm, act, tab_dt, M, C):
     x = inputs(30, M * C, o.BF16)
     res = inputs(31, M * C, o.BF16)
     tabs = [o.to_dt(0.5 * np.random.default_rng(32 + i).standard_normal(C).astype(np.float32), tab_dt) for i in range(3)]
@@ -262,6 +272,25 @@ def test_norm_mod_act_gate(dev, norm, act, tab_dt):
         assert_bits_equal(out.to_numpy(), want, "norm_mod_act_gate")
     else:
         assert_close_16(out.to_numpy(), want, o.BF16, "norm_mod_act_gate", max_frac=5e-3)
+
+
+def test_norm_mod_act_gate_float32_and_affine(dev):
+    """float32 rows, residual, tables and output, with an affine layer norm and per-token table rows."""
+    M, C, R = 13, 2048, 3
+    rng = np.random.default_rng(36)
+    x = (rng.standard_normal(M * C) * 2 + 0.5).astype(np.float32)
+    res = rng.standard_normal(M * C).astype(np.float32)
+    w, b = weight(37, C), (0.1 * rng.standard_normal(C)).astype(np.float32)
+    rows = (np.arange(M) % R).astype(np.int32)
+    tabs = [(0.5 * rng.standard_normal(R * C)).astype(np.float32) for _ in range(3)]
+    want = o.norm_mod_act_gate(x, o.F32, M, C, o.NORM_LAYER, w, b, 1e-5, rows, tabs[0], tabs[1], tabs[2], o.F32,
+                               o.ACT_NONE, res, o.F32, o.F32)
+    out = new(dev, "F32", [M, C])
+    tb = ops.Tables(scale=up(dev, tabs[0], "F32", [R, C]), shift=up(dev, tabs[1], "F32", [R, C]),
+                    gate=up(dev, tabs[2], "F32", [R, C]), rows=up(dev, rows, "I32", [M]))
+    ops.norm_mod_act_gate(up(dev, x, "F32", [M, C]), o.NORM_LAYER, up(dev, w, "F32", [C]), up(dev, b, "F32", [C]), 1e-5, tb,
+                          o.ACT_NONE, up(dev, res, "F32", [M, C]), out)
+    assert_bits_equal(out.to_numpy(), want, "norm_mod_act_gate f32")
 
 
 # ---- h3s_int8_linear and h3s_int8_gemm_dequant (kernels/h3sycl.cpp:404-652) ----

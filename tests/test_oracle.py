@@ -169,7 +169,8 @@ def test_gemm_dequant_brute_force(oracle):
 # ---- the canonical reduction ----
 def test_canon_sum_is_a_sum(oracle):
     rng = np.random.default_rng(5)
-    for n, V, L in [(4096, 8, 64), (5376, 8, 64), (100, 4, 64), (128, 8, 8), (17, 8, 64)]:
+    for n, V, L in [(4096, 8, 64), (5376, 8, 64), (100, 4, 64), (128, 8, 8), (17, 8, 64), (4096, 8, 256), (5376, 8, 256),
+                    (4096, 4, 256), (16384, 8, 512), (300, 1, 128)]:
         x = rng.standard_normal(n).astype(np.float32)
         exact = math.fsum(float(v) for v in x)
         got = oracle.canon_sum(x, V, L, oracle.SUM)
@@ -181,6 +182,19 @@ def test_canon_sum_is_a_sum(oracle):
     x = np.array([1e8, 1.0, -1e8, 1.0], dtype=np.float32)
     # lane 0: 1e8 + -1e8 = 0; lane 1: 1 + 1 = 2; total 2 (a sequential sum would give 1)
     assert oracle.canon_sum(x, 1, 2, oracle.SUM) == 2.0
+    # beyond one wavefront the 64-lane groups are summed first: lane 0 (1e8) and lane 1 (1) meet inside group 0,
+    # where 1e8 + 1 rounds to 1e8, and -1e8 + 1 in group 1 likewise, so the total is 0; a plain 128-lane butterfly
+    # would pair lane 0 with lane 64 first and give 2
+    x = np.zeros(128, dtype=np.float32)
+    x[0], x[1], x[64], x[65] = 1e8, 1.0, -1e8, 1.0
+    assert oracle.canon_sum(x, 1, 128, oracle.SUM) == 0.0
+    assert oracle.canon_sum(x, 1, 64, oracle.SUM) == 2.0
+
+
+def test_row_lanes(oracle):
+    # 64 lanes below 256 chunks of 16 bytes, 256 up to 1024 chunks, 512 up to 2048
+    assert [oracle.row_lanes(n, 8) for n in (8, 2040, 2048, 4096, 5376, 8192, 8200, 16384)] == [64, 64, 256, 256, 256, 256, 512, 512]
+    assert [oracle.row_lanes(n, 4) for n in (1020, 1024, 4096, 4100, 8192)] == [64, 256, 256, 512, 512]
 
 
 # ---- the norms: kernels/h3sycl.cpp:766-810, 1248-1274 ----
