@@ -29,6 +29,7 @@ struct Ctx {
     hipStream_t copy_stream = nullptr;     // h3s_upload, made on first use
     std::mutex copy_mu;
     std::string name;
+    int cus = 256;                         // compute units of the device (persistent grids are sized by them)
     bool poison = false;                   // H3S_POISON: fresh buffers filled with 0xff bytes
     // the allocation book (kernels/h3sycl.cpp:149-151): allocations and scratch counted against one cap
     std::mutex mem_mu;

@@ -7,16 +7,16 @@
 
 namespace h3 {
 
-template <int XDT> int quant_launch(Ctx*, const char*, const QuantArgs&, RowPlan);
-extern template int quant_launch<H3S_BF16>(Ctx*, const char*, const QuantArgs&, RowPlan);
-extern template int quant_launch<H3S_F16>(Ctx*, const char*, const QuantArgs&, RowPlan);
-extern template int quant_launch<H3S_F32>(Ctx*, const char*, const QuantArgs&, RowPlan);
+template <int XDT> int quant_launch(Ctx*, const char*, const QuantArgs&, bool, RowPlan);
+extern template int quant_launch<H3S_BF16>(Ctx*, const char*, const QuantArgs&, bool, RowPlan);
+extern template int quant_launch<H3S_F16>(Ctx*, const char*, const QuantArgs&, bool, RowPlan);
+extern template int quant_launch<H3S_F32>(Ctx*, const char*, const QuantArgs&, bool, RowPlan);
 
-static int dispatch(Ctx* c, const char* fn, int x_dt, const QuantArgs& A, RowPlan p) {
+static int dispatch(Ctx* c, const char* fn, int x_dt, const QuantArgs& A, bool norm, RowPlan p) {
     switch (x_dt) {
-        case H3S_BF16: return quant_launch<H3S_BF16>(c, fn, A, p);
-        case H3S_F16: return quant_launch<H3S_F16>(c, fn, A, p);
-        default: return quant_launch<H3S_F32>(c, fn, A, p);
+        case H3S_BF16: return quant_launch<H3S_BF16>(c, fn, A, norm, p);
+        case H3S_F16: return quant_launch<H3S_F16>(c, fn, A, norm, p);
+        default: return quant_launch<H3S_F32>(c, fn, A, norm, p);
     }
 }
 
@@ -30,9 +30,9 @@ int launch_quantize(Ctx* c, const void* x, int x_dt, int64_t M, int64_t K, int g
     if (K % V != 0) return fail(std::string(fn) + ": K must be whole 16-byte vectors");
     const RowPlan p = row_plan(K / V);
     if (!p.L) return fail(std::string(fn) + too_long);
-    const QuantArgs A{x, M, K, false, nullptr, 0.0f, nullptr, nullptr, nullptr, H3S_F32, H3S_F32,
+    const QuantArgs A{x, M, K, nullptr, 0.0f, nullptr, nullptr, nullptr, H3S_F32, H3S_F32,
                       group > 0 ? H3S_ROT_REGULAR : H3S_ROT_NONE, group, group > 0 ? inv_sqrt_group(group) : 1.0f, q, s};
-    return dispatch(c, fn, x_dt, A, p);
+    return dispatch(c, fn, x_dt, A, false, p);
 }
 
 }  // namespace h3
@@ -64,7 +64,7 @@ H3S_EXPORT int h3s_norm_quant(void* ctx, const void* x, int x_dt, int64_t M, int
     if (!p.L) return fail(std::string(fn) + too_long);
     Ctx* c = ctx_of(ctx, fn);
     if (!c) return -1;
-    const QuantArgs A{x, M, C, true, weight, eps, rows, mod ? scale : nullptr, mod ? shift : nullptr, tab_dt, h_dt, rot,
+    const QuantArgs A{x, M, C, weight, eps, rows, mod ? scale : nullptr, mod ? shift : nullptr, tab_dt, h_dt, rot,
                       rot != H3S_ROT_NONE ? group : 0, rot != H3S_ROT_NONE ? inv_sqrt_group(group) : 1.0f, q, s};
-    return dispatch(c, fn, x_dt, A, p);
+    return dispatch(c, fn, x_dt, A, true, p);
 } catch (const std::exception& e) { return fail(e.what()); }

@@ -66,12 +66,46 @@ template <int V, int H> __device__ __forceinline__ void syl_in(float (&v)[V]) {
             v[e + H] = a - b;
         }
 }
-// the pair S lanes apart: the lower lane keeps a + b, the upper a - b, both as fma(+-1, own, partner), which is
-// exactly that sum or difference
+// The stages across lanes keep each lane's values up to a sign fixed by the lane: at the stage S lanes apart the
+// lower lane forms own + partner and the upper lane own - partner, which is the negation of the a - b it owes.
+// Both partners carry the same sign from the earlier stages (they differ only in lane bit S), and rounding to
+// nearest is symmetric, so every value stays exactly +-(the value of the plain butterfly); the sign is
+// (-1)^popcount(lane & (G/V - 1)), folded into the final multiply by fl(1/sqrt(G)). One fused multiply-add with the
+// partner's value taken straight from a neighbouring lane (own + partner * (+-1)) per value and stage.
+// For partners 1, 2 or 8 lanes away the partner's value comes through the DPP operand of v_fmac_f32 itself (one
+// instruction a value); s_nop 1 gives the two wait states a DPP read needs after the VALU write of the previous stage.
+#define H3_FMAC_DPP8(CTRL)                                                                                      \
+    asm volatile("s_nop 1\n"                                                                                    \
+                 "v_fmac_f32_dpp %0, %8, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                             \
+                 "v_fmac_f32_dpp %1, %9, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                             \
+                 "v_fmac_f32_dpp %2, %10, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                            \
+                 "v_fmac_f32_dpp %3, %11, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                            \
+                 "v_fmac_f32_dpp %4, %12, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                            \
+                 "v_fmac_f32_dpp %5, %13, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                            \
+                 "v_fmac_f32_dpp %6, %14, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                            \
+                 "v_fmac_f32_dpp %7, %15, %16 " CTRL " row_mask:0xf bank_mask:0xf"                               \
+                 : "=v"(o[0]), "=v"(o[1]), "=v"(o[2]), "=v"(o[3]), "=v"(o[4]), "=v"(o[5]), "=v"(o[6]), "=v"(o[7]) \
+                 : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]), "v"(sg), \
+                   "0"(v[0]), "1"(v[1]), "2"(v[2]), "3"(v[3]), "4"(v[4]), "5"(v[5]), "6"(v[6]), "7"(v[7]))
 template <int V, int S> __device__ __forceinline__ void syl_x(float (&v)[V], int lane) {
     const float sg = (lane & S) ? -1.0f : 1.0f;
+    if constexpr (V == 8 && (S == 1 || S == 2 || S == 8)) {
+        float o[8];
+        if constexpr (S == 1) H3_FMAC_DPP8("quad_perm:[1,0,3,2]");
+        else if constexpr (S == 2) H3_FMAC_DPP8("quad_perm:[2,3,0,1]");
+        else H3_FMAC_DPP8("row_ror:8");
 #pragma unroll
-    for (int e = 0; e < V; ++e) v[e] = __builtin_fmaf(sg, v[e], lane_xor<S>(v[e]));
+        for (int e = 0; e < 8; ++e) v[e] = o[e];
+    } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[e] = __builtin_fmaf(lane_xor<S>(v[e]), sg, v[e]);
+    }
+}
+#undef H3_FMAC_DPP8
+// the sign the cross-lane stages leave on this lane's values
+template <int V> __device__ __forceinline__ float syl_sign(int lane, int G) {
+    const int span = G / V;                               // lanes of a group (1 when the group is inside a chunk)
+    return span > 1 && (__builtin_popcount((unsigned) (lane & (span - 1))) & 1) ? -1.0f : 1.0f;
 }
 template <int V> __device__ __forceinline__ void sylvester(float (&v)[V], int lane, int G) {
     if (G > 1) syl_in<V, 1>(v);
@@ -139,7 +173,6 @@ template <int V> __device__ __forceinline__ void regular(float (&v)[V], int G) {
 struct QuantArgs {
     const void* x;
     int64_t M, C;
-    bool norm;               // false: quantize x itself (h3s_int8_linear)
     const float* w;          // NULL: 1
     float eps;
     const int32_t* rows;     // NULL: table row 0
@@ -155,144 +188,187 @@ struct QuantArgs {
 };
 
 // ROTATED: a rotation runs (its kind, A.rot, and group size at run time); F: the side inputs (ROW_W, ROW_TAB,
-// ROW_TAB32 or ROW_DYN, as in rowcore.h)
+// ROW_TAB32 or ROW_DYN, as in rowcore.h), or ROW_RAW: no norm, x itself is quantized.
+//
+// Persistent: a unit (one block for rows of 256 or 512 lanes, one wavefront for 64-lane rows) quantizes the rows
+// [unit * rpu, (unit + 1) * rpu). A lane works on the same chunks of every row, so the weight and the table row
+// are decoded into registers once (the table row again only when rows[] changes), and the next row's x is in
+// flight while this row is computed.
 template <int XDT, int CPL, bool ROTATED, int F>
-__global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift) {
+__global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int64_t rpu) {
     constexpr int V = Vec<XDT>::V;
     constexpr bool DYN = F & ROW_DYN;
     constexpr bool TW = DYN || (F & ROW_TAB32);
+    constexpr bool NORM = !(F & ROW_RAW);
     __shared__ float red[2][8];
     const bool has_w = DYN ? A.w != nullptr : (F & ROW_W) != 0;
     const bool has_tab = DYN ? A.scale != nullptr : (F & ROW_TAB) != 0;
     const int tab_dt = (!DYN && (F & ROW_TAB32)) ? H3S_F32 : A.tab_dt;
-    const RowPos P = row_pos(lshift, A.M);
-    const int L = 1 << lshift, lane = (int) (threadIdx.x & 63);
-    const int64_t row = P.row, C = A.C, nch = C / V;
+    const int L = 1 << lshift, W = L >> 6, lane = (int) (threadIdx.x & 63);
+    const int t = (int) (threadIdx.x & (L - 1));
+    const int64_t unit = L >= 256 ? (int64_t) blockIdx.x : (int64_t) blockIdx.x * (256 >> lshift) + (threadIdx.x >> lshift);
+    const int64_t C = A.C, nch = C / V, r0 = unit * rpu, r1 = r0 + rpu < A.M ? r0 + rpu : A.M;
+    if (L < 256 && r0 >= A.M) return;    // a 64-lane unit past the rows (no barriers on 64-lane rows)
     int64_t cc[CPL];
     bool ok[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int64_t c = P.t + (int64_t) L * j;
+        const int64_t c = t + (int64_t) L * j;
         ok[j] = c < nch;
         cc[j] = ok[j] ? c : nch - 1;
     }
-
-    // ---- every load of the row, in flight together ----
-    const int64_t tr = has_tab && A.rows ? (int64_t) A.rows[row] * C : 0;
-    uint4 xr[CPL];
-    {
+    auto load_row = [&](uint4 (&xr)[CPL], int64_t row) {
         const uint4* xp = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * (16 / V));
 #pragma unroll
         for (int j = 0; j < CPL; ++j) xr[j] = xp[cc[j]];
-    }
-    Raw<V, true> wr[CPL];
-    Raw<V, TW> sr[CPL], hr[CPL];
-    if (has_w)
+    };
+    uint4 xr[CPL];
+    if (r0 < r1) load_row(xr, r0);
+    int64_t tn = has_tab && A.rows && r0 < r1 ? A.rows[r0] : 0;
+
+    // ---- the weight and the table row, as floats: w, 1 + scale, shift ----
+    float wv[CPL][V], s1[CPL][V], sh[CPL][V];
+    if (has_w) {
+        Raw<V, true> wr[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) fetch(wr[j], A.w, H3S_F32, cc[j] * V);
-    if (has_tab) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) decode(wr[j], H3S_F32, wv[j]);
+    }
+    int64_t tcur = -1;
+    auto load_tables = [&](int64_t trow) {
+        Raw<V, TW> sr[CPL], hr[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            fetch(sr[j], A.scale, tab_dt, tr + cc[j] * V);
-            fetch(hr[j], A.shift, tab_dt, tr + cc[j] * V);
+            fetch(sr[j], A.scale, tab_dt, trow * C + cc[j] * V);
+            fetch(hr[j], A.shift, tab_dt, trow * C + cc[j] * V);
         }
-    }
-
-    float v[CPL][V];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(xr[j], v[j]);
-
-    // ---- rms_norm_mod into h's type ----
-    if (A.norm) {
-        float ss = 0.0f;
+        for (int j = 0; j < CPL; ++j) {
+            decode(sr[j], tab_dt, s1[j]);
+            decode(hr[j], tab_dt, sh[j]);
 #pragma unroll
-        for (int j = 0; j < CPL; ++j)
+            for (int e = 0; e < V; ++e) s1[j][e] = 1.0f + s1[j][e];
+        }
+    };
+
+    // the normalization of a rotated group, with the sign the Sylvester cross-lane stages leave on this lane
+    const float cgs = ROTATED && A.rot == H3S_ROT_SYLVESTER ? A.cg * syl_sign<V>(lane, A.group) : A.cg;
+    int slot = 0;   // consecutive reductions use alternate LDS slots
+    for (int64_t row = r0; row < r1; ++row) {
+        // the next row's x and table row index, in flight during this row
+        uint4 xn[CPL];
+        const bool more = row + 1 < r1;
+        if (more) load_row(xn, row + 1);
+        const int64_t tr = tn;
+        if (has_tab && A.rows && more) tn = A.rows[row + 1];
+        if (has_tab && tr != tcur) {
+            load_tables(tr);
+            tcur = tr;
+        }
+
+        float v[CPL][V];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(xr[j], v[j]);
+
+        // ---- rms_norm_mod into h's type ----
+        if constexpr (NORM) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+                if (ok[j])
+#pragma unroll
+                    for (int e = 0; e < V; ++e) ss = __builtin_fmaf(v[j][e], v[j][e], ss);
+            const float inv = inv_root(row_sum(ss, red[slot], W), (float) C, A.eps);
+            slot ^= 1;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                if (has_w) {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * inv * wv[j][e];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * inv;
+                }
+                if (has_tab) {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * s1[j][e] + sh[j][e];
+                }
+                if (A.h_dt == H3S_BF16) {
+#pragma unroll
+                    for (int e = 0; e < V; e += 2) {
+                        const uint32_t p = pack_bf16(v[j][e], v[j][e + 1]);
+                        v[j][e] = bf16_lo(p);
+                        v[j][e + 1] = bf16_hi(p);
+                    }
+                } else if (A.h_dt == H3S_F16) {
+#pragma unroll
+                    for (int e = 0; e < V; e += 2) {
+                        const uint32_t p = pack_f16(v[j][e], v[j][e + 1]);
+                        v[j][e] = f16_lo(p);
+                        v[j][e + 1] = f16_hi(p);
+                    }
+                }
+            }
+        }
+
+        // ---- the block rotation, then the row's absolute maximum ----
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            if constexpr (ROTATED) {
+                if (A.rot == H3S_ROT_SYLVESTER) sylvester<V>(v[j], lane, A.group);
+                else regular<V>(v[j], A.group);
+#pragma unroll
+                for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * cgs;
+            }
             if (ok[j])
 #pragma unroll
-                for (int e = 0; e < V; ++e) ss = __builtin_fmaf(v[j][e], v[j][e], ss);
-        const float inv = inv_root(row_sum(ss, red[0], P.W), (float) C, A.eps);
+                for (int e = 0; e < V; ++e) m = fmaxf(m, fabsf(v[j][e]));
+        }
+        m = row_max(m, red[slot], W);
+        slot ^= 1;
+        const float sc = fmaxf(m / 127.0f, 1e-30f), r = 1.0f / sc;
+        if (t == 0) A.s[row] = sc;
+
+        // ---- the codes, V bytes a chunk ----
+        int8_t* qrow = A.q + row * C;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            float f[V], g[V];
-            if (has_w) {
-                decode(wr[j], H3S_F32, f);
-#pragma unroll
-                for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * inv * f[e];
+            if (!ok[j]) continue;
+            const float* o = v[j];
+            const uint32_t b0 = bytes4(code_of(o[0], sc, r), code_of(o[1], sc, r), code_of(o[2], sc, r), code_of(o[3], sc, r));
+            if constexpr (V == 8) {
+                const uint32_t b1 = bytes4(code_of(o[4], sc, r), code_of(o[5], sc, r), code_of(o[6], sc, r), code_of(o[7], sc, r));
+                st_nt(qrow + cc[j] * 8, make_uint2(b0, b1));
             } else {
-#pragma unroll
-                for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * inv;
-            }
-            if (has_tab) {
-                decode(sr[j], tab_dt, f);
-                decode(hr[j], tab_dt, g);
-#pragma unroll
-                for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * (1.0f + f[e]) + g[e];
-            }
-            if (A.h_dt == H3S_BF16) {
-#pragma unroll
-                for (int e = 0; e < V; e += 2) {
-                    const uint32_t p = pack_bf16(v[j][e], v[j][e + 1]);
-                    v[j][e] = bf16_lo(p);
-                    v[j][e + 1] = bf16_hi(p);
-                }
-            } else if (A.h_dt == H3S_F16) {
-#pragma unroll
-                for (int e = 0; e < V; e += 2) {
-                    const uint32_t p = pack_f16(v[j][e], v[j][e + 1]);
-                    v[j][e] = f16_lo(p);
-                    v[j][e + 1] = f16_hi(p);
-                }
+                st_nt(qrow + cc[j] * 4, b0);
             }
         }
-    }
-
-    // ---- the block rotation, then the row's absolute maximum ----
-    float m = 0.0f;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        if constexpr (ROTATED) {
-            if (A.rot == H3S_ROT_SYLVESTER) sylvester<V>(v[j], lane, A.group);
-            else regular<V>(v[j], A.group);
-#pragma unroll
-            for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * A.cg;
-        }
-        if (ok[j])
-#pragma unroll
-            for (int e = 0; e < V; ++e) m = fmaxf(m, fabsf(v[j][e]));
-    }
-    m = row_max(m, red[1], P.W);
-    const float sc = fmaxf(m / 127.0f, 1e-30f), r = 1.0f / sc;
-    if (P.live && P.t == 0) A.s[row] = sc;
-
-    // ---- the codes, V bytes a chunk ----
-    int8_t* qrow = A.q + row * C;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        if (!(P.live && ok[j])) continue;
-        const float* o = v[j];
-        const uint32_t b0 = bytes4(code_of(o[0], sc, r), code_of(o[1], sc, r), code_of(o[2], sc, r), code_of(o[3], sc, r));
-        if constexpr (V == 8) {
-            const uint32_t b1 = bytes4(code_of(o[4], sc, r), code_of(o[5], sc, r), code_of(o[6], sc, r), code_of(o[7], sc, r));
-            st_nt(qrow + cc[j] * 8, make_uint2(b0, b1));
-        } else {
-            st_nt(qrow + cc[j] * 4, b0);
-        }
+        for (int j = 0; j < CPL; ++j) xr[j] = xn[j];
     }
 }
 
 // The side-input masks compiled exactly for 16-bit inputs: none (h3s_int8_linear's quantizer), the weight
 // (configs 1 and 4), the weight with 16-bit or float32 tables (config 5's front pass, the DiT's AdaLN). Every other
 // call shape runs the ROW_DYN instantiation.
-constexpr int kQuantNone = 0, kQuantW = ROW_W, kQuantWTab = ROW_W | ROW_TAB, kQuantWTab32 = ROW_W | ROW_TAB | ROW_TAB32;
+constexpr int kQuantNone = 0, kQuantW = ROW_W, kQuantWTab = ROW_W | ROW_TAB, kQuantWTab32 = ROW_W | ROW_TAB | ROW_TAB32,
+              kQuantRaw = ROW_RAW;
 
 // Launches the kernel for one input type; the plan comes from row_plan.
-template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, RowPlan p) {
-    const RowLaunch R = row_launch(A.M, p);
+template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, bool norm, RowPlan p) {
     int f = (A.w ? ROW_W : 0) | (A.scale ? ROW_TAB | (A.tab_dt == H3S_F32 ? ROW_TAB32 : 0) : 0);
     if (XDT == H3S_F32 || !(f == kQuantNone || f == kQuantW || f == kQuantWTab || f == kQuantWTab32)) f = ROW_DYN;
+    if (!norm) f = kQuantRaw;
     const bool rotated = A.rot != H3S_ROT_NONE;
-#define H3_QUANT_F(CC, RR, FF) quant_kernel<XDT, CC, RR, FF><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift)
+#define H3_QUANT_F(CC, RR, FF)                                                                      \
+    {                                                                                                \
+        const PersistentLaunch R = persistent_launch(c, (const void*) quant_kernel<XDT, CC, RR, FF>, A.M, p); \
+        quant_kernel<XDT, CC, RR, FF><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift, R.rpu);    \
+    }
 #define H3_QUANT_R(CC, RR)                                                                           \
+    if (f == kQuantRaw) { H3_QUANT_F(CC, RR, kQuantRaw); return launched(fn); }                     \
     if constexpr (XDT != H3S_F32) {                                                                  \
         if (f == kQuantNone) { H3_QUANT_F(CC, RR, kQuantNone); return launched(fn); }               \
         if (f == kQuantW) { H3_QUANT_F(CC, RR, kQuantW); return launched(fn); }                     \

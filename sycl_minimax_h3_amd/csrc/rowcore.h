@@ -13,6 +13,8 @@
 // adds the same two values in every lane (a + b = b + a exactly), so all lanes end with identical bits.
 #pragma once
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace h3 {
@@ -40,6 +42,29 @@ inline RowLaunch row_launch(int64_t M, RowPlan p) {
     r.grid = (unsigned) ((M + rpb - 1) / rpb);
     r.threads = (unsigned) (p.L >= 256 ? p.L : 256);
     r.lshift = __builtin_ctz((unsigned) p.L);
+    return r;
+}
+// blocks of a kernel that fit one compute unit at once, asked of the runtime once per kernel and block size
+int blocks_per_cu(const void* kernel, int threads);
+
+// A persistent launch: twice as many units (blocks of L >= 256 lanes, wavefronts of 64) as the device holds at
+// once, each taking rpu consecutive rows. The occupancy of each kernel is asked once.
+struct PersistentLaunch {
+    unsigned grid, threads;
+    int lshift;
+    int64_t rpu;                                         // rows a unit
+};
+inline PersistentLaunch persistent_launch(const Ctx* c, const void* kernel, int64_t M, RowPlan p) {
+    PersistentLaunch r;
+    r.threads = (unsigned) (p.L >= 256 ? p.L : 256);
+    r.lshift = __builtin_ctz((unsigned) p.L);
+    const int upb = p.L >= 256 ? 1 : 256 / p.L;          // units a block
+    const int per_cu = blocks_per_cu(kernel, (int) r.threads);
+    // twice what is resident: short jobs get one row a unit, long ones a steady stream
+    const int64_t units = std::min<int64_t>(M, (int64_t) c->cus * per_cu * upb * 2);
+    r.rpu = (M + units - 1) / units;
+    const int64_t used = (M + r.rpu - 1) / r.rpu;        // units that get rows
+    r.grid = (unsigned) ((used + upb - 1) / upb);
     return r;
 }
 // where this thread sits: its lane t in the row, and the row (clamped into [0, M); live = false past M)
@@ -134,6 +159,7 @@ enum : int {
     ROW_RES = 32,       // residual [M, C] (16-bit unless ROW_RES32)
     ROW_RES32 = 64,
     ROW_DYN = 128,
+    ROW_RAW = 256,      // the quantizer on x itself, with no norm (h3s_int8_linear); no side inputs
 };
 
 // ---- stores that bypass the caches' retention (the outputs are streamed, never read back by the kernel) ----

@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <map>
 
 #include "common.h"
 
@@ -20,6 +21,22 @@ Ctx* ctx_of(void* ctx, const char* fn) {
     return c;
 }
 
+int blocks_per_cu(const void* kernel, int threads) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, int>, int> known;
+    std::lock_guard<std::mutex> l(mu);
+    const auto key = std::make_pair(kernel, threads);
+    const auto it = known.find(key);
+    if (it != known.end()) return it->second;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n < 1) {
+        (void) hipGetLastError();
+        n = 1;
+    }
+    known.emplace(key, n);
+    return n;
+}
+
 int launched(const char* fn) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(std::string(fn) + ": kernel launch failed: " + hipGetErrorString(e));
@@ -32,6 +49,7 @@ static void init(Ctx& c) {
     if (hipGetDeviceProperties(&p, c.device) == hipSuccess) {
         c.name = p.name;
         if (c.name.empty() || c.name.find("gfx") == 0) c.name = std::string(p.gcnArchName);
+        if (p.multiProcessorCount > 0) c.cus = p.multiProcessorCount;
     }
     size_t free_b = 0, total = 0;
     (void) hipMemGetInfo(&free_b, &total);
