@@ -5,10 +5,13 @@
 A step is one launch of the headline kernel over the whole batch: the AdaLN chain (LayerNorm without affine, then
 x * (1 + scale) + shift, GELU-tanh, out = res + gate * y) on X, res [16896 x 4096] bf16, token grid T16 x H24 x W44.
 ``value`` is its achieved HBM bandwidth: algorithmic bytes (X and res read once, out written once) divided by the
-mean kernel time, timed with HIP events on the stream the kernel runs on, inputs already in HBM. The other fused
-kernels are timed the same way and reported under ``kernels``; the int8 GEMM also as int8 TOPS. ``cpu_baseline``
-times the CPU oracle (the C restatement of the reference arithmetic) on the same workload on this host.
-Prints one JSON line.
+mean kernel time. The library context wraps PyTorch's current stream (h3s_create), so the kernels run on that
+stream and the HIP events recorded on it (torch.cuda.Event) bracket exactly the timed launches; inputs are already
+in HBM. The other fused kernels are timed the same way and reported under ``kernels``; the int8 GEMM also as int8
+TOPS. ``roofline.traffic`` is the headline kernel's HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+runs summarized in profiles/hbm_traffic_pmc.md (each counter scaled by what it reads for a 1 GiB device copy).
+``cpu_baseline`` times the CPU oracle (the C restatement of the reference arithmetic) on the same workload on this
+host. Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -39,6 +42,22 @@ def bytes_cfg():
         "cfg5a_rmsnorm_mod_quant_47104": M4 * C * 2 + M4 * C + M4 * 4,
         "cfg5b_int8_gemm_silu_47104x16384": M4 * C + 16384 * C + M4 * 4 + 16384 * 4 + M4 * 16384 * 2,
     }
+
+
+def measured_traffic(key):
+    """HBM bytes per launch of kernel `key` from the committed counter summary, scaled by the copy calibration."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic:") and line.split()[1] == key:
+                    kv = dict(t.split("=") for t in line.split()[2:])
+                    cal_f = float(kv["copy_kib"]) / float(kv["copy_fetch_kib"])
+                    cal_w = float(kv["copy_kib"]) / float(kv["copy_write_kib"])
+                    return int(round((float(kv["fetch_kib"]) * cal_f + float(kv["write_kib"]) * cal_w) * 1024))
+    except (OSError, KeyError, ValueError):
+        return None
+    return None
 
 
 def rope_table(T, Hh, Ww, dims=(32, 48, 48), theta=10000.0):
@@ -187,7 +206,7 @@ def main() -> int:
         "config": {"workload": "AdaLN chain: LayerNorm(no affine) -> x*(1+scale)+shift -> GELU-tanh -> res + gate*y, "
                                "X,res [16896 x 4096] bf16 (grid T16xH24xW44)", "tokens": M2, "hidden": C},
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / PEAK_GBS, 4), "traffic": None},
+                     "frac": round(value / PEAK_GBS, 4), "traffic": measured_traffic("cfg2_ln_mod_gelu_gate_16896")},
         "kernels": per,
         "device": dev.name(),
     }
