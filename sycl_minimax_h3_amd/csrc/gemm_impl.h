@@ -1,0 +1,288 @@
+// gemm_impl.h - the int8 GEMM with the dequant epilogue on gfx950's i8 matrix cores (kernels/h3sycl.cpp:576-631,
+// engine/h3-core/src/reference.rs:72-76), used by h3s_int8_linear and h3s_int8_gemm_dequant (int8_gemm.hip).
+//
+//   acc[m, n] = sum_k A[m, k] W[n, k]                    exact int32 (|acc| <= K 128 128 = 2^26 at K = 4096)
+//   one weight scale:  v = acc * fl(s[m] * wscale[0])     (the row factor the reference folds first, h3sycl.cpp:576)
+//   N weight scales:   v = (acc * s[m]) * wscale[n]       (the post-op order of h3sycl.cpp:588-602)
+//   then + bias[n], then the activation, rounded once to out's type.
+//
+// Block: 256 threads (four wavefronts, 2 x 2), a 256 x 256 tile of out; each wavefront 128 x 128 as 4 x 4
+// v_mfma_i32_32x32x32_i8 accumulators (256 registers, one wavefront per SIMD). K advances 64 bytes a step
+// through a ring of four LDS stages (32 KiB each: the A and W slices of the step), filled by direct global->LDS
+// loads (global_load_lds_dwordx4) up to four steps ahead, so no registers hold operands in flight. Each step publishes the
+// next stage (one barrier), reads that stage's fragments into registers, and runs its own products beside those
+// reads; the buffer whose fragments are already in registers is refilled right after the barrier.
+//
+// LDS layout of an operand slice: 256 rows x 4 16-byte chunks; chunk c of row r at unit 4 r + (c ^ ((r / 4) % 4)).
+// A fragment read (32 consecutive rows, one chunk each) then touches 16 distinct 4-bank groups in each 16-lane
+// half. The direct loads write 64 consecutive units per instruction, so each lane fetches the (row, chunk) that its
+// unit holds: four lanes cover one row's 64 bytes.
+//
+// Tile order: the 8 XCDs take blocks round robin; blocks are renumbered so that each XCD works on a contiguous
+// run of tiles, grouped 8 tiles high so that the resident blocks of an XCD share A and W panels in its L2.
+// Epilogue: per 32 x 128 slice of a wavefront's region, dequant + activation in registers, the slice through LDS,
+// then 16-byte row-contiguous stores.
+#pragma once
+
+#include <type_traits>
+
+#include "rowcore.h"
+
+namespace h3 {
+
+constexpr int kGemmBM = 256, kGemmBN = 256, kGemmBK = 64, kGemmStages = 4;
+constexpr int kGemmStageBytes = (kGemmBM + kGemmBN) * kGemmBK;   // 32 KiB
+constexpr int kGemmLds = kGemmStages * kGemmStageBytes;          // 128 KiB
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+struct GemmArgs {
+    const int8_t* A;          // [M, K] quantized activations
+    const float* sA;          // [M] their scales
+    int64_t M, K;
+    const int8_t* W;          // [N, K]
+    int64_t N;
+    const float* ws;          // [N] or [1]
+    const float* bias;        // [N] or NULL
+    void* out;                // [M, N]
+    int out_dt;
+    int tm, tn;               // tiles along M and N
+};
+
+__device__ __forceinline__ int gemm_unit(int r, int c) { return (r << 2) | (c ^ ((r >> 2) & 3)); }
+
+// the tile of block b: XCD-contiguous renumbering, then 8-high groups of tiles
+__device__ __forceinline__ void gemm_tile(int b, int tm, int tn, int* im, int* in) {
+    const int total = tm * tn;
+    int id = b;
+    if (total % 8 == 0) id = (b % 8) * (total / 8) + b / 8;
+    const int group = 8 * tn;
+    const int first = (id / group) * 8;
+    const int rows = tm - first < 8 ? tm - first : 8;
+    *im = first + (id % group) % rows;
+    *in = (id % group) / rows;
+}
+
+// a workgroup barrier without the memory fence of __syncthreads (which would wait for every direct load in flight):
+// the direct loads a stage needs are waited for explicitly (wait_vm) before it; the clobber keeps the compiler from
+// moving LDS accesses across it
+__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// waits until at most N vector-memory operations of this thread are outstanding (N a constant)
+template <int N> __device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int ACT, bool PER_N>
+__global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
+    __shared__ __attribute__((aligned(16))) int8_t lds[kGemmLds];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+    int im, in;
+    gemm_tile((int) blockIdx.x, P.tm, P.tn, &im, &in);
+    const int64_t m0 = (int64_t) im * kGemmBM, n0 = (int64_t) in * kGemmBN, K = P.K;
+
+    // the sources of this thread's direct loads: instruction q of wavefront w fills units 64 (4 w + q) .. + 63, so
+    // this lane fetches row r = 16 (4 w + q) + lane / 4 (clamped into the matrix) at chunk
+    // (lane % 4) ^ ((r / 4) % 4) = (lane % 4) ^ ((lane / 16) % 4): a uniform block base plus a 32-bit lane offset
+    const int8_t* baseA = P.A + m0 * K;
+    const int8_t* baseW = P.W + n0 * K;
+    uint32_t offA_g[4], offW_g[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = 16 * (4 * wave + q) + (lane >> 2), c = (lane & 3) ^ ((lane >> 4) & 3);
+        const int64_t ra = m0 + r < P.M ? r : P.M - 1 - m0, rw = n0 + r < P.N ? r : P.N - 1 - n0;
+        offA_g[q] = (uint32_t) (ra * K + 16 * c);
+        offW_g[q] = (uint32_t) (rw * K + 16 * c);
+    }
+    auto issue = [&](int kt) {
+        int8_t* st = lds + (kt % kGemmStages) * kGemmStageBytes;
+        const int64_t k0 = (int64_t) kt * kGemmBK;
+        const int8_t* a = baseA + k0;
+        const int8_t* w = baseW + k0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) (a + offA_g[q]),
+                                             (__attribute__((address_space(3))) void*) (st + (4 * wave + q) * 1024), 16, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) (w + offW_g[q]),
+                                             (__attribute__((address_space(3))) void*) (st + kGemmBM * kGemmBK + (4 * wave + q) * 1024),
+                                             16, 0, 0);
+    };
+
+    v16i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = (v16i) 0;
+
+    // fragment offsets (bytes in a stage): row l % 32 of each 32-row tile, chunk 2 kk + l / 32
+    int offA[2][4], offW[2][4];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = 2 * kk + (lane >> 5);
+            offA[kk][i] = gemm_unit(wm * 128 + i * 32 + (lane & 31), c) * 16;
+            offW[kk][i] = kGemmBM * kGemmBK + gemm_unit(wn * 128 + i * 32 + (lane & 31), c) * 16;
+        }
+
+    const int nk = (int) (K / kGemmBK);
+    // the fragments of one 32-deep slice kk of stage kt (four A and four W)
+    auto read_half = [&](int kt, int kk, v4i (&a)[4], v4i (&b)[4]) {
+        const int8_t* st = lds + (kt % kGemmStages) * kGemmStageBytes;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i] = *reinterpret_cast<const v4i*>(st + offA[kk][i]);
+            b[i] = *reinterpret_cast<const v4i*>(st + offW[kk][i]);
+        }
+    };
+    // W's fragment as the first operand: acc[i][j] holds rows (columns of out) from W tile j and columns (rows of
+    // out) from A tile i, so each lane ends with four consecutive output columns of one output row per register group
+    auto mfma = [&](const v4i (&a)[4], const v4i (&b)[4], int p) {
+        const int i = p / 4, j = p % 4;
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[j], a[i], acc[i][j], 0, 0, 0);
+    };
+    // stage kt has landed once at most the stages issued after it (8 loads each) are outstanding
+    auto wait_stage = [&](int kt, int issued) {
+        const int after = issued - 1 - kt;
+        if (after >= 3) wait_vm<24>();
+        else if (after == 2) wait_vm<16>();
+        else if (after == 1) wait_vm<8>();
+        else wait_vm<0>();
+    };
+    int issued = 0;
+    for (; issued < kGemmStages && issued < nk; ++issued) issue(issued);
+    v4i xa[4], xb[4], ya[4], yb[4];   // slice 0 and slice 1 fragments
+    wait_stage(0, issued);
+    block_barrier();
+    read_half(0, 0, xa, xb);
+    // Step kt: the 16 products of slice 0 with slice 1's fragment reads between them; then four products of slice 1,
+    // this wavefront's fragment reads done (lgkmcnt), stage kt + 1 landed (vmcnt) and the barrier - after which no
+    // wavefront reads stage kt's buffer, so it is refilled with stage kt + 4 - and the last 12 products of slice 1
+    // with the reads of stage kt + 1's slice 0 between them.
+    for (int kt = 0; kt < nk - 1; ++kt) {
+        read_half(kt, 1, ya, yb);
+#pragma unroll
+        for (int p = 0; p < 16; ++p) mfma(xa, xb, p);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 2, 0);   // two products
+            __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // one fragment read
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) mfma(ya, yb, p);
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+        wait_stage(kt + 1, issued);
+        block_barrier();
+        if (issued < nk) issue(issued++);
+        read_half(kt + 1, 0, xa, xb);
+#pragma unroll
+        for (int p = 4; p < 16; ++p) mfma(ya, yb, p);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x0100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x0008, 8, 0);
+    }
+    // the last step: its slice 1 read, no stage after it
+    read_half(nk - 1, 1, ya, yb);
+#pragma unroll
+    for (int p = 0; p < 16; ++p) mfma(xa, xb, p);
+#pragma unroll
+    for (int p = 0; p < 16; ++p) mfma(ya, yb, p);
+    wait_vm<0>();
+    __syncthreads();   // every stage read: the LDS is the epilogue's now
+
+    // ---- epilogue ----
+    // Register r of acc[i][j] holds out[m][n] with m = wm 128 + 32 i + lane % 32 and
+    // n = wn 128 + 32 j + 8 (r / 4) + 4 (lane / 32) + r % 4: four consecutive columns per group of four registers.
+    // Per 32-row slice i of this wavefront's 128 x 128 region: dequant + activation in registers, the four columns
+    // as one 8-byte (16-bit out) or 16-byte (float32 out) LDS write, then 16-byte row-contiguous global stores.
+    // One wavefront writes and reads its own slice, and a wavefront's LDS operations run in order.
+    float* srow = reinterpret_cast<float*>(lds);            // s[m] of the block's 256 rows
+    float* wcol = srow + kGemmBM;                           // wscale[n] of its 256 columns
+    float* bcol = wcol + kGemmBN;                           // bias[n]
+    {
+        const int64_t m = m0 + tid < P.M ? m0 + tid : P.M - 1, n = n0 + tid < P.N ? n0 + tid : P.N - 1;
+        srow[tid] = P.sA[m];
+        wcol[tid] = PER_N ? P.ws[n] : 0.0f;
+        bcol[tid] = P.bias ? P.bias[n] : 0.0f;
+    }
+    __syncthreads();
+    auto epilogue = [&](auto out_tag, auto bias_tag) {
+        constexpr int OUT = decltype(out_tag)::value;
+        constexpr bool BIAS = decltype(bias_tag)::value;
+        constexpr int esz = OUT == H3S_F32 ? 4 : 2;
+        constexpr int pitch = 128 * esz + 16;               // bytes a slice row (16 bytes of pad: distinct banks)
+        int8_t* slice = lds + 3 * 1024 + wave * (32 * pitch);
+        const float ws0 = PER_N ? 0.0f : P.ws[0];
+        // rows of out start on 16-byte boundaries and the block's tile lies inside out: plain 16-byte stores
+        const bool full = (P.N * esz) % 16 == 0 && m0 + kGemmBM <= P.M && n0 + kGemmBN <= P.N;
+        constexpr int per_row = 128 * esz / 16, epc = 16 / esz;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float sr = srow[wm * 128 + i * 32 + (lane & 31)];
+            const float f1 = sr * ws0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int cl = wn * 128 + j * 32 + 8 * g + 4 * (lane >> 5);    // first of the four columns
+                    float v[4];
+                    if constexpr (PER_N) {
+                        const float4 w4 = *reinterpret_cast<const float4*>(wcol + cl);
+                        const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) v[q] = (float) acc[i][j][4 * g + q] * sr * wv[q];
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) v[q] = (float) acc[i][j][4 * g + q] * f1;
+                    }
+                    if constexpr (BIAS) {
+                        const float4 b4 = *reinterpret_cast<const float4*>(bcol + cl);
+                        v[0] = v[0] + b4.x; v[1] = v[1] + b4.y; v[2] = v[2] + b4.z; v[3] = v[3] + b4.w;
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) v[q] = act<ACT>(v[q]);
+                    int8_t* at = slice + (lane & 31) * pitch + (j * 32 + 8 * g + 4 * (lane >> 5)) * esz;
+                    if constexpr (OUT == H3S_F32)
+                        *reinterpret_cast<float4*>(at) = make_float4(v[0], v[1], v[2], v[3]);
+                    else if constexpr (OUT == H3S_BF16)
+                        *reinterpret_cast<uint2*>(at) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+                    else
+                        *reinterpret_cast<uint2*>(at) = make_uint2(pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
+                }
+            const int64_t mt = m0 + wm * 128 + i * 32, nt = n0 + wn * 128;
+#pragma unroll
+            for (int k = 0; k < 32 * per_row / 64; ++k) {
+                const int ch = lane + 64 * k, rr = ch / per_row, cg = ch % per_row;
+                const int64_t m = mt + rr, n = nt + (int64_t) cg * epc;
+                const uint4 val = *reinterpret_cast<const uint4*>(slice + rr * pitch + cg * 16);
+                char* o = reinterpret_cast<char*>(P.out) + (m * P.N + n) * esz;
+                if (full) {
+                    st_nt(o, val);
+                } else if (m < P.M && n < P.N) {
+                    const uint32_t w4[4] = {val.x, val.y, val.z, val.w};
+                    for (int e = 0; e < epc && n + e < P.N; ++e) {
+                        if constexpr (esz == 4) reinterpret_cast<uint32_t*>(o)[e] = w4[e];
+                        else reinterpret_cast<uint16_t*>(o)[e] = (uint16_t) (w4[e / 2] >> (16 * (e & 1)));
+                    }
+                }
+            }
+        }
+    };
+    using bf16_t = std::integral_constant<int, H3S_BF16>;
+    using f16_t = std::integral_constant<int, H3S_F16>;
+    using f32_t = std::integral_constant<int, H3S_F32>;
+    using yes = std::true_type;
+    using no = std::false_type;
+    if (P.out_dt == H3S_BF16) { if (P.bias) epilogue(bf16_t{}, yes{}); else epilogue(bf16_t{}, no{}); }
+    else if (P.out_dt == H3S_F16) { if (P.bias) epilogue(f16_t{}, yes{}); else epilogue(f16_t{}, no{}); }
+    else { if (P.bias) epilogue(f32_t{}, yes{}); else epilogue(f32_t{}, no{}); }
+}
+
+}  // namespace h3
