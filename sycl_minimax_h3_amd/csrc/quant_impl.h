@@ -96,6 +96,25 @@ template <int V, int S> __device__ __forceinline__ void syl_x(float (&v)[V], int
         else H3_FMAC_DPP8("row_ror:8");
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = o[e];
+    } else if constexpr (V == 8 && S == 4) {
+        // lane ^ 4 = (lane ^ 3) ^ 7: a quad reversal, then the half-row mirror inside the multiply-add
+        float x[8], o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[e]), 0x1B, 0xF, 0xF, true));
+        asm volatile("s_nop 1\n"
+                     "v_fmac_f32_dpp %0, %8, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+                     "v_fmac_f32_dpp %1, %9, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+                     "v_fmac_f32_dpp %2, %10, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+                     "v_fmac_f32_dpp %3, %11, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+                     "v_fmac_f32_dpp %4, %12, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+                     "v_fmac_f32_dpp %5, %13, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+                     "v_fmac_f32_dpp %6, %14, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+                     "v_fmac_f32_dpp %7, %15, %16 row_half_mirror row_mask:0xf bank_mask:0xf"
+                     : "=v"(o[0]), "=v"(o[1]), "=v"(o[2]), "=v"(o[3]), "=v"(o[4]), "=v"(o[5]), "=v"(o[6]), "=v"(o[7])
+                     : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(sg),
+                       "0"(v[0]), "1"(v[1]), "2"(v[2]), "3"(v[3]), "4"(v[4]), "5"(v[5]), "6"(v[6]), "7"(v[7]));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = o[e];
     } else {
 #pragma unroll
         for (int e = 0; e < V; ++e) v[e] = __builtin_fmaf(lane_xor<S>(v[e]), sg, v[e]);
@@ -187,15 +206,17 @@ struct QuantArgs {
     float* s;
 };
 
-// ROTATED: a rotation runs (its kind, A.rot, and group size at run time); F: the side inputs (ROW_W, ROW_TAB,
-// ROW_TAB32 or ROW_DYN, as in rowcore.h), or ROW_RAW: no norm, x itself is quantized.
+// ROT: the rotation kind (group size at run time); F: the side inputs (ROW_W, ROW_TAB, ROW_TAB32 or ROW_DYN, as in
+// rowcore.h), or ROW_RAW: no norm, x itself is quantized. The exact masks round h to bfloat16 (the type of the
+// reference's scratch h); ROW_DYN takes h's type at run time.
 //
-// Persistent: a unit (one block for rows of 256 or 512 lanes, one wavefront for 64-lane rows) quantizes the rows
-// [unit * rpu, (unit + 1) * rpu). A lane works on the same chunks of every row, so the weight and the table row
-// are decoded into registers once (the table row again only when rows[] changes), and the next row's x is in
-// flight while this row is computed.
-template <int XDT, int CPL, bool ROTATED, int F>
+// A unit (one block for rows of 256 or 512 lanes, one wavefront for 64-lane rows) quantizes the rows
+// [unit * rpu, (unit + 1) * rpu). A lane works on the same chunks of every row, so the weight and the table row are
+// decoded into registers once (the table row again only when rows[] changes), and the next row's x is in flight
+// while this one is computed.
+template <int XDT, int CPL, int ROT, int F>
 __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int64_t rpu) {
+    constexpr bool ROTATED = ROT != H3S_ROT_NONE;
     constexpr int V = Vec<XDT>::V;
     constexpr bool DYN = F & ROW_DYN;
     constexpr bool TW = DYN || (F & ROW_TAB32);
@@ -204,11 +225,12 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
     const bool has_w = DYN ? A.w != nullptr : (F & ROW_W) != 0;
     const bool has_tab = DYN ? A.scale != nullptr : (F & ROW_TAB) != 0;
     const int tab_dt = (!DYN && (F & ROW_TAB32)) ? H3S_F32 : A.tab_dt;
+    const int h_dt = DYN ? A.h_dt : H3S_BF16;
     const int L = 1 << lshift, W = L >> 6, lane = (int) (threadIdx.x & 63);
     const int t = (int) (threadIdx.x & (L - 1));
     const int64_t unit = L >= 256 ? (int64_t) blockIdx.x : (int64_t) blockIdx.x * (256 >> lshift) + (threadIdx.x >> lshift);
     const int64_t C = A.C, nch = C / V, r0 = unit * rpu, r1 = r0 + rpu < A.M ? r0 + rpu : A.M;
-    if (L < 256 && r0 >= A.M) return;    // a 64-lane unit past the rows (no barriers on 64-lane rows)
+    if (r0 >= A.M) return;               // a unit with no rows (a whole block, or a 64-lane wavefront, which has no barrier)
     int64_t cc[CPL];
     bool ok[CPL];
 #pragma unroll
@@ -222,9 +244,10 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
 #pragma unroll
         for (int j = 0; j < CPL; ++j) xr[j] = xp[cc[j]];
     };
-    uint4 xr[CPL];
-    if (r0 < r1) load_row(xr, r0);
-    int64_t tn = has_tab && A.rows && r0 < r1 ? A.rows[r0] : 0;
+    // this row's and the next row's x (x0, x1) and table row indices
+    uint4 x0[CPL];
+    load_row(x0, r0);
+    int64_t t0 = has_tab && A.rows ? A.rows[r0] : 0;
 
     // ---- the weight and the table row, as floats: w, 1 + scale, shift ----
     float wv[CPL][V], s1[CPL][V], sh[CPL][V];
@@ -253,23 +276,24 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
     };
 
     // the normalization of a rotated group, with the sign the Sylvester cross-lane stages leave on this lane
-    const float cgs = ROTATED && A.rot == H3S_ROT_SYLVESTER ? A.cg * syl_sign<V>(lane, A.group) : A.cg;
+    const float cgs = ROT == H3S_ROT_SYLVESTER ? A.cg * syl_sign<V>(lane, A.group) : A.cg;
     int slot = 0;   // consecutive reductions use alternate LDS slots
     for (int64_t row = r0; row < r1; ++row) {
         // the next row's x and table row index, in flight during this row
-        uint4 xn[CPL];
-        const bool more = row + 1 < r1;
-        if (more) load_row(xn, row + 1);
-        const int64_t tr = tn;
-        if (has_tab && A.rows && more) tn = A.rows[row + 1];
-        if (has_tab && tr != tcur) {
-            load_tables(tr);
-            tcur = tr;
+        uint4 x1[CPL];
+        int64_t t1 = 0;
+        if (row + 1 < r1) {
+            load_row(x1, row + 1);
+            if (has_tab && A.rows) t1 = A.rows[row + 1];
+        }
+        if (has_tab && t0 != tcur) {
+            load_tables(t0);
+            tcur = t0;
         }
 
         float v[CPL][V];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(xr[j], v[j]);
+        for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(x0[j], v[j]);
 
         // ---- rms_norm_mod into h's type ----
         if constexpr (NORM) {
@@ -294,14 +318,14 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
 #pragma unroll
                     for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * s1[j][e] + sh[j][e];
                 }
-                if (A.h_dt == H3S_BF16) {
+                if (h_dt == H3S_BF16) {
 #pragma unroll
                     for (int e = 0; e < V; e += 2) {
                         const uint32_t p = pack_bf16(v[j][e], v[j][e + 1]);
                         v[j][e] = bf16_lo(p);
                         v[j][e + 1] = bf16_hi(p);
                     }
-                } else if (A.h_dt == H3S_F16) {
+                } else if (h_dt == H3S_F16) {
 #pragma unroll
                     for (int e = 0; e < V; e += 2) {
                         const uint32_t p = pack_f16(v[j][e], v[j][e + 1]);
@@ -317,7 +341,7 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             if constexpr (ROTATED) {
-                if (A.rot == H3S_ROT_SYLVESTER) sylvester<V>(v[j], lane, A.group);
+                if constexpr (ROT == H3S_ROT_SYLVESTER) sylvester<V>(v[j], lane, A.group);
                 else regular<V>(v[j], A.group);
 #pragma unroll
                 for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * cgs;
@@ -346,7 +370,8 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
             }
         }
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) xr[j] = xn[j];
+        for (int j = 0; j < CPL; ++j) x0[j] = x1[j];
+        t0 = t1;
     }
 }
 
@@ -359,12 +384,12 @@ constexpr int kQuantNone = 0, kQuantW = ROW_W, kQuantWTab = ROW_W | ROW_TAB, kQu
 // Launches the kernel for one input type; the plan comes from row_plan.
 template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, bool norm, RowPlan p) {
     int f = (A.w ? ROW_W : 0) | (A.scale ? ROW_TAB | (A.tab_dt == H3S_F32 ? ROW_TAB32 : 0) : 0);
-    if (XDT == H3S_F32 || !(f == kQuantNone || f == kQuantW || f == kQuantWTab || f == kQuantWTab32)) f = ROW_DYN;
+    if (XDT == H3S_F32 || A.h_dt != H3S_BF16 || !(f == kQuantNone || f == kQuantW || f == kQuantWTab || f == kQuantWTab32))
+        f = ROW_DYN;
     if (!norm) f = kQuantRaw;
-    const bool rotated = A.rot != H3S_ROT_NONE;
 #define H3_QUANT_F(CC, RR, FF)                                                                      \
     {                                                                                                \
-        const PersistentLaunch R = persistent_launch(c, (const void*) quant_kernel<XDT, CC, RR, FF>, A.M, p); \
+        const PersistentLaunch R = persistent_launch(c, (const void*) quant_kernel<XDT, CC, RR, FF>, A.M, p, A.scale != nullptr); \
         quant_kernel<XDT, CC, RR, FF><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift, R.rpu);    \
     }
 #define H3_QUANT_R(CC, RR)                                                                           \
@@ -377,10 +402,11 @@ template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, 
     }                                                                                                \
     H3_QUANT_F(CC, RR, ROW_DYN);                                                                     \
     return launched(fn);
-#define H3_QUANT_CPL(CC)                           \
-    if (p.cpl == CC) {                             \
-        if (rotated) { H3_QUANT_R(CC, true) }      \
-        else { H3_QUANT_R(CC, false) }             \
+#define H3_QUANT_CPL(CC)                                                      \
+    if (p.cpl == CC) {                                                        \
+        if (A.rot == H3S_ROT_SYLVESTER) { H3_QUANT_R(CC, H3S_ROT_SYLVESTER) }  \
+        else if (A.rot == H3S_ROT_REGULAR) { H3_QUANT_R(CC, H3S_ROT_REGULAR) } \
+        else { H3_QUANT_R(CC, H3S_ROT_NONE) }                                 \
     }
     H3_QUANT_CPL(1)
     H3_QUANT_CPL(2)

@@ -47,21 +47,22 @@ inline RowLaunch row_launch(int64_t M, RowPlan p) {
 // blocks of a kernel that fit one compute unit at once, asked of the runtime once per kernel and block size
 int blocks_per_cu(const void* kernel, int threads);
 
-// A persistent launch: twice as many units (blocks of L >= 256 lanes, wavefronts of 64) as the device holds at
-// once, each taking rpu consecutive rows. The occupancy of each kernel is asked once.
+// A launch of row units (blocks of L >= 256 lanes, wavefronts of 64); unit u takes rows [u rpu, (u + 1) rpu). With
+// `keep` (side inputs worth holding in registers across rows: table rows) twice as many units as the device holds
+// at once, each taking a contiguous run of rows; else one unit a row (measured faster when there is nothing to
+// keep). The occupancy of each kernel is asked once.
 struct PersistentLaunch {
     unsigned grid, threads;
     int lshift;
     int64_t rpu;                                         // rows a unit
 };
-inline PersistentLaunch persistent_launch(const Ctx* c, const void* kernel, int64_t M, RowPlan p) {
+inline PersistentLaunch persistent_launch(const Ctx* c, const void* kernel, int64_t M, RowPlan p, bool keep) {
     PersistentLaunch r;
     r.threads = (unsigned) (p.L >= 256 ? p.L : 256);
     r.lshift = __builtin_ctz((unsigned) p.L);
     const int upb = p.L >= 256 ? 1 : 256 / p.L;          // units a block
     const int per_cu = blocks_per_cu(kernel, (int) r.threads);
-    // twice what is resident: short jobs get one row a unit, long ones a steady stream
-    const int64_t units = std::min<int64_t>(M, (int64_t) c->cus * per_cu * upb * 2);
+    const int64_t units = keep ? std::min<int64_t>(M, (int64_t) c->cus * per_cu * upb * 2) : M;
     r.rpu = (M + units - 1) / units;
     const int64_t used = (M + r.rpu - 1) / r.rpu;        // units that get rows
     r.grid = (unsigned) ((used + upb - 1) / upb);
