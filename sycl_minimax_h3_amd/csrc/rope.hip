@@ -6,8 +6,8 @@
 // one passed-through chunk. A head takes P2 lanes (its slot count rounded up to a power of two), so a wave holds
 // 64 / P2 heads side by side; the head's sum of squares is the lane's own in chunk order, then an xor butterfly over
 // its P2 lanes: the canonical order of the CPU oracle. One wave per token: it reads the token's cos/sin row once
-// and the weights once, then every head of q and of k.
-#include "common.h"
+// and the weights once, then every head of q and of k. The rows are written back with nontemporal stores.
+#include "rowcore.h"
 
 namespace h3 {
 
@@ -85,13 +85,13 @@ __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M
                     oa[e] = A * co[e] - B * si[e];
                     ob[e] = B * co[e] + A * si[e];
                 }
-                *reinterpret_cast<uint4*>(base + off0 * (16 / V / 2)) = Vec<XDT>::pack(oa);
-                *reinterpret_cast<uint4*>(base + off1 * (16 / V / 2)) = Vec<XDT>::pack(ob);
+                st_nt(base + off0 * (16 / V / 2), Vec<XDT>::pack(oa));
+                st_nt(base + off1 * (16 / V / 2), Vec<XDT>::pack(ob));
             } else {
                 float oa[V];
 #pragma unroll
                 for (int e = 0; e < V; ++e) oa[e] = a[e] * inv * wa[e];
-                *reinterpret_cast<uint4*>(base + off0 * (16 / V / 2)) = Vec<XDT>::pack(oa);
+                st_nt(base + off0 * (16 / V / 2), Vec<XDT>::pack(oa));
             }
         }
     }
