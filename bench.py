@@ -5,7 +5,8 @@
 A step is one launch of the headline kernel over the whole batch: the AdaLN chain (LayerNorm without affine, then
 x * (1 + scale) + shift, GELU-tanh, out = res + gate * y) on X, res [16896 x 4096] bf16, token grid T16 x H24 x W44.
 ``value`` is its achieved HBM bandwidth: algorithmic bytes (X and res read once, out written once) divided by the
-mean kernel time. The library context wraps PyTorch's current stream (h3s_create), so the kernels run on that
+mean kernel time. Each kernel first runs untimed for 0.15 s (the clocks ramp up over the first milliseconds of load),
+then W warm-up launches, then the K timed launches. The library context wraps PyTorch's current stream (h3s_create), so the kernels run on that
 stream and the HIP events recorded on it (torch.cuda.Event) bracket exactly the timed launches; inputs are already
 in HBM. The other fused kernels are timed the same way and reported under ``kernels``; the int8 GEMM also as int8
 TOPS. ``roofline.traffic`` is the headline kernel's HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE
@@ -78,7 +79,7 @@ def rope_table(T, Hh, Ww, dims=(32, 48, 48), theta=10000.0):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of kernel keys to time (default all)")
@@ -107,7 +108,15 @@ def main() -> int:
     def bf16(*shape, scale=1.0):
         return (torch.randn(*shape, device=dev_t) * scale).to(torch.bfloat16)
 
-    def timed(fn, steps, warmup):
+    def timed(fn, steps, warmup, settle_s=0.15):
+        # The device's clocks ramp up over the first ~10 ms of sustained load: before the W warm-up launches, keep
+        # launching (untimed) until settle_s seconds of this kernel have run, so the timed launches see the sustained
+        # state a busy serving loop runs in.
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < settle_s:
+            for _ in range(10):
+                fn()
+            torch.cuda.synchronize()
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()

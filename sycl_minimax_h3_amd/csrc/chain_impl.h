@@ -46,8 +46,12 @@ __global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift)
     const bool has_tab = DYN ? A.scale != nullptr : (F & ROW_TAB) != 0;
     const bool has_gate = DYN ? A.gate != nullptr : (F & ROW_GATE) != 0;
     const bool has_res = DYN ? A.res != nullptr : (F & ROW_RES) != 0;
-    const int tab_dt = (!DYN && (F & ROW_TAB32)) ? H3S_F32 : A.tab_dt;
-    const int res_dt = (!DYN && (F & ROW_RES32)) ? H3S_F32 : A.res_dt;
+    // exact masks: norm and activation fixed, every 16-bit tensor bfloat16
+    const int tab_dt = DYN ? A.tab_dt : (F & ROW_TAB32) ? H3S_F32 : H3S_BF16;
+    const int res_dt = DYN ? A.res_dt : (F & ROW_RES32) ? H3S_F32 : H3S_BF16;
+    const int out_dt = DYN ? A.out_dt : H3S_BF16;
+    const int norm = DYN ? A.norm : (F & ROW_LN) ? H3S_NORM_LAYER : H3S_NORM_RMS;
+    const int act_kind = DYN ? A.act : row_act(F);
     const RowPos P = row_pos(lshift, A.M);
     const int L = 1 << lshift;
     const int64_t row = P.row, C = A.C, nch = C / V;
@@ -99,7 +103,7 @@ __global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift)
 #pragma unroll
     for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(xr[j], v[j]);
     float mean = 0.0f, inv;
-    if (A.norm == H3S_NORM_LAYER) {
+    if (norm == H3S_NORM_LAYER) {
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < CPL; ++j)
@@ -131,7 +135,7 @@ __global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift)
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         float o[V], f[V], g[V];
-        if (A.norm == H3S_NORM_LAYER) {
+        if (norm == H3S_NORM_LAYER) {
 #pragma unroll
             for (int e = 0; e < V; ++e) o[e] = (v[j][e] - mean) * inv;
         } else {
@@ -154,10 +158,10 @@ __global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift)
 #pragma unroll
             for (int e = 0; e < V; ++e) o[e] = o[e] * (1.0f + f[e]) + g[e];
         }
-        if (A.act == H3S_ACT_GELU_TANH) {
+        if (act_kind == H3S_ACT_GELU_TANH) {
 #pragma unroll
             for (int e = 0; e < V; ++e) o[e] = act_gelu_tanh(o[e]);
-        } else if (A.act == H3S_ACT_SILU) {
+        } else if (act_kind == H3S_ACT_SILU) {
 #pragma unroll
             for (int e = 0; e < V; ++e) o[e] = act_silu(o[e]);
         }
@@ -171,48 +175,55 @@ __global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift)
 #pragma unroll
             for (int e = 0; e < V; ++e) o[e] = f[e] + o[e];
         }
-        if (P.live && ok[j]) store_chunk<V>(A.out, A.out_dt, row * C + cc[j] * V, o);
+        if (P.live && ok[j]) store_chunk<V>(A.out, out_dt, row * C + cc[j] * V, o);
     }
 }
 
-// The feature masks compiled exactly (16-bit inputs): h3s_rms_norm_mod without and with its float32 tables,
-// h3s_layer_norm without and with weight and bias, and the AdaLN chain with 16-bit tables, gate and residual.
-// Every other call shape runs the ROW_DYN instantiation.
-constexpr int kChainW = ROW_W, kChainWTab32 = ROW_W | ROW_TAB | ROW_TAB32, kChainNone = 0, kChainWB = ROW_W | ROW_B,
-              kChainTabGateRes = ROW_TAB | ROW_GATE | ROW_RES;
+// The call shapes compiled exactly (bfloat16 rows, 16-bit tensors all bfloat16): h3s_rms_norm_mod without and with
+// its float32 tables, h3s_layer_norm without and with weight and bias, and the AdaLN chain (16-bit tables, gate and
+// residual) for each norm and activation. Every other call shape runs the ROW_DYN instantiation.
+constexpr int kChainW = ROW_W, kChainWTab32 = ROW_W | ROW_TAB | ROW_TAB32, kChainLn = ROW_LN, kChainLnWB = ROW_LN | ROW_W | ROW_B,
+              kChainAda = ROW_TAB | ROW_GATE | ROW_RES;
 
-inline int chain_features(const ChainArgs& A) {
-    const bool t16 = A.tab_dt != H3S_F32, r16 = A.res_dt != H3S_F32;
-    const int f = (A.w ? ROW_W : 0) | (A.b ? ROW_B : 0) | (A.scale ? ROW_TAB | (t16 ? 0 : ROW_TAB32) : 0) |
-                  (A.gate ? ROW_GATE : 0) | (A.res ? ROW_RES | (r16 ? 0 : ROW_RES32) : 0);
-    if (A.gate && !A.scale && !t16) return ROW_DYN;   // a float32 gate alone has no exact mask
-    return f;
+inline int chain_features(const ChainArgs& A, int x_dt) {
+    const bool bf = x_dt == H3S_BF16 && A.out_dt == H3S_BF16 && (!(A.scale || A.gate) || A.tab_dt != H3S_F16) &&
+                    (!A.res || A.res_dt == H3S_BF16);
+    const int f = (A.w ? ROW_W : 0) | (A.b ? ROW_B : 0) | (A.scale ? ROW_TAB | (A.tab_dt == H3S_F32 ? ROW_TAB32 : 0) : 0) |
+                  (A.gate ? ROW_GATE : 0) | (A.res ? ROW_RES : 0) | (A.norm == H3S_NORM_LAYER ? ROW_LN : 0);
+    if (!bf || (A.gate && A.tab_dt == H3S_F32)) return ROW_DYN;
+    if (A.act == H3S_ACT_NONE && (f == kChainW || f == kChainWTab32 || f == kChainLn || f == kChainLnWB)) return f;
+    if ((f & ~ROW_LN) == kChainAda) return f | A.act * ROW_ACT1;
+    return ROW_DYN;
 }
 
 // Launches the chain for one input type; the plan comes from row_plan.
 template <int XDT> int chain_launch(Ctx* c, const char* fn, const ChainArgs& A, RowPlan p) {
     const RowLaunch R = row_launch(A.M, p);
-    int f = chain_features(A);
-    if (XDT == H3S_F32 || !(f == kChainW || f == kChainWTab32 || f == kChainNone || f == kChainWB || f == kChainTabGateRes))
-        f = ROW_DYN;
+    const int f = chain_features(A, XDT);
 #define H3_CHAIN_F(CC, FF) row_chain_kernel<XDT, CC, FF><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift)
-#define H3_CHAIN_CPL(CC)                                                    \
-    if (p.cpl == CC) {                                                      \
-        if constexpr (XDT != H3S_F32) {                                     \
-            if (f == kChainW) { H3_CHAIN_F(CC, kChainW); return launched(fn); }                     \
-            if (f == kChainWTab32) { H3_CHAIN_F(CC, kChainWTab32); return launched(fn); }           \
-            if (f == kChainNone) { H3_CHAIN_F(CC, kChainNone); return launched(fn); }               \
-            if (f == kChainWB) { H3_CHAIN_F(CC, kChainWB); return launched(fn); }                   \
-            if (f == kChainTabGateRes) { H3_CHAIN_F(CC, kChainTabGateRes); return launched(fn); }   \
-        }                                                                   \
-        H3_CHAIN_F(CC, ROW_DYN);                                            \
-        return launched(fn);                                                \
+#define H3_CHAIN_ADA(CC, NORM)                                                                                        \
+    if (f == (kChainAda | NORM)) { H3_CHAIN_F(CC, kChainAda | NORM); return launched(fn); }                          \
+    if (f == (kChainAda | NORM | H3S_ACT_GELU_TANH * ROW_ACT1)) { H3_CHAIN_F(CC, kChainAda | NORM | H3S_ACT_GELU_TANH * ROW_ACT1); return launched(fn); } \
+    if (f == (kChainAda | NORM | H3S_ACT_SILU * ROW_ACT1)) { H3_CHAIN_F(CC, kChainAda | NORM | H3S_ACT_SILU * ROW_ACT1); return launched(fn); }
+#define H3_CHAIN_CPL(CC)                                                                        \
+    if (p.cpl == CC) {                                                                          \
+        if constexpr (XDT == H3S_BF16) {                                                        \
+            if (f == kChainW) { H3_CHAIN_F(CC, kChainW); return launched(fn); }                 \
+            if (f == kChainWTab32) { H3_CHAIN_F(CC, kChainWTab32); return launched(fn); }       \
+            if (f == kChainLn) { H3_CHAIN_F(CC, kChainLn); return launched(fn); }               \
+            if (f == kChainLnWB) { H3_CHAIN_F(CC, kChainLnWB); return launched(fn); }           \
+            H3_CHAIN_ADA(CC, 0)                                                                  \
+            H3_CHAIN_ADA(CC, ROW_LN)                                                             \
+        }                                                                                       \
+        H3_CHAIN_F(CC, ROW_DYN);                                                                \
+        return launched(fn);                                                                    \
     }
     H3_CHAIN_CPL(1)
     H3_CHAIN_CPL(2)
     H3_CHAIN_CPL(3)
     H3_CHAIN_CPL(4)
 #undef H3_CHAIN_CPL
+#undef H3_CHAIN_ADA
 #undef H3_CHAIN_F
     return fail(std::string(fn) + ": no kernel for this row length");
 }

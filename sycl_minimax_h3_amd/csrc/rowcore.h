@@ -161,7 +161,10 @@ enum : int {
     ROW_RES32 = 64,
     ROW_DYN = 128,
     ROW_RAW = 256,      // the quantizer on x itself, with no norm (h3s_int8_linear); no side inputs
+    ROW_LN = 512,       // the row chain: layer norm (else RMS norm)
+    ROW_ACT1 = 1024,    // the row chain's activation, 2 bits: H3S_ACT_NONE, H3S_ACT_GELU_TANH or H3S_ACT_SILU
 };
+constexpr int row_act(int f) { return (f / ROW_ACT1) & 3; }
 
 // ---- stores that bypass the caches' retention (the outputs are streamed, never read back by the kernel) ----
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
