@@ -2,17 +2,17 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 
-A step is one launch of the headline kernel over the whole batch: the AdaLN chain (LayerNorm without affine, then
-x * (1 + scale) + shift, GELU-tanh, out = res + gate * y) on X, res [16896 x 4096] bf16, token grid T16 x H24 x W44.
+A step is one launch of the headline kernel over the whole batch: the AdaLN chain (LayerNorm without affine, then x
+* (1 + scale) + shift, GELU-tanh, out = res + gate * y) on X, res [16896 x 4096] bf16, token grid T16 x H24 x W44.
 ``value`` is its achieved HBM bandwidth: algorithmic bytes (X and res read once, out written once) divided by the
-mean kernel time. Each kernel first runs untimed for 0.15 s (the clocks ramp up over the first milliseconds of load),
-then W warm-up launches, then the K timed launches. The library context wraps PyTorch's current stream (h3s_create), so the kernels run on that
-stream and the HIP events recorded on it (torch.cuda.Event) bracket exactly the timed launches; inputs are already
-in HBM. The other fused kernels are timed the same way and reported under ``kernels``; the int8 GEMM also as int8
-TOPS. ``roofline.traffic`` is the headline kernel's HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE
-runs summarized in profiles/hbm_traffic_pmc.md (each counter scaled by what it reads for a 1 GiB device copy).
-``cpu_baseline`` times the CPU oracle (the C restatement of the reference arithmetic) on the same workload on this
-host. Prints one JSON line.
+mean kernel time. Each kernel first runs untimed for 0.15 s (``--settle``; the clocks ramp up over the first
+milliseconds of load), then W warm-up launches, then the K timed launches. The library context wraps PyTorch's
+current stream (h3s_create), so the kernels run on that stream and the HIP events recorded on it (torch.cuda.Event)
+bracket exactly the timed launches; inputs are already in HBM. The other fused kernels are timed the same way and
+reported under ``kernels``; the int8 GEMM also as int8 TOPS. ``roofline.traffic`` is the headline kernel's HBM bytes
+per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarized in profiles/hbm_traffic_pmc.md (each counter
+scaled by what it reads for a 1 GiB device copy). ``cpu_baseline`` times the CPU oracle (the C restatement of the
+reference arithmetic) on the same workload on this host. Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -81,6 +81,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--settle", type=float, default=0.15, help="seconds each kernel runs untimed before its warm-up")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of kernel keys to time (default all)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -108,7 +109,7 @@ def main() -> int:
     def bf16(*shape, scale=1.0):
         return (torch.randn(*shape, device=dev_t) * scale).to(torch.bfloat16)
 
-    def timed(fn, steps, warmup, settle_s=0.15):
+    def timed(fn, steps, warmup, settle_s=args.settle):
         # The device's clocks ramp up over the first ~10 ms of sustained load: before the W warm-up launches, keep
         # launching (untimed) until settle_s seconds of this kernel have run, so the timed launches see the sustained
         # state a busy serving loop runs in.
