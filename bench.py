@@ -42,6 +42,7 @@ def bytes_cfg():
         "cfg4_rmsnorm_wht128_quant_47104": M4 * C * 2 + M4 * C + M4 * 4,
         "cfg5a_rmsnorm_mod_quant_47104": M4 * C * 2 + M4 * C + M4 * 4,
         "cfg5b_int8_gemm_silu_47104x16384": M4 * C + 16384 * C + M4 * 4 + 16384 * 4 + M4 * 16384 * 2,
+        "mlp_swiglu_quant_g256_47104x8192": M4 * 16384 * 2 + M4 * 8192 + M4 * 4,
     }
 
 
@@ -177,10 +178,15 @@ def main() -> int:
     run("cfg5a_rmsnorm_mod_quant_47104", lambda: ops.norm_quant(X5, G1, 1e-6, tb5, Q4, S4))
     w5 = torch.randint(-127, 128, (16384, C), dtype=torch.int8, device=dev_t)
     ws5 = (0.005 + 0.015 * torch.rand(16384, device=dev_t)).float()
-    out5 = torch.empty(M4, 16384, dtype=torch.bfloat16, device=dev_t)
+    out5 = bf16(M4, 16384)
     layer = ops.Int8Linear(T(w5), T(ws5))
     O5 = T(out5)
     run("cfg5b_int8_gemm_silu_47104x16384", lambda: ops.int8_gemm_dequant(Q4, S4, layer, A.ACT_SILU, O5), 5)
+
+    # ---- the MLP's middle: swiglu of fc1's [gate | up] output [47104 x 2*8192] -> fc2's quantizer (regular g 256) ----
+    q6, s6 = torch.empty(M4, 8192, dtype=torch.int8, device=dev_t), torch.empty(M4, device=dev_t)
+    X6, Q6, S6 = O5, T(q6), T(s6)    # the GEMM's output rows are [gate | up] halves of 8192
+    run("mlp_swiglu_quant_g256_47104x8192", lambda: ops.swiglu_quant(X6, Q6, S6, rot=A.ROT_REGULAR, group=256))
 
     copy = None
     if args.copy_probe:

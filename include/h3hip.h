@@ -167,6 +167,14 @@ int h3s_norm_quant(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, con
                    const int32_t* rows, const void* scale, const void* shift, int tab_dt, int h_dt, int rot, int group,
                    int8_t* q, float* s);
 
+/* h3s_swiglu then int8_linear's quantizer, in one pass over x (the MLP's act scratch and fc2's quantizer at
+ * engine/h3-core/src/dit.rs:363-364; kernels/h3sycl.cpp:1378-1419 and 404-474):
+ *   a = round_to_h_dt(silu(g) * u) with g = x[r, i], u = x[r, C + i]            (x rows of 2C, as h3s_swiglu)
+ *   then rotation and quantization of a as in h3s_norm_quant (rot, group; h3s_int8_linear's group is REGULAR).
+ * q int8 [M, C], s float32 [M]: the inputs of h3s_int8_gemm_dequant for fc2. */
+int h3s_swiglu_quant(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, int h_dt, int rot, int group, int8_t* q,
+                     float* s);
+
 /* out = res + gate * act(norm(x) * (1 + scale) + shift), in one pass; norm RMS (x * inv_rms * weight) or LAYER
  * ((x - mean) * inv_std * weight + bias); weight, bias float32 [C] or NULL; tables [R, C] in tab_dt with rows as in
  * h3s_norm_quant; gate NULL: 1; res NULL: none. Everything in float32, one rounding to out_dt at the end. */

@@ -540,6 +540,47 @@ int h3o_norm_quant(const void* x, int x_dt, int64_t M, int64_t C, const float* w
     return 0;
 }
 
+/* ---- swiglu into the MLP's act scratch, then fc2's quantizer (dit.rs:363-364; h3sycl.cpp:1378-1419, 404-474);
+ * with swiglu == 0 the quantizer alone on x (rows of C): h3s_int8_linear's quantizer with any rotation kind ---- */
+typedef struct {
+    const void* x; int x_dt; int64_t C; int h_dt; int rot; int group; int swiglu; int8_t* q; float* s;
+} sq_ctx;
+static void sq_rows(void* p, int64_t r0, int64_t r1) {
+    const sq_ctx* c = (const sq_ctx*) p;
+    const int64_t C = c->C;
+    float* y = (float*) malloc((size_t) C * sizeof(float));
+    for (int64_t r = r0; r < r1; ++r) {
+        for (int64_t i = 0; i < C; ++i) {
+            if (c->swiglu) {
+                const float g = h3o_load(c->x, c->x_dt, r * 2 * C + i), u = h3o_load(c->x, c->x_dt, r * 2 * C + C + i);
+                y[i] = h3o_round_to(g / (1.0f + expf(-g)) * u, c->h_dt);        /* h3sycl.cpp:1396, 1416 */
+            } else {
+                y[i] = h3o_load(c->x, c->x_dt, r * C + i);
+            }
+        }
+        if (c->rot != H3O_ROT_NONE)
+            for (int64_t g0 = 0; g0 < C; g0 += c->group) h3o_rotate_group(y + g0, c->group, c->rot);
+        quantize_row(y, C, c->q + r * C, c->s + r);
+    }
+    free(y);
+}
+static int sq_run(const void* x, int x_dt, int64_t M, int64_t C, int h_dt, int rot, int group, int swiglu, int8_t* q, float* s) {
+    if (M <= 0 || C <= 0) return 0;
+    if (!dt_ok(x_dt) || !dt_ok(h_dt)) return fail("swiglu_quant: unknown element type");
+    if (rot == H3O_ROT_REGULAR && (!is_pow4(group) || C % group != 0)) return fail("swiglu_quant: regular rotation needs g = 4^k dividing C");
+    if (rot == H3O_ROT_SYLVESTER && (group < 2 || (group & (group - 1)) != 0 || C % group != 0))
+        return fail("swiglu_quant: Sylvester rotation needs g = 2^k dividing C");
+    sq_ctx c = {x, x_dt, C, h_dt, rot, group, swiglu, q, s};
+    parallel_rows(M, sq_rows, &c);
+    return 0;
+}
+int h3o_swiglu_quant(const void* x, int x_dt, int64_t M, int64_t C, int h_dt, int rot, int group, int8_t* q, float* s) {
+    return sq_run(x, x_dt, M, C, h_dt, rot, group, 1, q, s);
+}
+int h3o_quantize_act(const void* x, int x_dt, int64_t M, int64_t C, int rot, int group, int8_t* q, float* s) {
+    return sq_run(x, x_dt, M, C, x_dt, rot, group, 0, q, s);
+}
+
 typedef struct {
     const void* x; int x_dt; int64_t C; int norm; const float* w; const float* b; float eps; const int32_t* rows;
     const void* scale; const void* shift; const void* gate; int tab_dt; int act; const void* res; int res_dt; void* out;

@@ -112,6 +112,10 @@ int h3o_gemm_dequant(const int8_t* q, const float* s, int64_t M, int64_t K, cons
  * no modulation. */
 int h3o_norm_quant(const void* x, int x_dt, int64_t M, int64_t C, const float* weight, float eps, const int32_t* rows,
                    const void* scale, const void* shift, int tab_dt, int h_dt, int rot, int group, int8_t* q, float* s);
+/* h3o_swiglu into a scratch of h_dt, then the quantizer of h3o_norm_quant (rotation rot/group) on it */
+int h3o_swiglu_quant(const void* x, int x_dt, int64_t M, int64_t C, int h_dt, int rot, int group, int8_t* q, float* s);
+/* the quantizer alone on x [M, C]: rotation rot/group, then s = max(max|y| / 127, 1e-30), q = rint(y / s) */
+int h3o_quantize_act(const void* x, int x_dt, int64_t M, int64_t C, int rot, int group, int8_t* q, float* s);
 /* out = res + gate * act(norm(x) * (1 + scale) + shift): norm RMS (weight) or layer norm (weight, bias optional);
  * tables as above, gate NULL: 1; res NULL: 0. */
 int h3o_norm_mod_act_gate(const void* x, int x_dt, int64_t M, int64_t C, int norm, const float* weight,

@@ -62,6 +62,8 @@ _SIGS = {
     "h3o_gemm_dequant": (i32, [vp, vp, i64, i64, vp, i64, vp, i64, vp, i32, vp, i32]),
     "h3o_norm_quant": (i32, [vp, i32, i64, i64, vp, f32, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "h3o_norm_mod_act_gate": (i32, [vp, i32, i64, i64, i32, vp, vp, f32, vp, vp, vp, vp, i32, i32, vp, i32, vp, i32]),
+    "h3o_swiglu_quant": (i32, [vp, i32, i64, i64, i32, i32, i32, vp, vp]),
+    "h3o_quantize_act": (i32, [vp, i32, i64, i64, i32, i32, vp, vp]),
     "h3o_act": (f32, [f32, i32]),
     "h3o_compare": (None, [vp, vp, i64, vp, vp]),
     "h3o_last_error": (C.c_char_p, []),
@@ -269,6 +271,22 @@ def norm_quant(x, x_dt, M, C_, weight, eps, rows=None, scale=None, shift=None, t
     s = np.empty(M, dtype=np.float32)
     _check(lib().h3o_norm_quant(_p(x), x_dt, M, C_, _p(weight), eps, _p(rows), _p(scale), _p(shift), tab_dt, h_dt, rot,
                                 group, _p(q), _p(s)))
+    return q, s
+
+
+def swiglu_quant(x, x_dt, M, C_, h_dt=BF16, rot=ROT_NONE, group=0):
+    """x [M, 2C] -> (q int8 [M*C], s f32 [M]): swiglu into h_dt, then the (rotated) quantizer."""
+    q = np.empty(M * C_, dtype=np.int8)
+    s = np.empty(M, dtype=np.float32)
+    _check(lib().h3o_swiglu_quant(_p(x), x_dt, M, C_, h_dt, rot, group, _p(q), _p(s)))
+    return q, s
+
+
+def quantize_act(x, x_dt, M, C_, rot=ROT_NONE, group=0):
+    """x [M, C] -> (q int8 [M*C], s f32 [M]): the (rotated) quantizer on x itself."""
+    q = np.empty(M * C_, dtype=np.int8)
+    s = np.empty(M, dtype=np.float32)
+    _check(lib().h3o_quantize_act(_p(x), x_dt, M, C_, rot, group, _p(q), _p(s)))
     return q, s
 
 

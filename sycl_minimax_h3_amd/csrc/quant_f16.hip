@@ -2,5 +2,5 @@
 #include "quant_impl.h"
 
 namespace h3 {
-template int quant_launch<H3S_F16>(Ctx*, const char*, const QuantArgs&, bool, RowPlan);
+template int quant_launch<H3S_F16>(Ctx*, const char*, const QuantArgs&, int, RowPlan);
 }

@@ -1,10 +1,12 @@
 // quant_impl.h - the row quantizer kernel behind h3s_norm_quant and h3s_int8_linear, instantiated per input type in
 // quant_bf16.hip, quant_f16.hip and quant_f32.hip.
 //
-// What it computes (the oracle's h3o_norm_quant / h3o_int8_linear quantizer):
-//   NORM:  h = round_to_h_dt(x * inv_rms [* w] [* (1 + scale[t]) + shift[t]])  rms_norm_mod into the reference's
-//          scratch h (engine/h3-core/src/dit.rs:340-342, kernels/h3sycl.cpp:766-810)
-//   !NORM: h = x                                                               (h3s_int8_linear's own input)
+// What it computes (the oracle's h3o_norm_quant / h3o_int8_linear quantizer / h3o_swiglu_quant):
+//   NORM:   h = round_to_h_dt(x * inv_rms [* w] [* (1 + scale[t]) + shift[t]])  rms_norm_mod into the reference's
+//           scratch h (engine/h3-core/src/dit.rs:340-342, kernels/h3sycl.cpp:766-810)
+//   RAW:    h = x                                                               (h3s_int8_linear's own input)
+//   SWIGLU: h = round_to_h_dt(silu(g) * u), x = [g | u] rows of 2C              (h3s_swiglu into the MLP's scratch
+//           act, then fc2's quantizer: engine/h3-core/src/dit.rs:363-364, kernels/h3sycl.cpp:1378-1419)
 //   y = h . H per group of G features (none, regular h4^(x)k, or Sylvester H2^(x)k), then * fl(1/sqrt(G))
 //   s = max(max|y| / 127, 1e-30); q = rint(y / s)                               (kernels/h3sycl.cpp:465-472)
 //
@@ -207,8 +209,9 @@ struct QuantArgs {
 };
 
 // ROT: the rotation kind (group size at run time); F: the side inputs (ROW_W, ROW_TAB, ROW_TAB32 or ROW_DYN, as in
-// rowcore.h), or ROW_RAW: no norm, x itself is quantized. The exact masks round h to bfloat16 (the type of the
-// reference's scratch h); ROW_DYN takes h's type at run time.
+// rowcore.h), or ROW_RAW: no norm, x itself is quantized, or ROW_SWIGLU: no norm, silu(gate) * up is quantized. The
+// exact masks round h to bfloat16 (the type of the reference's scratch h and act); ROW_DYN takes h's type at run
+// time.
 //
 // A unit (one block for rows of 256 or 512 lanes, one wavefront for 64-lane rows) quantizes the rows
 // [unit * rpu, (unit + 1) * rpu). A lane works on the same chunks of every row, so the weight and the table row are
@@ -220,7 +223,8 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
     constexpr int V = Vec<XDT>::V;
     constexpr bool DYN = F & ROW_DYN;
     constexpr bool TW = DYN || (F & ROW_TAB32);
-    constexpr bool NORM = !(F & ROW_RAW);
+    constexpr bool SWI = F & ROW_SWIGLU;
+    constexpr bool NORM = !(F & (ROW_RAW | ROW_SWIGLU));
     __shared__ float red[2][8];
     const bool has_w = DYN ? A.w != nullptr : (F & ROW_W) != 0;
     const bool has_tab = DYN ? A.scale != nullptr : (F & ROW_TAB) != 0;
@@ -239,14 +243,36 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
         ok[j] = c < nch;
         cc[j] = ok[j] ? c : nch - 1;
     }
-    auto load_row = [&](uint4 (&xr)[CPL], int64_t row) {
-        const uint4* xp = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * (16 / V));
+    // a row of x, and with SWIGLU the up half beside it (the gate half is xr)
+    auto load_row = [&](uint4 (&xr)[CPL], uint4 (&ur)[CPL], int64_t row) {
+        const uint4* xp = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * (SWI ? 2 : 1) * (16 / V));
 #pragma unroll
         for (int j = 0; j < CPL; ++j) xr[j] = xp[cc[j]];
+        if constexpr (SWI)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) ur[j] = xp[nch + cc[j]];
     };
-    // this row's and the next row's x (x0, x1) and table row indices
-    uint4 x0[CPL];
-    load_row(x0, r0);
+    // rounds a chunk to h's type (the reference's 16-bit scratch between its kernels)
+    auto round_h = [&](float (&o)[V]) {
+        if (h_dt == H3S_BF16) {
+#pragma unroll
+            for (int e = 0; e < V; e += 2) {
+                const uint32_t p = pack_bf16(o[e], o[e + 1]);
+                o[e] = bf16_lo(p);
+                o[e + 1] = bf16_hi(p);
+            }
+        } else if (h_dt == H3S_F16) {
+#pragma unroll
+            for (int e = 0; e < V; e += 2) {
+                const uint32_t p = pack_f16(o[e], o[e + 1]);
+                o[e] = f16_lo(p);
+                o[e + 1] = f16_hi(p);
+            }
+        }
+    };
+    // this row's and the next row's x (x0, x1; u0, u1 the up halves) and table row indices
+    uint4 x0[CPL], u0[CPL];
+    load_row(x0, u0, r0);
     int64_t t0 = has_tab && A.rows ? A.rows[r0] : 0;
 
     // ---- the weight and the table row, as floats: w, 1 + scale, shift ----
@@ -280,10 +306,10 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
     int slot = 0;   // consecutive reductions use alternate LDS slots
     for (int64_t row = r0; row < r1; ++row) {
         // the next row's x and table row index, in flight during this row
-        uint4 x1[CPL];
+        uint4 x1[CPL], u1[CPL];
         int64_t t1 = 0;
         if (row + 1 < r1) {
-            load_row(x1, row + 1);
+            load_row(x1, u1, row + 1);
             if (has_tab && A.rows) t1 = A.rows[row + 1];
         }
         if (has_tab && t0 != tcur) {
@@ -318,21 +344,18 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
 #pragma unroll
                     for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * s1[j][e] + sh[j][e];
                 }
-                if (h_dt == H3S_BF16) {
+                round_h(v[j]);
+            }
+        }
+        // ---- swiglu into h's type: silu(g) * u, as h3s_swiglu computes it ----
+        if constexpr (SWI) {
 #pragma unroll
-                    for (int e = 0; e < V; e += 2) {
-                        const uint32_t p = pack_bf16(v[j][e], v[j][e + 1]);
-                        v[j][e] = bf16_lo(p);
-                        v[j][e + 1] = bf16_hi(p);
-                    }
-                } else if (h_dt == H3S_F16) {
+            for (int j = 0; j < CPL; ++j) {
+                float u[V];
+                Vec<XDT>::unpack(u0[j], u);
 #pragma unroll
-                    for (int e = 0; e < V; e += 2) {
-                        const uint32_t p = pack_f16(v[j][e], v[j][e + 1]);
-                        v[j][e] = f16_lo(p);
-                        v[j][e + 1] = f16_hi(p);
-                    }
-                }
+                for (int e = 0; e < V; ++e) v[j][e] = act_silu(v[j][e]) * u[e];
+                round_h(v[j]);
             }
         }
 
@@ -370,7 +393,10 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
             }
         }
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) x0[j] = x1[j];
+        for (int j = 0; j < CPL; ++j) {
+            x0[j] = x1[j];
+            if constexpr (SWI) u0[j] = u1[j];
+        }
         t0 = t1;
     }
 }
@@ -379,14 +405,18 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
 // (configs 1 and 4), the weight with 16-bit or float32 tables (config 5's front pass, the DiT's AdaLN). Every other
 // call shape runs the ROW_DYN instantiation.
 constexpr int kQuantNone = 0, kQuantW = ROW_W, kQuantWTab = ROW_W | ROW_TAB, kQuantWTab32 = ROW_W | ROW_TAB | ROW_TAB32,
-              kQuantRaw = ROW_RAW;
+              kQuantRaw = ROW_RAW, kQuantSwiglu = ROW_SWIGLU;
+
+// what the quantizer runs on: rms_norm_mod of x, x itself, or swiglu of x
+enum QuantMode { QUANT_NORM, QUANT_RAW, QUANT_SWIGLU };
 
 // Launches the kernel for one input type; the plan comes from row_plan.
-template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, bool norm, RowPlan p) {
+template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, int mode, RowPlan p) {
     int f = (A.w ? ROW_W : 0) | (A.scale ? ROW_TAB | (A.tab_dt == H3S_F32 ? ROW_TAB32 : 0) : 0);
     if (XDT == H3S_F32 || A.h_dt != H3S_BF16 || !(f == kQuantNone || f == kQuantW || f == kQuantWTab || f == kQuantWTab32))
         f = ROW_DYN;
-    if (!norm) f = kQuantRaw;
+    if (mode == QUANT_RAW) f = kQuantRaw;
+    if (mode == QUANT_SWIGLU) f = XDT == H3S_F32 || A.h_dt != H3S_BF16 ? (ROW_SWIGLU | ROW_DYN) : kQuantSwiglu;
 #define H3_QUANT_F(CC, RR, FF)                                                                      \
     {                                                                                                \
         const PersistentLaunch R = persistent_launch(c, (const void*) quant_kernel<XDT, CC, RR, FF>, A.M, p, A.scale != nullptr); \
@@ -394,6 +424,8 @@ template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, 
     }
 #define H3_QUANT_R(CC, RR)                                                                           \
     if (f == kQuantRaw) { H3_QUANT_F(CC, RR, kQuantRaw); return launched(fn); }                     \
+    if (f == kQuantSwiglu) { H3_QUANT_F(CC, RR, kQuantSwiglu); return launched(fn); }               \
+    if (f == (ROW_SWIGLU | ROW_DYN)) { H3_QUANT_F(CC, RR, ROW_SWIGLU | ROW_DYN); return launched(fn); } \
     if constexpr (XDT != H3S_F32) {                                                                  \
         if (f == kQuantNone) { H3_QUANT_F(CC, RR, kQuantNone); return launched(fn); }               \
         if (f == kQuantW) { H3_QUANT_F(CC, RR, kQuantW); return launched(fn); }                     \

@@ -216,6 +216,21 @@ def norm_quant(x: Tensor, weight: Tensor | None, eps: float, tables: Tables | No
     dev.check(dev.api.norm_quant(dev.ctx, *args))
 
 
+def swiglu_quant(x: Tensor, q: Tensor, s: Tensor, rot: int = _api.ROT_NONE, group: int = 0,
+                 h_dtype: DType = DType.BF16) -> None:
+    """swiglu of x [M, 2C] into a virtual act (h_dtype), then the int8 quantizer (optionally rotated): q int8 [M, C],
+    s f32 [M] - swiglu (ops.rs:349-360) and the quantizer of fc2's int8 linear in one pass (dit.rs:363-364)."""
+    if not q.shape or q.dtype != DType.I8:
+        raise Error("swiglu_quant: q must be int8 [M, C]")
+    c = q.shape[-1]
+    m = q.elements() // c
+    if c == 0 or x.elements() != 2 * m * c or s.dtype != DType.F32 or s.elements() != m:
+        raise Error(f"swiglu_quant: x {x.shape} is not [M, 2C] for q {q.shape}, or s {s.dtype} {s.shape} is not [M]")
+    dev = _dev(x)
+    dev.check(dev.api.swiglu_quant(dev.ctx, x.ptr(), x.dtype.kernel_code(), m, c, h_dtype.kernel_code(), rot, group,
+                                   q.ptr(), s.ptr()))
+
+
 def norm_mod_act_gate(x: Tensor, norm: int, weight: Tensor | None, bias: Tensor | None, eps: float, tables: Tables | None,
                       act: int, res: Tensor | None, out: Tensor) -> None:
     """out = res + gate * act(norm(x) * (1 + scale) + shift), one pass."""

@@ -31,7 +31,7 @@ def declared():
 
 def test_header_and_library_agree(api):
     names = declared()
-    assert len(names) == 54
+    assert len(names) == 55          # the 49 of kernels/h3sycl.h and the 6 additions
     out = subprocess.run(["nm", "-D", "--defined-only", api.path], capture_output=True, text=True, check=True).stdout
     exported = sorted(set(l.split()[-1] for l in out.splitlines() if l.split()[-1].startswith("h3s_")))
     assert exported == names, f"missing {set(names) - set(exported)}, extra {set(exported) - set(names)}"
@@ -85,6 +85,12 @@ def test_arguments_are_checked_before_the_device(api):
     assert "power of 4" in api.error()
     assert api.norm_mod_act_gate(None, p, 2, 4, 4096, 5, None, None, 1e-5, None, None, None, None, 0, 0, None, 2, p, 2) == -1
     assert "norm" in api.error()
+    assert api.swiglu_quant(None, p, 2, 4, 4100, 2, 0, 0, p, p) == -1
+    assert "multiple of 8" in api.error()
+    assert api.swiglu_quant(None, p, 2, 4, 4096, 2, 1, 32, p, p) == -1
+    assert "power of 4" in api.error()
+    assert api.swiglu_quant(None, p, 2, 4, 4096, 2, 0, 0, p, None) == -1
+    assert "required" in api.error()
 
 
 def test_empty_shapes_do_nothing(api):
@@ -93,6 +99,7 @@ def test_empty_shapes_do_nothing(api):
     assert api.int8_linear(None, None, 2, 0, 4096, None, 8, None, 1, None, None, 2, 0) == 0
     assert api.rms_rope(None, None, 2, 4, 0, 128, 4096, None, 1e-5, None, 128) == 0
     assert api.swiglu(None, None, 2, 0, 64, None, 2) == 0
+    assert api.swiglu_quant(None, None, 2, 0, 64, 2, 0, 0, None, None) == 0
 
 
 def test_out_of_scope_entry_points_refuse(api):

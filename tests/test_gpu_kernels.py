@@ -251,6 +251,34 @@ def test_norm_quant_edge_rows(dev):
     assert s.to_numpy()[0] == np.float32(1e-30) and not q.to_numpy()[0].any()
 
 
+# ---- h3s_swiglu_quant: swiglu -> the MLP's act scratch -> fc2's quantizer, in one pass ----
+@pytest.mark.parametrize("rot,group", [(o.ROT_NONE, 0), (o.ROT_REGULAR, 256), (o.ROT_REGULAR, 16), (o.ROT_SYLVESTER, 128)])
+@pytest.mark.parametrize("x_dt,h_dt", [(o.BF16, o.BF16), (o.F16, o.F16), (o.F32, o.F32), (o.F32, o.BF16), (o.BF16, o.F32)])
+@pytest.mark.parametrize("M,C", [(23, 2048), (7, 4096), (3, 16384), (5, 64), (9, 528)])
+def test_swiglu_quant(dev, rot, group, x_dt, h_dt, M, C):
+    if group and C % group:
+        pytest.skip("group does not divide C")
+    if C % (16 // (4 if x_dt == o.F32 else 2)) or too_long(C, x_dt):
+        pytest.skip("not whole vectors, or a row longer than the kernels take")
+    x = inputs(40, M * 2 * C, x_dt, 3.0)
+    xt = up(dev, x, DTS[x_dt], [M, 2 * C])
+    q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+    ops.swiglu_quant(xt, q, s, rot=rot, group=group, h_dtype=DTS[h_dt])
+    gq, gs = q.to_numpy().ravel(), s.to_numpy()
+    # bit for bit: the library's own swiglu into act, then the oracle's quantizer on those bits
+    act = new(dev, DTS[h_dt], [M, C])
+    ops.swiglu(xt, act)
+    want_q, want_s = o.quantize_act(act.to_numpy().ravel(), h_dt, M, C, rot, group)
+    assert_bits_equal(gs, want_s, "scales")
+    codes_close(gq, want_q, "codes")
+    # against the oracle's whole chain (its expf and division): BASELINE's tolerance
+    oq, os_ = o.swiglu_quant(x, x_dt, M, C, h_dt, rot, group)
+    rel, _ = o.compare(gs, os_)
+    assert rel < 1e-3 and np.all(np.abs(gs / os_ - 1) <= 2.0 ** -7), "scales"
+    d = np.abs(gq.astype(np.int32) - oq.astype(np.int32))
+    assert d.max() <= 1 and (d > 0).mean() <= 1e-2, f"codes: {(d > 0).mean():.2e} differ by 1"
+
+
 # ---- h3s_norm_mod_act_gate (config 2's chain) ----
 @pytest.mark.parametrize("norm", [o.NORM_LAYER, o.NORM_RMS])
 @pytest.mark.parametrize("act", [o.ACT_GELU_TANH, o.ACT_SILU, o.ACT_NONE])

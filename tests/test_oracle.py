@@ -305,3 +305,24 @@ def test_fused_chains_are_compositions(oracle):
     got = oracle.norm_mod_act_gate(x, oracle.BF16, M, C, oracle.NORM_RMS, w, None, 1e-6, rows, sc, sh, gate, oracle.F32,
                                    oracle.ACT_GELU_TANH, res, oracle.BF16, oracle.BF16)
     assert np.array_equal(got, want.ravel())
+
+
+# ---- swiglu -> act -> quantizer: the fused oracle is the composition of the pinned steps ----
+@pytest.mark.parametrize("x_dt,h_dt", [(o.BF16, o.BF16), (o.F16, o.F16), (o.F32, o.F32), (o.F32, o.BF16)])
+@pytest.mark.parametrize("rot,group", [(o.ROT_NONE, 0), (o.ROT_REGULAR, 256), (o.ROT_SYLVESTER, 128)])
+def test_swiglu_quant_is_swiglu_then_quantizer(x_dt, h_dt, rot, group):
+    M, C = 5, 512
+    x = o.to_dt(np.random.default_rng(41).standard_normal(M * 2 * C).astype(np.float32) * 3, x_dt)
+    q, s = o.swiglu_quant(x, x_dt, M, C, h_dt, rot, group)
+    act = o.swiglu(x, x_dt, M, C, h_dt)
+    q2, s2 = o.quantize_act(act, h_dt, M, C, rot, group)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+    # the quantizer alone, unrotated, is h3o_quantize_rows on the values (the quantizer of h3o_int8_linear)
+    if rot == o.ROT_NONE:
+        y = o.from_dt(act, h_dt).astype(np.float32)
+        q3 = np.empty(M * C, dtype=np.int8)
+        s3 = np.empty(M, dtype=np.float32)
+        o.lib().h3o_quantize_rows(o._p(y), M, C, o._p(q3), o._p(s3))
+        assert np.array_equal(q, q3) and np.array_equal(s, s3)
+    # the invariants of the quantizer hold on the rotated act
+    assert np.all(np.abs(q.reshape(M, C)).max(1) == 127)
