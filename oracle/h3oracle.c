@@ -624,6 +624,136 @@ int h3o_norm_mod_act_gate(const void* x, int x_dt, int64_t M, int64_t C, int nor
 }
 
 /* ---- reference::compare: engine/h3-core/src/reference.rs:84-95 ---- */
+/* ---- attention: kernels/h3sycl.cpp:1676-1767 (sage), 1496-1550 (16-bit) ---- */
+void h3o_sage_quantize(const void* src, int dt, int64_t S, int64_t H, int64_t D, int64_t stride, const float* mean,
+                       int8_t* codes, float* scales) {
+    const int64_t nb = (S + 63) / 64;
+    for (int64_t h = 0; h < H; ++h)
+        for (int64_t b = 0; b < nb; ++b) {
+            const int64_t r0 = b * 64, rows = S - r0 < 64 ? S - r0 : 64;
+            float m = 0.0f;                                                      /* h3sycl.cpp:1738-1742 */
+            for (int64_t r = r0; r < r0 + rows; ++r)
+                for (int64_t d = 0; d < D; ++d) {
+                    const float x = fabsf(h3o_load(src, dt, r * stride + h * D + d) - (mean ? mean[h * D + d] : 0.0f));
+                    m = fmaxf(m, x);
+                }
+            const float inv = m > 0.0f ? 127.0f / m : 0.0f;                      /* h3sycl.cpp:1744-1745 */
+            scales[h * nb + b] = m / 127.0f;
+            for (int64_t r = r0; r < r0 + rows; ++r)
+                for (int64_t d = 0; d < D; ++d) {
+                    const float x = (h3o_load(src, dt, r * stride + h * D + d) - (mean ? mean[h * D + d] : 0.0f)) * inv;
+                    float c = roundf(x);                                         /* sycl::round: half away from zero */
+                    c = c < -127.0f ? -127.0f : c > 127.0f ? 127.0f : c;
+                    codes[(h * S + r) * D + d] = (int8_t) c;
+                }
+        }
+}
+
+typedef struct {
+    int64_t S, H, D;
+    int sage;
+    const int8_t* iq; const int8_t* ik; const float* qs; const float* ks;   /* sage */
+    const float* hq; const float* hk;                                       /* 16-bit: half values as float */
+    const float* hv;                                                        /* [H, S, D] half values as float */
+    float scale;
+    void* out; int out_dt;
+} attn_ctx;
+static void attn_rows(void* p, int64_t r0, int64_t r1) {
+    const attn_ctx* c = (const attn_ctx*) p;
+    const int64_t S = c->S, H = c->H, D = c->D, nb = (S + 63) / 64;
+    double* sc = (double*) malloc((size_t) S * sizeof(double));
+    double* acc = (double*) malloc((size_t) D * sizeof(double));
+    for (int64_t t = r0; t < r1; ++t)                 /* a row of the [S * H] (token, head) pairs */
+    {
+        const int64_t i = t / H, h = t % H;
+        double mx = -1e300;
+        for (int64_t j = 0; j < S; ++j) {
+            double v;
+            if (c->sage) {
+                int64_t a = 0;
+                const int8_t* qi = c->iq + (h * S + i) * D;
+                const int8_t* kj = c->ik + (h * S + j) * D;
+                for (int64_t d = 0; d < D; ++d) a += (int64_t) qi[d] * kj[d];
+                v = (double) a * c->qs[h * nb + i / 64] * c->ks[h * nb + j / 64] * c->scale;
+            } else {
+                double a = 0.0;
+                const float* qi = c->hq + (h * S + i) * D;
+                const float* kj = c->hk + (h * S + j) * D;
+                for (int64_t d = 0; d < D; ++d) a += (double) qi[d] * kj[d];
+                v = a * c->scale;
+            }
+            sc[j] = v;
+            if (v > mx) mx = v;
+        }
+        double l = 0.0;
+        for (int64_t d = 0; d < D; ++d) acc[d] = 0.0;
+        for (int64_t j = 0; j < S; ++j) {
+            const double w = exp(sc[j] - mx);
+            l += w;
+            const float* vj = c->hv + (h * S + j) * D;
+            for (int64_t d = 0; d < D; ++d) acc[d] += w * vj[d];
+        }
+        for (int64_t d = 0; d < D; ++d) {
+            const float ao = h3o_f16_to_f32(h3o_f32_to_f16((float) (acc[d] / l)));   /* the half result buffer */
+            h3o_store(c->out, c->out_dt, (i * H + h) * D + d, ao);
+        }
+    }
+    free(sc);
+    free(acc);
+}
+int h3o_attention(const void* q, const void* k, const void* v, int dt, int64_t S, int64_t H, int64_t D, int64_t stride,
+                  void* out, int out_dt, int sage, int8_t* iq, int8_t* ik, float* qs, float* ks, float* kmean) {
+    if (S <= 0 || H <= 0 || D <= 0) return 0;
+    if (!dt_ok(dt) || !dt_ok(out_dt)) return fail("attention: unknown element type");
+    if (stride < H * D) return fail("attention: the row stride is shorter than a row");
+    const int64_t n = S * H * D, nb = (S + 63) / 64;
+    float* hv = (float*) malloc((size_t) n * sizeof(float));
+    for (int64_t h = 0; h < H; ++h)
+        for (int64_t t = 0; t < S; ++t)
+            for (int64_t d = 0; d < D; ++d)
+                hv[(h * S + t) * D + d] = h3o_f16_to_f32(h3o_f32_to_f16(h3o_load(v, dt, t * stride + h * D + d)));
+    attn_ctx c = {S, H, D, sage, NULL, NULL, NULL, NULL, NULL, NULL, hv, 1.0f / sqrtf((float) D), out, out_dt};
+    int8_t *bq = NULL, *bk = NULL;
+    float *bqs = NULL, *bks = NULL, *bm = NULL, *fq = NULL, *fk = NULL;
+    if (sage) {
+        bq = iq ? iq : (int8_t*) malloc((size_t) n);
+        bk = ik ? ik : (int8_t*) malloc((size_t) n);
+        bqs = qs ? qs : (float*) malloc((size_t) (H * nb) * sizeof(float));
+        bks = ks ? ks : (float*) malloc((size_t) (H * nb) * sizeof(float));
+        bm = kmean ? kmean : (float*) malloc((size_t) (H * D) * sizeof(float));
+        for (int64_t hd = 0; hd < H * D; ++hd) {                                  /* h3sycl.cpp:1729-1733 */
+            float sum = 0.0f;
+            for (int64_t t = 0; t < S; ++t) sum += h3o_load(k, dt, t * stride + hd);
+            bm[hd] = sum / (float) S;
+        }
+        h3o_sage_quantize(q, dt, S, H, D, stride, NULL, bq, bqs);
+        h3o_sage_quantize(k, dt, S, H, D, stride, bm, bk, bks);
+        c.iq = bq; c.ik = bk; c.qs = bqs; c.ks = bks;
+    } else {
+        fq = (float*) malloc((size_t) n * sizeof(float));
+        fk = (float*) malloc((size_t) n * sizeof(float));
+        for (int64_t h = 0; h < H; ++h)
+            for (int64_t t = 0; t < S; ++t)
+                for (int64_t d = 0; d < D; ++d) {
+                    fq[(h * S + t) * D + d] = h3o_f16_to_f32(h3o_f32_to_f16(h3o_load(q, dt, t * stride + h * D + d)));
+                    fk[(h * S + t) * D + d] = h3o_f16_to_f32(h3o_f32_to_f16(h3o_load(k, dt, t * stride + h * D + d)));
+                }
+        c.hq = fq; c.hk = fk;
+    }
+    parallel_rows(S * H, attn_rows, &c);
+    free(hv);
+    free(fq);
+    free(fk);
+    if (sage) {
+        if (!iq) free(bq);
+        if (!ik) free(bk);
+        if (!qs) free(bqs);
+        if (!ks) free(bks);
+        if (!kmean) free(bm);
+    }
+    return 0;
+}
+
 void h3o_compare(const float* a, const float* b, int64_t n, double* rel, double* cos) {
     double d2 = 0, a2 = 0, b2 = 0, ab = 0;
     for (int64_t i = 0; i < n; ++i) {

@@ -124,6 +124,24 @@ int h3o_norm_mod_act_gate(const void* x, int x_dt, int64_t M, int64_t C, int nor
 /* the pointwise activations, float32 */
 float h3o_act(float v, int act);
 
+/* ---- attention (kernels/h3sycl.h:185-192; kernels/h3sycl.cpp:1433-1917) ----
+ * out = softmax(q . k^T / sqrt(D)) . v per head; q, k, v: S rows of H heads x D features at row stride `stride`
+ * (elements) in dt; out [S, H * D] in out_dt.
+ * sage != 0: the reference's default for S >= 8192 (h3sycl.cpp:1676-1767): k's mean over the sequence per (head,
+ *   feature) taken out (a float32 sum in token order / S), q and k - mean to int8 with one scale per head per 64
+ *   rows (m = the block's max |x|, code = clamp(round_half_away(x * fl(127 / m)), -127, 127), scale = m / 127), v in
+ *   IEEE half; scores from the exact integer products times qscale, kscale and fl(1 / sqrt(D)).
+ * sage == 0: the 16-bit form (h3sycl.cpp:1496-1550): q, k and v in IEEE half, scores times fl(1 / sqrt(D)).
+ * Both: the softmax and the weighted sum in float64 (the reference's kernels are third-party: oneDNN and Intel's
+ * ARK, whose internal rounding is not restated), the result rounded to half (the reference's ao buffer), then
+ * stored in out_dt. The int8 codes and scales of the sage form are written to iq, ik [H, S, D], qs, ks [H, nb]
+ * and kmean [H, D] when those are not NULL. */
+int h3o_attention(const void* q, const void* k, const void* v, int dt, int64_t S, int64_t H, int64_t D, int64_t stride,
+                  void* out, int out_dt, int sage, int8_t* iq, int8_t* ik, float* qs, float* ks, float* kmean);
+/* the sage form's quantization of one tensor: mean NULL for q; codes [H, S, D], scales [H, ceil(S / 64)] */
+void h3o_sage_quantize(const void* src, int dt, int64_t S, int64_t H, int64_t D, int64_t stride, const float* mean,
+                       int8_t* codes, float* scales);
+
 /* reference::compare (engine/h3-core/src/reference.rs:84-95): relative L2 error and cosine */
 void h3o_compare(const float* a, const float* b, int64_t n, double* rel, double* cos);
 

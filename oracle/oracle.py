@@ -64,6 +64,8 @@ _SIGS = {
     "h3o_norm_mod_act_gate": (i32, [vp, i32, i64, i64, i32, vp, vp, f32, vp, vp, vp, vp, i32, i32, vp, i32, vp, i32]),
     "h3o_swiglu_quant": (i32, [vp, i32, i64, i64, i32, i32, i32, vp, vp]),
     "h3o_quantize_act": (i32, [vp, i32, i64, i64, i32, i32, vp, vp]),
+    "h3o_attention": (i32, [vp, vp, vp, i32, i64, i64, i64, i64, vp, i32, i32, vp, vp, vp, vp, vp]),
+    "h3o_sage_quantize": (None, [vp, i32, i64, i64, i64, i64, vp, vp, vp]),
     "h3o_act": (f32, [f32, i32]),
     "h3o_compare": (None, [vp, vp, i64, vp, vp]),
     "h3o_last_error": (C.c_char_p, []),
@@ -288,6 +290,28 @@ def quantize_act(x, x_dt, M, C_, rot=ROT_NONE, group=0):
     s = np.empty(M, dtype=np.float32)
     _check(lib().h3o_quantize_act(_p(x), x_dt, M, C_, rot, group, _p(q), _p(s)))
     return q, s
+
+
+def attention(q, k, v, dt, S, H, D, stride=None, out_dt=BF16, sage=True):
+    """softmax(q k^T / sqrt(D)) v per head -> out [S * H * D] in out_dt; with sage also the int8 codes, scales and
+    k's mean: (out, iq [H, S, D], ik, qs [H, nb], ks, kmean [H, D])."""
+    stride = H * D if stride is None else stride
+    nb = (S + 63) // 64
+    out = np.empty(S * H * D, dtype=np_dtype(out_dt))
+    iq, ik = np.zeros(H * S * D, np.int8), np.zeros(H * S * D, np.int8)
+    qs, ks = np.zeros(H * nb, np.float32), np.zeros(H * nb, np.float32)
+    km = np.zeros(H * D, np.float32)
+    _check(lib().h3o_attention(_p(q), _p(k), _p(v), dt, S, H, D, stride, _p(out), out_dt, int(sage), _p(iq), _p(ik),
+                               _p(qs), _p(ks), _p(km)))
+    return (out, iq, ik, qs, ks, km) if sage else out
+
+
+def sage_quantize(src, dt, S, H, D, stride=None, mean=None):
+    stride = H * D if stride is None else stride
+    nb = (S + 63) // 64
+    codes, scales = np.zeros(H * S * D, np.int8), np.zeros(H * nb, np.float32)
+    lib().h3o_sage_quantize(_p(src), dt, S, H, D, stride, _p(mean), _p(codes), _p(scales))
+    return codes, scales
 
 
 def norm_mod_act_gate(x, x_dt, M, C_, norm, weight, bias, eps, rows=None, scale=None, shift=None, gate=None,

@@ -1,0 +1,100 @@
+// attention.hip - h3s_attention and h3s_attention_batch (kernels/h3sycl.h:185-197, kernels/h3sycl.cpp:1433-1917) on
+// the kernels of attn_impl.h. The form follows the reference's choice: the int8 (SageAttention) form for sequences of
+// at least H3S_SAGE_MIN_S tokens (8192) unless H3S_ATTN=onednn, the 16-bit form otherwise. Head sizes 64 and 128.
+#include <cmath>
+
+#include "attn_impl.h"
+
+namespace h3 {
+
+template <int DT>
+static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S, int64_t Sp, int64_t H, int D,
+                 int64_t stride, bool sage, int8_t* aq, int8_t* ak, uint16_t* av, float* qs, float* ks, float* km) {
+    const unsigned blocks = (unsigned) (H * (Sp / kAttnRows));
+    if (sage) {
+        const int64_t hd = H * D;
+        attn_kmean_kernel<DT><<<(unsigned) ((hd + 255) / 256), 256, 0, c->stream>>>(k, S, hd, stride, km);
+        attn_qk_prep_kernel<DT, true><<<blocks, 256, 0, c->stream>>>(q, S, Sp, D, stride, nullptr, aq, qs);
+        attn_qk_prep_kernel<DT, true><<<blocks, 256, 0, c->stream>>>(k, S, Sp, D, stride, km, ak, ks);
+    } else {
+        attn_qk_prep_kernel<DT, false><<<blocks, 256, 0, c->stream>>>(q, S, Sp, D, stride, nullptr, aq, nullptr);
+        attn_qk_prep_kernel<DT, false><<<blocks, 256, 0, c->stream>>>(k, S, Sp, D, stride, nullptr, ak, nullptr);
+    }
+    attn_v_prep_kernel<DT><<<blocks, 256, 0, c->stream>>>(v, S, Sp, D, stride, av);
+}
+
+static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, const void* v, int dt, int64_t S, int64_t H,
+                         int64_t D, int64_t stride, void* out, int out_dt) {
+    const bool sage = c->sage_want && S >= c->sage_min_s;
+    const int64_t Sp = (S + kAttnQBlock - 1) / kAttnQBlock * kAttnQBlock, nbp = Sp / kAttnRows;
+    const int64_t n = Sp * H * D, esz = sage ? 1 : 2;
+    if (H * (Sp / kAttnQBlock) > 0x7fffffff) return fail(std::string(fn) + ": too many query blocks");
+    int8_t* aq = c->grow(c->aq, c->aq_cap, (size_t) (n * esz));
+    int8_t* ak = c->grow(c->ak, c->ak_cap, (size_t) (n * esz));
+    uint16_t* av = c->grow(c->av, c->av_cap, (size_t) n);
+    float* af = c->grow(c->af, c->af_cap, (size_t) (2 * H * nbp + H * D));
+    if (!aq || !ak || !av || !af) return -1;
+    float *qs = af, *ks = af + H * nbp, *km = af + 2 * H * nbp;
+    switch (dt) {
+        case H3S_BF16: prep<H3S_BF16>(c, q, k, v, S, Sp, H, (int) D, stride, sage, aq, ak, av, qs, ks, km); break;
+        case H3S_F16: prep<H3S_F16>(c, q, k, v, S, Sp, H, (int) D, stride, sage, aq, ak, av, qs, ks, km); break;
+        default: prep<H3S_F32>(c, q, k, v, S, Sp, H, (int) D, stride, sage, aq, ak, av, qs, ks, km); break;
+    }
+    if (launched(fn)) return -1;
+    AttnArgs P;
+    P.q = aq; P.k = ak; P.vt = av; P.qs = qs; P.ks = ks;
+    P.S = S; P.Sp = Sp; P.H = H;
+    P.c = (float) (1.4426950408889634 * (double) (1.0f / std::sqrt((float) D)));
+    P.out = out; P.out_dt = out_dt;
+    P.nqb = (int) (Sp / kAttnQBlock);
+    const unsigned grid = (unsigned) (H * P.nqb);
+    if (sage) {
+        if (D == 128) attn_kernel<true, 128><<<grid, 256, 0, c->stream>>>(P);
+        else attn_kernel<true, 64><<<grid, 256, 0, c->stream>>>(P);
+    } else {
+        if (D == 128) attn_kernel<false, 128><<<grid, 256, 0, c->stream>>>(P);
+        else attn_kernel<false, 64><<<grid, 256, 0, c->stream>>>(P);
+    }
+    return launched(fn);
+}
+
+static int attention_checks(const char* fn, int dt, int64_t H, int64_t D, int64_t stride, int out_dt, const void* q,
+                            const void* k, const void* v, const void* out) {
+    if (stride < H * D) return fail(std::string(fn) + ": the row stride is shorter than a row");
+    if (!dt_ok(dt) || !dt_ok(out_dt)) return fail(std::string(fn) + ": unknown element type");
+    if (D != 64 && D != 128) return fail(std::string(fn) + ": head size " + std::to_string(D) + " (64 or 128 only)");
+    if (!q || !k || !v || !out) return fail(std::string(fn) + ": q, k, v and out are required");
+    return 0;
+}
+
+}  // namespace h3
+
+using namespace h3;
+
+H3S_EXPORT int h3s_attention(void* ctx, const void* q, const void* k, const void* v, int dt, int64_t S, int64_t H, int64_t D,
+                             int64_t stride, void* out, int out_dt) try {
+    const char* fn = "h3s_attention";
+    if (S <= 0 || H <= 0 || D <= 0) return 0;
+    if (attention_checks(fn, dt, H, D, stride, out_dt, q, k, v, out)) return -1;
+    Ctx* c = ctx_of(ctx, fn);
+    if (!c) return -1;
+    return attention_one(c, fn, q, k, v, dt, S, H, D, stride, out, out_dt);
+} catch (const std::exception& e) { return fail(e.what()); }
+
+// B sequences of S tokens: sequence b's rows start at row b S of q, k, v and out (kernels/h3sycl.cpp:1800-1815)
+H3S_EXPORT int h3s_attention_batch(void* ctx, const void* q, const void* k, const void* v, int dt, int64_t B, int64_t S,
+                                   int64_t H, int64_t D, int64_t stride, void* out, int out_dt) try {
+    const char* fn = "h3s_attention_batch";
+    if (B <= 0 || S <= 0 || H <= 0 || D <= 0) return 0;
+    if (attention_checks(fn, dt, H, D, stride, out_dt, q, k, v, out)) return -1;
+    Ctx* c = ctx_of(ctx, fn);
+    if (!c) return -1;
+    const size_t ei = (size_t) elem_size(dt), eo = (size_t) elem_size(out_dt);
+    for (int64_t b = 0; b < B; ++b) {
+        const size_t io = (size_t) (b * S * stride) * ei, oo = (size_t) (b * S * H * D) * eo;
+        if (attention_one(c, fn, (const char*) q + io, (const char*) k + io, (const char*) v + io, dt, S, H, D, stride,
+                          (char*) out + oo, out_dt))
+            return -1;
+    }
+    return 0;
+} catch (const std::exception& e) { return fail(e.what()); }

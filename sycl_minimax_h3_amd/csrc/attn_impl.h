@@ -1,0 +1,307 @@
+// attn_impl.h - attention on gfx950's matrix cores: out = softmax(q k^T / sqrt(D)) v per head (kernels/h3sycl.h:185-192),
+// in the reference's two forms (kernels/h3sycl.cpp:1676-1767 and 1496-1550):
+//   SAGE:  q and k - mean(k) as int8 with one scale per head per 64 rows (the preparation kernels below restate the
+//          reference's quantization exactly), scores on the i8 matrix cores, exact in int32;
+//   16-bit: q and k in IEEE half, scores on the f16 matrix cores with float32 accumulation.
+// Both: v in IEEE half, the softmax online in float32 (base 2), P in half, P v on the f16 matrix cores, the result
+// divided by the row sum, rounded to half (the reference's result buffer is half) and stored in out's type.
+//
+// Layouts (prepared once per call, in the context's scratch): codes or halves of q and k [H, Sp, D], v transposed to
+// half [H, D, Sp], Sp = S rounded up to 128 with zero rows. One block = 4 wavefronts = 128 queries of one head; a
+// wavefront owns 32 queries and walks all keys 64 at a time. Per 64-key tile:
+//   S^T = K Q^T:  v_mfma_i32_32x32x32_i8 (or f32_32x32x16_f16) with K as the first operand, so every lane ends with
+//                 scores of one query (lane % 32) for 32 of the 64 keys (the other 32 in lane ^ 32);
+//   softmax:      the row max needs one exchange with lane ^ 32 (v_permlane32_swap); the row sum stays a per-lane
+//                 partial until the end;
+//   O^T += V^T P^T: v_mfma_f32_32x32x16_f16 with V^T as the first operand; P's registers become the second operand
+//                 after one v_permlane32_swap per register pair (each lane then holds 8 consecutive keys).
+// K and V^T tiles go global -> LDS by direct loads (global_load_lds_dwordx4) into two stages, the next tile in flight
+// while this one is computed. Tile rows are R bytes long (R / 16 chunks); chunk c of row r sits at chunk
+// c ^ ((r / (16 / (R / 16))) % (R / 16)) of its row, so the 16-byte fragment reads of 16 consecutive rows hit distinct
+// banks.
+#pragma once
+
+#include "rowcore.h"
+
+namespace h3 {
+
+typedef int v4i_a __attribute__((ext_vector_type(4)));
+typedef int v16i_a __attribute__((ext_vector_type(16)));
+typedef float v16f_a __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h_a __attribute__((ext_vector_type(8)));
+
+constexpr int kAttnRows = 64;            // the reference's scale block (kSageBlock, h3sycl.cpp:1681) and the key tile
+constexpr int kAttnQBlock = 128;         // queries of a block
+
+// ---- preparation ----
+template <int DT> __device__ __forceinline__ float attn_elem(const void* p, int64_t i) {
+    if constexpr (DT == H3S_F32) return ((const float*) p)[i];
+    else if constexpr (DT == H3S_BF16) return bf16_lo(((const uint16_t*) p)[i]);
+    else return f16_lo(((const uint16_t*) p)[i]);
+}
+__device__ __forceinline__ uint16_t half_bits(float x) {
+    _Float16 h = (_Float16) x;
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+// k's mean over the sequence per (head, feature): a float32 sum in token order, / S (h3sycl.cpp:1729-1733)
+template <int DT>
+__global__ __launch_bounds__(256) void attn_kmean_kernel(const void* __restrict__ k, int64_t S, int64_t HD, int64_t stride,
+                                                         float* __restrict__ mean) {
+    const int64_t hd = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (hd >= HD) return;
+    float sum = 0.0f;
+    int64_t t = 0;
+    for (; t + 8 <= S; t += 8) {
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = attn_elem<DT>(k, (t + i) * stride + hd);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum = sum + x[i];
+    }
+    for (; t < S; ++t) sum = sum + attn_elem<DT>(k, t * stride + hd);
+    mean[hd] = sum / (float) S;
+}
+
+// q or k (- mean) of one head and 64 rows: SAGE to int8 codes with the block's scale (h3sycl.cpp:1735-1754), else to
+// half; rows past S become zeros (and a block entirely past S gets scale 0)
+template <int DT, bool SAGE>
+__global__ __launch_bounds__(256) void attn_qk_prep_kernel(const void* __restrict__ src, int64_t S, int64_t Sp, int D,
+                                                           int64_t stride, const float* __restrict__ mean,
+                                                           int8_t* __restrict__ dst, float* __restrict__ scales) {
+    __shared__ float red[4];
+    const int64_t nbp = Sp / kAttnRows, b = blockIdx.x % nbp, h = blockIdx.x / nbp, r0 = b * kAttnRows;
+    const int tid = threadIdx.x, n = kAttnRows * D;
+    const int64_t base = r0 * stride + h * D;
+    if constexpr (SAGE) {
+        float m = 0.0f;
+        for (int e = tid; e < n; e += 256) {
+            const int r = e / D, d = e % D;
+            if (r0 + r < S) m = fmaxf(m, fabsf(attn_elem<DT>(src, base + r * stride + d) - (mean ? mean[h * D + d] : 0.0f)));
+        }
+        m = wave_max<64>(m);
+        if ((tid & 63) == 0) red[tid >> 6] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+        if (tid == 0) scales[h * nbp + b] = m / 127.0f;
+        for (int e = tid; e < n; e += 256) {
+            const int r = e / D, d = e % D;
+            float c = 0.0f;
+            if (r0 + r < S) {
+                c = roundf((attn_elem<DT>(src, base + r * stride + d) - (mean ? mean[h * D + d] : 0.0f)) * inv);
+                c = fminf(fmaxf(c, -127.0f), 127.0f);
+            }
+            dst[(h * Sp + r0 + r) * D + d] = (int8_t) c;
+        }
+    } else {
+        uint16_t* d16 = reinterpret_cast<uint16_t*>(dst);
+        for (int e = tid; e < n; e += 256) {
+            const int r = e / D, d = e % D;
+            d16[(h * Sp + r0 + r) * D + d] = r0 + r < S ? half_bits(attn_elem<DT>(src, base + r * stride + d)) : (uint16_t) 0;
+        }
+    }
+}
+
+// v of one head and 64 tokens to half, transposed: vt [H, D, Sp]; tokens past S become zeros
+template <int DT>
+__global__ __launch_bounds__(256) void attn_v_prep_kernel(const void* __restrict__ v, int64_t S, int64_t Sp, int D,
+                                                          int64_t stride, uint16_t* __restrict__ vt) {
+    __shared__ uint16_t tile[kAttnRows * (128 + 2)];
+    const int64_t nbp = Sp / kAttnRows, b = blockIdx.x % nbp, h = blockIdx.x / nbp, t0 = b * kAttnRows;
+    const int tid = threadIdx.x, n = kAttnRows * D, pitch = D + 2;
+    for (int e = tid; e < n; e += 256) {
+        const int t = e / D, d = e % D;
+        tile[t * pitch + d] = t0 + t < S ? half_bits(attn_elem<DT>(v, (t0 + t) * stride + h * D + d)) : (uint16_t) 0;
+    }
+    __syncthreads();
+    for (int e = tid; e < n; e += 256) {
+        const int d = e / kAttnRows, t = e % kAttnRows;
+        vt[(h * D + d) * Sp + t0 + t] = tile[t * pitch + d];
+    }
+}
+
+// ---- the attention kernel ----
+struct AttnArgs {
+    const int8_t* q;          // [H, Sp, D]: int8 codes (SAGE) or half bits
+    const int8_t* k;
+    const uint16_t* vt;       // [H, D, Sp] half bits
+    const float* qs;          // [H, Sp / 64] (SAGE)
+    const float* ks;
+    int64_t S, Sp, H;
+    float c;                  // log2(e) * fl(1 / sqrt(D)): scores in base 2
+    void* out;                // [S, H * D]
+    int out_dt;
+    int nqb;                  // blocks of 128 queries per head
+};
+
+// the chunk of row r (rows of CPR 16-byte chunks) where logical chunk c is stored
+template <int CPR> __device__ __forceinline__ int attn_swz(int r, int c) { return c ^ ((r / (16 / CPR)) % CPR); }
+
+// {x of this lane, x of lane ^ 32} in some order
+__device__ __forceinline__ float attn_pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+__device__ __forceinline__ float attn_pair_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+
+template <bool SAGE, int D>
+__global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs P) {
+    constexpr int ESZ = SAGE ? 1 : 2, RB = D * ESZ, CPR = RB / 16, NQF = RB / 32;
+    constexpr int KTB = kAttnRows * RB, VTB = D * kAttnRows * 2, STAGE = KTB + VTB;
+    constexpr int NDT = D / 32;                               // 32-row tiles of V^T (32 features each)
+    __shared__ __attribute__((aligned(16))) int8_t lds[2 * STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hl = lane >> 5, ql = lane & 31;
+    const int64_t h = blockIdx.x / P.nqb, qb = blockIdx.x % P.nqb, Sp = P.Sp, S = P.S;
+    const int64_t q0 = qb * kAttnQBlock + 32 * wave;          // this wavefront's first query
+    const int64_t nbp = Sp / kAttnRows;
+    const int ntiles = (int) ((S + kAttnRows - 1) / kAttnRows);
+
+    // this lane's query fragments (second operand of the score products), held for the whole key walk
+    v4i_a qf[NQF];
+    {
+        const int8_t* qrow = P.q + ((h * Sp + q0 + ql) * D) * ESZ;
+#pragma unroll
+        for (int kk = 0; kk < NQF; ++kk) qf[kk] = *reinterpret_cast<const v4i_a*>(qrow + 32 * kk + 16 * hl);
+    }
+    const float fq = SAGE ? P.qs[h * nbp + q0 / kAttnRows] * P.c : P.c;
+
+    // direct loads of key tile t into stage st: the K rows (64 x RB bytes) and the V^T rows (D x 128 bytes)
+    const int8_t* kbase = P.k + h * Sp * RB;
+    const uint16_t* vbase = P.vt + h * D * Sp;
+    auto issue = [&](int t, int st) {
+        int8_t* s = lds + st * STAGE;
+        constexpr int KI = CPR / 4;                            // K instructions a wavefront
+#pragma unroll
+        for (int j = 0; j < KI; ++j) {
+            const int i = wave * KI + j, u = 64 * i + lane, r = u / CPR, c = attn_swz<CPR>(r, u % CPR);
+            const int8_t* g = kbase + ((int64_t) t * kAttnRows + r) * RB + 16 * c;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) g,
+                                             (__attribute__((address_space(3))) void*) (s + 1024 * i), 16, 0, 0);
+        }
+        constexpr int VI = D / 32;                              // V^T instructions a wavefront (D * 8 units / 64 / 4)
+#pragma unroll
+        for (int j = 0; j < VI; ++j) {
+            const int i = wave * VI + j, u = 64 * i + lane, r = u / 8, c = attn_swz<8>(r, u % 8);
+            const uint16_t* g = vbase + (int64_t) r * Sp + (int64_t) t * kAttnRows + 8 * c;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) g,
+                                             (__attribute__((address_space(3))) void*) (s + KTB + 1024 * i), 16, 0, 0);
+        }
+    };
+
+    v16f_a o[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) o[i] = (v16f_a) 0.0f;
+    float m = -INFINITY, l = 0.0f;
+
+    issue(0, 0);
+    for (int t = 0; t < ntiles; ++t) {
+        wait_vm<0>();
+        __syncthreads();                                       // tile t is in; every wavefront is done with tile t - 1
+        if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1);
+        const int8_t* st = lds + (t & 1) * STAGE;
+
+        // ---- scores: two 32-key halves of the tile ----
+        float x[32];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int r = 32 * j + ql;
+            if constexpr (SAGE) {
+                v16i_a a = (v16i_a) 0;
+#pragma unroll
+                for (int kk = 0; kk < NQF; ++kk) {
+                    const v4i_a kf = *reinterpret_cast<const v4i_a*>(st + (r * CPR + attn_swz<CPR>(r, 2 * kk + hl)) * 16);
+                    a = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[kk], a, 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) x[16 * j + i] = (float) a[i];
+            } else {
+                v16f_a a = (v16f_a) 0.0f;
+#pragma unroll
+                for (int kk = 0; kk < NQF; ++kk) {
+                    const v4i_a kf = *reinterpret_cast<const v4i_a*>(st + (r * CPR + attn_swz<CPR>(r, 2 * kk + hl)) * 16);
+                    a = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, kf), __builtin_bit_cast(v8h_a, qf[kk]), a, 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) x[16 * j + i] = a[i];
+            }
+        }
+        // register i of half j holds key 32 j + 8 (i / 4) + 4 hl + i % 4 of the tile
+        const float f = SAGE ? fq * P.ks[h * nbp + t] : fq;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[i] = x[i] * f;
+        if ((int64_t) (t + 1) * kAttnRows > S) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const int64_t key = (int64_t) t * kAttnRows + 32 * (i / 16) + 8 * ((i % 16) / 4) + 4 * hl + i % 4;
+                if (key >= S) x[i] = -INFINITY;
+            }
+        }
+        float mx = x[0];
+#pragma unroll
+        for (int i = 1; i < 32; ++i) mx = fmaxf(mx, x[i]);
+        mx = attn_pair_max(mx);
+        const float mn = fmaxf(m, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);
+        m = mn;
+        float ls = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            x[i] = __builtin_amdgcn_exp2f(x[i] - mn);
+            ls = ls + x[i];
+        }
+        l = __builtin_fmaf(l, alpha, ls);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[dt] = o[dt] * alpha;
+
+        // ---- O^T += V^T P^T, 16 keys a product ----
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            // keys 16 s + 4 hl + (0..3) and 16 s + 8 + 4 hl + (0..3) of this lane's query, as half pairs
+            const int b = 16 * (s / 2) + 8 * (s % 2);
+            uint32_t a0 = pack_f16(x[b + 0], x[b + 1]), a1 = pack_f16(x[b + 2], x[b + 3]);
+            uint32_t b0 = pack_f16(x[b + 4], x[b + 5]), b1 = pack_f16(x[b + 6], x[b + 7]);
+            // the upper half's first group for the lower half's second: each lane then has keys 16 s + 8 hl + (0..7)
+            const auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+            const auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+            a0 = s0[0]; b0 = s0[1]; a1 = s1[0]; b1 = s1[1];
+            v4i_a pf;
+            pf[0] = (int) a0; pf[1] = (int) a1; pf[2] = (int) b0; pf[3] = (int) b1;
+            const v8h_a pb = __builtin_bit_cast(v8h_a, pf);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const int r = 32 * dt + ql;
+                const v4i_a vf = *reinterpret_cast<const v4i_a*>(st + KTB + (r * 8 + attn_swz<8>(r, 2 * s + hl)) * 16);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, vf), pb, o[dt], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- out = O / l, rounded to half, in out's type ----
+    const float inv = 1.0f / attn_pair_sum(l);
+    const int64_t qi = q0 + ql;
+    if (qi < S) {
+        const int esz = P.out_dt == H3S_F32 ? 4 : 2;
+        char* orow = reinterpret_cast<char*>(P.out) + ((qi * P.H + h) * D) * esz;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                // registers 4 g .. 4 g + 3 of o[dt]: features 32 dt + 8 g + 4 hl + (0..3)
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = round_f16(o[dt][4 * g + i] * inv);
+                char* at = orow + (32 * dt + 8 * g + 4 * hl) * esz;
+                if (P.out_dt == H3S_F32) *reinterpret_cast<float4*>(at) = make_float4(v[0], v[1], v[2], v[3]);
+                else if (P.out_dt == H3S_BF16) *reinterpret_cast<uint2*>(at) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+                else *reinterpret_cast<uint2*>(at) = make_uint2(pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
+            }
+    }
+}
+
+}  // namespace h3

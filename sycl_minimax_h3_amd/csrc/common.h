@@ -38,6 +38,13 @@ struct Ctx {
     // scratch of h3s_int8_linear: the int8 activations and the row scales of one row chunk
     int8_t* xq = nullptr; size_t xq_cap = 0;
     float* rs = nullptr; size_t rs_cap = 0;
+    // scratch of h3s_attention: q and k prepared [H, Sp, D] (int8 or half), v as half [H, D, Sp], the scales and k's mean
+    int8_t* aq = nullptr; size_t aq_cap = 0;
+    int8_t* ak = nullptr; size_t ak_cap = 0;
+    uint16_t* av = nullptr; size_t av_cap = 0;
+    float* af = nullptr; size_t af_cap = 0;
+    bool sage_want = true;                 // H3S_ATTN=onednn: false
+    int64_t sage_min_s = 8192;             // H3S_SAGE_MIN_S
 
     // A scratch buffer of at least n elements, counted against the cap; NULL with the reason on failure.
     template <typename T> T* grow(T*& p, size_t& cap, size_t n);
@@ -83,6 +90,12 @@ template <typename T> T* Ctx::grow(T*& p, size_t& cap, size_t n) {
 // ---- device side -----------------------------------------------------------------------------------------------
 
 constexpr int kWave = 64;
+
+// waits until at most N vector-memory operations of this thread are outstanding (N a constant)
+template <int N> __device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
 // bf16 <-> f32: widen by shifting; narrow with the hardware's round-to-nearest-even (finite values: the same bits
 // as kernels/h3sycl.cpp:42-49; a NaN stays a NaN)

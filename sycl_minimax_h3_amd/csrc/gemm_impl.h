@@ -69,11 +69,6 @@ __device__ __forceinline__ void gemm_tile(int b, int tm, int tn, int* im, int* i
 // moving LDS accesses across it
 __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// waits until at most N vector-memory operations of this thread are outstanding (N a constant)
-template <int N> __device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
 
 template <int ACT, bool PER_N>
 __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {

@@ -57,6 +57,10 @@ static void init(Ctx& c) {
     if (const char* e = std::getenv("H3S_MEM_FRACTION")) frac = std::min(0.97, std::max(0.05, std::atof(e)));
     c.mem_cap = (size_t) ((double) total * frac);
     c.poison = std::getenv("H3S_POISON") != nullptr;
+    // the attention form (kernels/h3sycl.cpp:231-232): H3S_ATTN=onednn keeps every call on the 16-bit form;
+    // H3S_SAGE_MIN_S sets the shortest sequence that takes the int8 (SageAttention) form
+    if (const char* e = std::getenv("H3S_ATTN")) c.sage_want = std::strcmp(e, "onednn") != 0;
+    if (const char* e = std::getenv("H3S_SAGE_MIN_S")) c.sage_min_s = std::max<int64_t>(0, std::atoll(e));
 }
 
 static Ctx* open_on(int index) {
@@ -256,6 +260,8 @@ H3S_EXPORT void h3s_destroy(void* ctx) {
     if (c->copy_stream) { (void) hipStreamSynchronize(c->copy_stream); (void) hipStreamDestroy(c->copy_stream); }
     if (c->xq) (void) hipFree(c->xq);
     if (c->rs) (void) hipFree(c->rs);
+    for (void* p : {(void*) c->aq, (void*) c->ak, (void*) c->av, (void*) c->af})
+        if (p) (void) hipFree(p);
     for (auto& kv : c->mem) (void) hipFree(kv.first);
     if (c->own_stream) (void) hipStreamDestroy(c->stream);
     delete c;
@@ -321,10 +327,3 @@ H3S_EXPORT int h3s_aa_snake(void*, const float*, int64_t, int64_t, int64_t, cons
 }
 H3S_EXPORT int h3s_scale(void*, float*, int64_t, float) { H3S_NOT_HERE("h3s_scale", "audio"); }
 H3S_EXPORT int h3s_snake(void*, const float*, int64_t, int64_t, int64_t, const float*, float*) { H3S_NOT_HERE("h3s_snake", "audio"); }
-H3S_EXPORT int h3s_attention(void*, const void*, const void*, const void*, int, int64_t, int64_t, int64_t, int64_t, void*, int) {
-    H3S_NOT_HERE("h3s_attention", "attention");
-}
-H3S_EXPORT int h3s_attention_batch(void*, const void*, const void*, const void*, int, int64_t, int64_t, int64_t, int64_t, int64_t, void*,
-                                   int) {
-    H3S_NOT_HERE("h3s_attention_batch", "attention");
-}

@@ -133,6 +133,30 @@ def rms_rope(x: Rows, weight: Tensor, eps: float, cs: Tensor, rot_dim: int) -> N
     dev.check(dev.api.rms_rope(dev.ctx, *args))
 
 
+def attention(q: Rows, k: Rows, v: Rows, out: Tensor) -> None:
+    """softmax(q k^T / sqrt(D)) v per head; out [tokens, heads * dim] (ops.rs:436-461)."""
+    if q.layout() != k.layout() or q.layout() != v.layout():
+        raise Error("attention: q, k and v must have the same layout")
+    if out.elements() != q.tokens * q.heads * q.dim:
+        raise Error(f"attention: out {out.shape} for {q.tokens} tokens of {q.heads} x {q.dim}")
+    dev = _dev(out)
+    dev.check(dev.api.attention(dev.ctx, q.ptr(), k.ptr(), v.ptr(), q.t.dtype.kernel_code(), q.tokens, q.heads, q.dim,
+                                q.stride, out.ptr(), out.dtype.kernel_code()))
+
+
+def attention_batch(q: Rows, k: Rows, v: Rows, seqs: int, out: Tensor) -> None:
+    """attention over `seqs` equal sequences of the rows, each on its own (ops.rs:405-434)."""
+    if q.layout() != k.layout() or q.layout() != v.layout():
+        raise Error("attention_batch: q, k and v must have the same layout")
+    if seqs == 0 or q.tokens % seqs:
+        raise Error(f"attention_batch: {q.tokens} tokens are not {seqs} equal sequences")
+    if out.elements() != q.tokens * q.heads * q.dim:
+        raise Error(f"attention_batch: out {out.shape} for {q.tokens} tokens of {q.heads} x {q.dim}")
+    dev = _dev(out)
+    dev.check(dev.api.attention_batch(dev.ctx, q.ptr(), k.ptr(), v.ptr(), q.t.dtype.kernel_code(), seqs, q.tokens // seqs,
+                                      q.heads, q.dim, q.stride, out.ptr(), out.dtype.kernel_code()))
+
+
 def swiglu(x: Tensor, out: Tensor) -> None:
     """out[r, i] = silu(x[r, i]) * x[r, C + i]: x [M, 2C], out [M, C] (ops.rs:349-360)."""
     if not out.shape:

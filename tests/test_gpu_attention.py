@@ -1,0 +1,130 @@
+"""GPU parity of h3s_attention / h3s_attention_batch (kernels/h3sycl.cpp:1433-1917) against the oracle's restatement:
+the int8 (SageAttention) form and the 16-bit form, through the C ABI. The reference's kernels are third-party (Intel's
+ARK, oneDNN) and their rounding inside the softmax is not restated, so the bar is BASELINE's tolerance on the result:
+relative L2 below 1e-3 against the oracle's float64 softmax of the same quantized operands."""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from helpers import new, up
+
+pytestmark = pytest.mark.gpu
+
+from sycl_minimax_h3_amd import DType, Device, Error, Tensor, ops  # noqa: E402
+
+DTS = {o.F32: DType.F32, o.F16: DType.F16, o.BF16: DType.BF16}
+o.set_threads(8)
+
+
+def _open_with(env):
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return Device.open()
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+@pytest.fixture(scope="module")
+def dev_sage():
+    """A context that takes the int8 form at every length (H3S_SAGE_MIN_S=0)."""
+    d = _open_with({"H3S_SAGE_MIN_S": "0"})
+    yield d
+    d.close()
+
+
+@pytest.fixture(scope="module")
+def dev_16():
+    """A context that keeps every call on the 16-bit form (H3S_ATTN=onednn)."""
+    d = _open_with({"H3S_ATTN": "onednn"})
+    yield d
+    d.close()
+
+
+def qkv(seed, S, H, D, dt, stride, spread=1.0):
+    g = np.random.default_rng(seed)
+    mk = lambda: o.to_dt((g.standard_normal((S, stride)) * spread).astype(np.float32), dt).ravel()  # noqa: E731
+    return mk(), mk(), mk()
+
+
+def run(d, q, k, v, dt, S, H, D, stride, out_dt):
+    qt, kt, vt = (up(d, a, DTS[dt], [S, stride]) for a in (q, k, v))
+    out = new(d, DTS[out_dt], [S, H * D])
+    ops.attention(ops.Rows(qt, 0, stride, S, H, D), ops.Rows(kt, 0, stride, S, H, D), ops.Rows(vt, 0, stride, S, H, D), out)
+    return out.to_numpy().ravel()
+
+
+def check(got, want, out_dt, what):
+    g, w = o.from_dt(got, out_dt).astype(np.float32), o.from_dt(want, out_dt).astype(np.float32)
+    assert np.isfinite(g).all(), f"{what}: non-finite outputs"
+    rel, cos = o.compare(g, w)
+    assert rel < 1e-3 and cos > 0.99999, f"{what}: relative L2 {rel:.2e}, cos {cos:.7f}"
+
+
+@pytest.mark.parametrize("sage", [True, False])
+@pytest.mark.parametrize("dt,out_dt", [(o.BF16, o.BF16), (o.F16, o.F32), (o.F32, o.BF16)])
+@pytest.mark.parametrize("S,H,D,pad", [(64, 1, 128, 0), (130, 3, 128, 16), (257, 2, 64, 0), (1000, 2, 128, 8), (77, 4, 64, 24)])
+def test_attention(dev_sage, dev_16, sage, dt, out_dt, S, H, D, pad):
+    stride = H * D + pad
+    q, k, v = qkv(60 + S, S, H, D, dt, stride)
+    want = o.attention(q, k, v, dt, S, H, D, stride, out_dt=out_dt, sage=sage)
+    want = want[0] if sage else want
+    got = run(dev_sage if sage else dev_16, q, k, v, dt, S, H, D, stride, out_dt)
+    check(got, want, out_dt, f"{'int8' if sage else '16-bit'} S={S} H={H} D={D}")
+
+
+@pytest.mark.parametrize("sage", [True, False])
+def test_attention_peaked_and_shifted(dev_sage, dev_16, sage):
+    """Large score spreads (the online max moves a lot, most weights underflow) and a large common offset in k (the
+    int8 form takes k's mean out)."""
+    S, H, D = 300, 2, 128
+    q, k, v = qkv(70, S, H, D, o.BF16, H * D, spread=4.0)
+    k = o.to_dt(o.from_dt(k, o.BF16) + 3.0, o.BF16)
+    want = o.attention(q, k, v, o.BF16, S, H, D, out_dt=o.F32, sage=sage)
+    want = want[0] if sage else want
+    got = run(dev_sage if sage else dev_16, q, k, v, o.BF16, S, H, D, H * D, o.F32)
+    check(got, want, o.F32, "peaked")
+
+
+def test_attention_default_form_by_length(dev):
+    """The default context: below 8192 tokens the 16-bit form, from 8192 on the int8 form (kernels/h3sycl.cpp:138, 1773)."""
+    H, D = 1, 64
+    for S, sage in ((500, False), (8200, True)):
+        q, k, v = qkv(71, S, H, D, o.BF16, H * D)
+        want = o.attention(q, k, v, o.BF16, S, H, D, out_dt=o.BF16, sage=sage)
+        want = want[0] if sage else want
+        other = o.attention(q, k, v, o.BF16, S, H, D, out_dt=o.BF16, sage=not sage)
+        other = other[0] if not sage else other
+        got = run(dev, q, k, v, o.BF16, S, H, D, H * D, o.BF16)
+        check(got, want, o.BF16, f"default S={S}")
+        # and it is measurably the form named, not the other one
+        rg, _ = o.compare(o.from_dt(got, o.BF16), o.from_dt(want, o.BF16))
+        ro, _ = o.compare(o.from_dt(got, o.BF16), o.from_dt(other, o.BF16))
+        assert rg < ro, f"S={S}: closer to the other form ({rg:.2e} vs {ro:.2e})"
+
+
+def test_attention_batch(dev_16):
+    B, S, H, D = 3, 96, 2, 64
+    stride = H * D
+    q, k, v = qkv(72, B * S, H, D, o.BF16, stride)
+    qt, kt, vt = (up(dev_16, a, "BF16", [B * S, stride]) for a in (q, k, v))
+    out = new(dev_16, "BF16", [B * S, H * D])
+    ops.attention_batch(ops.Rows(qt, 0, stride, B * S, H, D), ops.Rows(kt, 0, stride, B * S, H, D),
+                        ops.Rows(vt, 0, stride, B * S, H, D), B, out)
+    got = out.to_numpy().reshape(B, S * H * D)
+    for b in range(B):
+        sl = slice(b * S * stride, (b + 1) * S * stride)
+        want = o.attention(q[sl], k[sl], v[sl], o.BF16, S, H, D, out_dt=o.BF16, sage=False)
+        check(got[b], want, o.BF16, f"sequence {b}")
+
+
+def test_attention_refuses(dev):
+    p = new(dev, "BF16", [64, 96])
+    with pytest.raises(Error, match="64 or 128"):
+        ops.attention(ops.Rows(p, 0, 96, 64, 1, 96), ops.Rows(p, 0, 96, 64, 1, 96), ops.Rows(p, 0, 96, 64, 1, 96), p)

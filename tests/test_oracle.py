@@ -326,3 +326,102 @@ def test_swiglu_quant_is_swiglu_then_quantizer(x_dt, h_dt, rot, group):
         assert np.array_equal(q, q3) and np.array_equal(s, s3)
     # the invariants of the quantizer hold on the rotated act
     assert np.all(np.abs(q.reshape(M, C)).max(1) == 127)
+
+
+# ---- attention (kernels/h3sycl.cpp:1676-1767, 1496-1550) ----
+def _attn_inputs(seed, S, H, D, dt, stride=None, spread=1.0):
+    stride = H * D if stride is None else stride
+    g = np.random.default_rng(seed)
+    mk = lambda: o.to_dt((g.standard_normal((S, stride)) * spread).astype(np.float32), dt).ravel()  # noqa: E731
+    return mk(), mk(), mk(), stride
+
+
+def test_sage_quantize_invariants():
+    """One scale per head per 64 rows; max |code| 127 in every nonzero block; |x - code * scale| <= scale / 2 up to
+    the rounding of x * (127 / m); exact halves round away from zero; a zero block has scale 0 and codes 0."""
+    S, H, D = 150, 3, 64
+    x = np.random.default_rng(50).standard_normal((S, H * D)).astype(np.float32)
+    x[64:128, D:2 * D] = 0.0                         # head 1, block 1: zeros
+    codes, scales = o.sage_quantize(x.ravel(), o.F32, S, H, D)
+    nb = 3
+    c = codes.reshape(H, S, D).astype(np.int32)
+    sc = scales.reshape(H, nb)
+    for h in range(H):
+        for b in range(nb):
+            blk = x[b * 64:(b + 1) * 64, h * D:(h + 1) * D]
+            cb = c[h, b * 64:(b + 1) * 64]
+            if not blk.any():
+                assert sc[h, b] == 0 and not cb.any()
+                continue
+            assert sc[h, b] == np.float32(np.float32(np.abs(blk).max()) / np.float32(127))
+            assert np.abs(cb).max() == 127
+            err = np.abs(blk.astype(np.float64) - cb * np.float64(sc[h, b]))
+            assert err.max() <= sc[h, b] * (0.5 + 1e-4)
+    # halves: x * 127 / m lands exactly on k + 0.5 for x = (k + 0.5) m / 127 with m = 127 (inv = 1)
+    y = np.zeros((64, 4), np.float32)
+    y[0, 0] = 127.0
+    y[1, :] = [2.5, -2.5, 0.5, -0.5]
+    codes, scales = o.sage_quantize(y.ravel(), o.F32, 64, 1, 4)
+    assert scales[0] == 1.0
+    assert list(codes.reshape(64, 4)[1]) == [3, -3, 1, -1]
+
+
+def test_sage_mean_is_a_float32_sum_in_token_order():
+    S, H, D = 300, 2, 64
+    q, k, v, _ = _attn_inputs(51, S, H, D, o.BF16)
+    _, _, _, _, _, km = o.attention(q, k, v, o.BF16, S, H, D, sage=True)
+    kf = o.from_dt(k, o.BF16).reshape(S, H * D)
+    want = (np.add.accumulate(kf, axis=0, dtype=np.float32)[-1] / np.float32(S)).astype(np.float32)
+    assert np.array_equal(km, want)
+
+
+@pytest.mark.parametrize("sage", [True, False])
+def test_attention_special_cases(sage):
+    H, D = 2, 64
+    # one token: the softmax is 1, out = v (through half)
+    q, k, v, _ = _attn_inputs(52, 1, H, D, o.F32)
+    out = o.attention(q, k, v, o.F32, 1, H, D, out_dt=o.F32, sage=sage)
+    out = out[0] if sage else out
+    assert np.array_equal(out, o.from_dt(o.to_dt(v, o.F16), o.F16))
+    # identical keys: uniform weights, out = the mean of v (within half's rounding)
+    S = 96
+    q, _, v, _ = _attn_inputs(53, S, H, D, o.F32)
+    k = np.tile(np.random.default_rng(54).standard_normal(H * D).astype(np.float32), S)
+    out = o.attention(q, k, v, o.F32, S, H, D, out_dt=o.F32, sage=sage)
+    out = out[0] if sage else out
+    vh = o.from_dt(o.to_dt(v, o.F16), o.F16).reshape(S, H * D).astype(np.float64)
+    assert np.allclose(out.reshape(S, H * D), vh.mean(0)[None, :], rtol=2e-3, atol=2e-3)
+    # one key far above the rest: out = that key's v
+    q = np.ones(S * H * D, np.float32)
+    k = -np.ones(S * H * D, np.float32)
+    k.reshape(S, H * D)[37] = 1.0
+    out = o.attention(q, k, v, o.F32, S, H, D, out_dt=o.F32, sage=sage)
+    out = out[0] if sage else out
+    assert np.allclose(out.reshape(S, H * D), vh[37][None, :], rtol=1e-3, atol=1e-3)
+
+
+def test_attention_against_dense_softmax():
+    """The 16-bit form against an independent dense formulation (numpy matmul + softmax over half values), and the
+    sage form against the same formulation on its dequantized q and k - mean (the mean cancels in the softmax)."""
+    S, H, D, stride = 130, 3, 64, 3 * 64 + 16
+    q, k, v, _ = _attn_inputs(55, S, H, D, o.BF16, stride)
+    half = lambda a: o.from_dt(o.to_dt(o.from_dt(a, o.BF16), o.F16), o.F16).reshape(S, stride)[:, :H * D].reshape(S, H, D).astype(np.float64)  # noqa: E731
+    qh, kh, vh = half(q), half(k), half(v)
+    sm = np.float32(1) / np.sqrt(np.float32(D))
+
+    def dense(qq, kk, vv):
+        s = np.einsum("shd,thd->hst", qq, kk) * float(sm)
+        s -= s.max(-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(-1, keepdims=True)
+        return np.einsum("hst,thd->shd", p, vv).reshape(S, H * D)
+
+    out16 = o.attention(q, k, v, o.BF16, S, H, D, stride, out_dt=o.F32, sage=False)
+    assert np.allclose(out16.reshape(S, H * D), dense(qh, kh, vh), rtol=1e-3, atol=1e-3)
+    out, iq, ik, qs, ks, km = o.attention(q, k, v, o.BF16, S, H, D, stride, out_dt=o.F32, sage=True)
+    nb = (S + 63) // 64
+    deq = lambda c, s_: (c.reshape(H, S, D).astype(np.float64) * np.repeat(s_.reshape(H, nb), 64, 1)[:, :S, None]).transpose(1, 0, 2)  # noqa: E731
+    assert np.allclose(out.reshape(S, H * D), dense(deq(iq, qs), deq(ik, ks), vh), rtol=1e-3, atol=1e-3)
+    # and the sage result stays close to the exact attention (the quantization error of q and k)
+    rel, cos = o.compare(out.astype(np.float32), dense(qh, kh, vh).astype(np.float32).ravel())
+    assert rel < 0.05 and cos > 0.998
