@@ -27,6 +27,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_GBS = 8000.0          # MI355X HBM3E
 PEAK_I8_TOPS = 5000.0      # MI355X dense int8 matrix peak
+PEAK_F16_TFLOPS = 2500.0   # MI355X dense fp16 / bf16 matrix peak
 
 M2 = 16 * 24 * 44          # 16896 tokens (T16 x H24 x W44)
 M4 = 47104
@@ -43,6 +44,7 @@ def bytes_cfg():
         "cfg5a_rmsnorm_mod_quant_47104": M4 * C * 2 + M4 * C + M4 * 4,
         "cfg5b_int8_gemm_silu_47104x16384": M4 * C + 16384 * C + M4 * 4 + 16384 * 4 + M4 * 16384 * 2,
         "mlp_swiglu_quant_g256_47104x8192": M4 * 16384 * 2 + M4 * 8192 + M4 * 4,
+        "attn_sage_16896x32x128": 4 * M2 * 4096 * 2,     # q, k, v read, out written (the products are the bound)
     }
 
 
@@ -188,6 +190,13 @@ def main() -> int:
     X6, Q6, S6 = O5, T(q6), T(s6)    # the GEMM's output rows are [gate | up] halves of 8192
     run("mlp_swiglu_quant_g256_47104x8192", lambda: ops.swiglu_quant(X6, Q6, S6, rot=A.ROT_REGULAR, group=256))
 
+    # ---- attention of the 16896-token grid, 32 heads of 128 (the int8 form: S >= 8192) ----
+    qkv7 = bf16(M2, 3 * 4096)
+    o7 = torch.empty(M2, 4096, dtype=torch.bfloat16, device=dev_t)
+    QKV7, O7 = T(qkv7), T(o7)
+    rows7 = [ops.Rows(QKV7, i * 4096, 3 * 4096, M2, 32, 128) for i in range(3)]
+    run("attn_sage_16896x32x128", lambda: ops.attention(*rows7, O7), 10)
+
     copy = None
     if args.copy_probe:
         src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev_t).fill_(1.0)
@@ -203,6 +212,11 @@ def main() -> int:
         if k.startswith("cfg5b"):
             tops = 2 * M4 * C * 16384 / (ms * 1e-3) / 1e12
             e.update({"TOPS_i8": round(tops, 1), "frac_i8_peak": round(tops / PEAK_I8_TOPS, 4)})
+        if k.startswith("attn"):
+            # q k^T on the i8 cores (5 POPS) and P v on the f16 cores (2.5 PFLOP/s): the time both take at peak
+            half_ops = 2.0 * M2 * M2 * 4096
+            t_peak = half_ops / (PEAK_I8_TOPS * 1e12) + half_ops / (PEAK_F16_TFLOPS * 1e12)
+            e.update({"TOPS": round(2 * half_ops / (ms * 1e-3) / 1e12, 1), "frac_mfma_peak": round(t_peak / (ms * 1e-3), 4)})
         per[k] = e
 
     value = B["cfg2_ln_mod_gelu_gate_16896"] / (ms2 * 1e-3) / 1e9

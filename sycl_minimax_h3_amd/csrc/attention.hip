@@ -13,7 +13,10 @@ static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S,
     const unsigned blocks = (unsigned) (H * (Sp / kAttnRows));
     if (sage) {
         const int64_t hd = H * D;
-        attn_kmean_kernel<DT><<<(unsigned) ((hd + 255) / 256), 256, 0, c->stream>>>(k, S, hd, stride, km);
+        if (aligned16(k) && (stride * elem_size(DT)) % 16 == 0)
+            attn_kmean_kernel<DT><<<(unsigned) (hd / 64), 256, 0, c->stream>>>(k, S, stride, km);
+        else
+            attn_kmean_rows_kernel<DT><<<(unsigned) ((hd + 255) / 256), 256, 0, c->stream>>>(k, S, hd, stride, km);
         attn_qk_prep_kernel<DT, true><<<blocks, 256, 0, c->stream>>>(q, S, Sp, D, stride, nullptr, aq, qs);
         attn_qk_prep_kernel<DT, true><<<blocks, 256, 0, c->stream>>>(k, S, Sp, D, stride, km, ak, ks);
     } else {

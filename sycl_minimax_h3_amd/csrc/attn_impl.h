@@ -21,6 +21,8 @@
 // banks.
 #pragma once
 
+#include <type_traits>
+
 #include "rowcore.h"
 
 namespace h3 {
@@ -29,6 +31,8 @@ typedef int v4i_a __attribute__((ext_vector_type(4)));
 typedef int v16i_a __attribute__((ext_vector_type(16)));
 typedef float v16f_a __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h_a __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_a __attribute__((ext_vector_type(2)));
+constexpr h2_a h2_one = {(_Float16) 1.0f, (_Float16) 1.0f};
 
 constexpr int kAttnRows = 64;            // the reference's scale block (kSageBlock, h3sycl.cpp:1681) and the key tile
 constexpr int kAttnQBlock = 128;         // queries of a block
@@ -46,10 +50,58 @@ __device__ __forceinline__ uint16_t half_bits(float x) {
     return b;
 }
 
-// k's mean over the sequence per (head, feature): a float32 sum in token order, / S (h3sycl.cpp:1729-1733)
+// k's mean over the sequence per (head, feature): a float32 sum in token order, / S (h3sycl.cpp:1729-1733). A block
+// takes 64 features: all 256 threads stage 32 KiB of rows at a time into LDS with 16-byte loads (the next stage in
+// flight), and the first wavefront runs the 64 sums, one feature a lane, in token order. Needs the rows 16-byte
+// aligned (k and the stride); attn_kmean_rows_kernel is the general form.
 template <int DT>
-__global__ __launch_bounds__(256) void attn_kmean_kernel(const void* __restrict__ k, int64_t S, int64_t HD, int64_t stride,
+__global__ __launch_bounds__(256) void attn_kmean_kernel(const void* __restrict__ k, int64_t S, int64_t stride,
                                                          float* __restrict__ mean) {
+    constexpr int ESZ = DT == H3S_F32 ? 4 : 2, ROWS = 32768 / (64 * ESZ), CPR = 64 * ESZ / 16, LOADS = ROWS * CPR / 256;
+    __shared__ uint4 buf[2][ROWS * CPR];
+    const int tid = threadIdx.x;
+    const int64_t c0 = (int64_t) blockIdx.x * 64, nch = (S + ROWS - 1) / ROWS;
+    const char* base = reinterpret_cast<const char*>(k) + c0 * ESZ;
+    uint4 reg[LOADS];
+    auto load = [&](int64_t ch) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int u = tid + 256 * i, r = u / CPR, cc = u % CPR;
+            const int64_t row = ch * ROWS + r;
+            reg[i] = row < S ? *reinterpret_cast<const uint4*>(base + row * stride * ESZ + 16 * cc) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto store = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) buf[st][tid + 256 * i] = reg[i];
+    };
+    float sum = 0.0f;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int64_t ch = 0; ch < nch; ++ch) {
+        if (ch + 1 < nch) load(ch + 1);
+        if (tid < 64) {
+            const int rows = S - ch * ROWS < ROWS ? (int) (S - ch * ROWS) : ROWS;
+            const char* b = reinterpret_cast<const char*>(buf[ch & 1]) + tid * ESZ;
+            for (int r = 0; r < rows; ++r) {
+                const char* e = b + r * 64 * ESZ;
+                float x;
+                if constexpr (DT == H3S_F32) x = *reinterpret_cast<const float*>(e);
+                else if constexpr (DT == H3S_BF16) x = bf16_lo(*reinterpret_cast<const uint16_t*>(e));
+                else x = f16_lo(*reinterpret_cast<const uint16_t*>(e));
+                sum = sum + x;
+            }
+        }
+        if (ch + 1 < nch) store((ch + 1) & 1);
+        __syncthreads();
+    }
+    if (tid < 64) mean[c0 + tid] = sum / (float) S;
+}
+// the same sums with element loads, for rows that are not 16-byte aligned
+template <int DT>
+__global__ __launch_bounds__(256) void attn_kmean_rows_kernel(const void* __restrict__ k, int64_t S, int64_t HD, int64_t stride,
+                                                              float* __restrict__ mean) {
     const int64_t hd = (int64_t) blockIdx.x * 256 + threadIdx.x;
     if (hd >= HD) return;
     float sum = 0.0f;
@@ -151,7 +203,7 @@ __device__ __forceinline__ float attn_pair_sum(float x) {
 }
 
 template <bool SAGE, int D>
-__global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs P) {
+__global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
     constexpr int ESZ = SAGE ? 1 : 2, RB = D * ESZ, CPR = RB / 16, NQF = RB / 32;
     constexpr int KTB = kAttnRows * RB, VTB = D * kAttnRows * 2, STAGE = KTB + VTB;
     constexpr int NDT = D / 32;                               // 32-row tiles of V^T (32 features each)
@@ -199,8 +251,9 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs P) {
     for (int i = 0; i < NDT; ++i) o[i] = (v16f_a) 0.0f;
     float m = -INFINITY, l = 0.0f;
 
-    issue(0, 0);
-    for (int t = 0; t < ntiles; ++t) {
+    // one 64-key tile; TAIL: the last tile, which holds keys past S
+    auto step = [&](int t, auto tail_tag) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
         wait_vm<0>();
         __syncthreads();                                       // tile t is in; every wavefront is done with tile t - 1
         if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1);
@@ -231,33 +284,37 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs P) {
                 for (int i = 0; i < 16; ++i) x[16 * j + i] = a[i];
             }
         }
-        // register i of half j holds key 32 j + 8 (i / 4) + 4 hl + i % 4 of the tile
+        // register i of half j holds key 32 j + 8 (i / 4) + 4 hl + i % 4 of the tile. The scale f > 0 is applied after
+        // the max (max(a f) = f max(a)) and inside the exponent: p = 2^(a f - m) with one fused multiply-add.
         const float f = SAGE ? fq * P.ks[h * nbp + t] : fq;
+        // key of register i, less than `lim` for the keys inside the sequence
+        const int lim = (int) (S - (int64_t) t * kAttnRows) - 4 * hl;
+        auto live = [&](int i) { return 32 * (i / 16) + 8 * ((i % 16) / 4) + i % 4 < lim; };
+        if constexpr (TAIL) {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) x[i] = x[i] * f;
-        if ((int64_t) (t + 1) * kAttnRows > S) {
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                const int64_t key = (int64_t) t * kAttnRows + 32 * (i / 16) + 8 * ((i % 16) / 4) + 4 * hl + i % 4;
-                if (key >= S) x[i] = -INFINITY;
-            }
+            for (int i = 0; i < 32; ++i)
+                if (!live(i)) x[i] = -INFINITY;
         }
         float mx = x[0];
 #pragma unroll
         for (int i = 1; i < 32; ++i) mx = fmaxf(mx, x[i]);
-        mx = attn_pair_max(mx);
+        mx = attn_pair_max(mx) * f;
         const float mn = fmaxf(m, mx);
         const float alpha = __builtin_amdgcn_exp2f(m - mn);
         m = mn;
-        float ls = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            x[i] = __builtin_amdgcn_exp2f(x[i] - mn);
-            ls = ls + x[i];
+        for (int i = 0; i < 32; ++i) x[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], f, -mn));
+        if constexpr (TAIL) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                if (!live(i)) x[i] = 0.0f;
         }
-        l = __builtin_fmaf(l, alpha, ls);
+        // O and l carry the scale of the running max; rescale only when some lane's max moved
+        if (__any(alpha != 1.0f)) {
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) o[dt] = o[dt] * alpha;
+            for (int dt = 0; dt < NDT; ++dt) o[dt] = o[dt] * alpha;
+        }
+        float ls = 0.0f;
 
         // ---- O^T += V^T P^T, 16 keys a product ----
 #pragma unroll
@@ -266,6 +323,11 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs P) {
             const int b = 16 * (s / 2) + 8 * (s % 2);
             uint32_t a0 = pack_f16(x[b + 0], x[b + 1]), a1 = pack_f16(x[b + 2], x[b + 3]);
             uint32_t b0 = pack_f16(x[b + 4], x[b + 5]), b1 = pack_f16(x[b + 6], x[b + 7]);
+            // the row sum of the weights as rounded to half (the ones P v uses), two at a time
+            ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, a0), h2_one, ls, false);
+            ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, a1), h2_one, ls, false);
+            ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, b0), h2_one, ls, false);
+            ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, b1), h2_one, ls, false);
             // the upper half's first group for the lower half's second: each lane then has keys 16 s + 8 hl + (0..7)
             const auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
             const auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
@@ -280,7 +342,12 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs P) {
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, vf), pb, o[dt], 0, 0, 0);
             }
         }
-    }
+        l = __builtin_fmaf(l, alpha, ls);
+    };
+    issue(0, 0);
+    const int full = (int) (S / kAttnRows);                    // tiles with no key past S
+    for (int t = 0; t < full; ++t) step(t, std::false_type{});
+    if (full < ntiles) step(full, std::true_type{});
 
     // ---- out = O / l, rounded to half, in out's type ----
     const float inv = 1.0f / attn_pair_sum(l);

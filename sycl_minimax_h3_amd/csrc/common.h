@@ -114,11 +114,13 @@ __device__ __forceinline__ float round_bf16(float v) { return bf16_lo(pack_bf16(
 __device__ __forceinline__ float f16_lo(uint32_t u) { _Float16 h; uint16_t b = (uint16_t) u; __builtin_memcpy(&h, &b, 2); return (float) h; }
 __device__ __forceinline__ float f16_hi(uint32_t u) { return f16_lo(u >> 16); }
 __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
-    _Float16 ha = (_Float16) a, hb = (_Float16) b;
-    uint16_t ua, ub;
-    __builtin_memcpy(&ua, &ha, 2);
-    __builtin_memcpy(&ub, &hb, 2);
-    return (uint32_t) ua | ((uint32_t) ub << 16);
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    f2 v = {a, b};
+    h2 r = __builtin_convertvector(v, h2);          // v_cvt_pk_f16_f32: both halves, round to nearest even
+    uint32_t u;
+    __builtin_memcpy(&u, &r, 4);
+    return u;
 }
 __device__ __forceinline__ float round_f16(float v) { return (float) (_Float16) v; }
 
