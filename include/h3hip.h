@@ -175,6 +175,17 @@ int h3s_norm_quant(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, con
 int h3s_swiglu_quant(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, int h_dt, int rot, int group, int8_t* q,
                      float* s);
 
+/* What a sampler step fixes for every block, on the device instead of the reference's host loops:
+ * h3s_adaln_tables (engine/h3-core/src/dit.rs:155-174, Block::tables): the six AdaLN tables of one block for R timestep
+ *   embeddings t_emb [R, t_dim]; w [6 m C, t_dim], b [6 m C] (the block's adaln_proj), all float32;
+ *   out [6, R * m, C]: table ci (shift, scale, gate of the attention half, then of the MLP half) at out + ci R m C, row
+ *   r m + mi, value b[o] + sum_k w[o, k] t[r, k] with o = mi 6 C + ci C + i, summed in k order in float32.
+ * h3s_rotations (engine/h3-core/src/dit.rs:188-203, rotations): cs [S, 3 n, 2] float32, the (cos, sin) of
+ *   fl((float) positions[s, a] * inv_freq[f]) for the axes a = 0, 1, 2 in turn; positions float64 [S, 3]. */
+int h3s_adaln_tables(void* ctx, const float* w, const float* b, const float* t_emb, int64_t R, int64_t t_dim, int64_t m,
+                     int64_t C, float* out);
+int h3s_rotations(void* ctx, const double* positions, int64_t S, const float* inv_freq, int64_t n, float* cs);
+
 /* out = res + gate * act(norm(x) * (1 + scale) + shift), in one pass; norm RMS (x * inv_rms * weight) or LAYER
  * ((x - mean) * inv_std * weight + bias); weight, bias float32 [C] or NULL; tables [R, C] in tab_dt with rows as in
  * h3s_norm_quant; gate NULL: 1; res NULL: none. Everything in float32, one rounding to out_dt at the end. */

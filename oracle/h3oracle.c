@@ -754,6 +754,30 @@ int h3o_attention(const void* q, const void* k, const void* v, int dt, int64_t S
     return 0;
 }
 
+/* ---- a step's tables: engine/h3-core/src/dit.rs:155-174 and 188-203 ---- */
+void h3o_adaln_tables(const float* w, const float* b, const float* t_emb, int64_t R, int64_t t_dim, int64_t m, int64_t C,
+                      float* out) {
+    for (int64_t r = 0; r < R; ++r)
+        for (int64_t mi = 0; mi < m; ++mi)
+            for (int64_t ci = 0; ci < 6; ++ci)
+                for (int64_t i = 0; i < C; ++i) {
+                    const int64_t o = mi * 6 * C + ci * C + i;
+                    float sum = -0.0f;                                   /* dit.rs:168-169: iter().zip().map().sum() */
+                    for (int64_t k = 0; k < t_dim; ++k) sum = sum + w[o * t_dim + k] * t_emb[r * t_dim + k];
+                    out[ci * R * m * C + (r * m + mi) * C + i] = b[o] + sum;
+                }
+}
+void h3o_rotations(const double* positions, int64_t S, const float* inv_freq, int64_t n, float* cs) {
+    float* p = cs;
+    for (int64_t s = 0; s < S; ++s)
+        for (int a = 0; a < 3; ++a)
+            for (int64_t f = 0; f < n; ++f) {
+                const float ang = (float) positions[s * 3 + a] * inv_freq[f];   /* dit.rs:196 */
+                *p++ = cosf(ang);
+                *p++ = sinf(ang);
+            }
+}
+
 void h3o_compare(const float* a, const float* b, int64_t n, double* rel, double* cos) {
     double d2 = 0, a2 = 0, b2 = 0, ab = 0;
     for (int64_t i = 0; i < n; ++i) {

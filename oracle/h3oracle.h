@@ -142,6 +142,16 @@ int h3o_attention(const void* q, const void* k, const void* v, int dt, int64_t S
 void h3o_sage_quantize(const void* src, int dt, int64_t S, int64_t H, int64_t D, int64_t stride, const float* mean,
                        int8_t* codes, float* scales);
 
+/* ---- a step's tables (engine/h3-core/src/dit.rs:155-203) ----
+ * adaln_tables: the six AdaLN tables of one block for R timestep embeddings t_emb [R, t_dim]:
+ *   out[ci][(r * m + mi) * C + i] = b[o] + sum_k fl(w[o * t_dim + k] * t[r * t_dim + k]), o = mi 6 C + ci C + i,
+ *   the sum in k order from -0.0 in float32 (Rust's f32 Sum); out is [6, R * m, C].
+ * rotations: (cos, sin) of fl((float) pos * inv_freq[f]) for each token's three axes in order: cs [S, 3 n, 2] with
+ *   positions float64 [S, 3] (cosf / sinf of the C library, which Rust's f32::cos and f32::sin call). */
+void h3o_adaln_tables(const float* w, const float* b, const float* t_emb, int64_t R, int64_t t_dim, int64_t m, int64_t C,
+                      float* out);
+void h3o_rotations(const double* positions, int64_t S, const float* inv_freq, int64_t n, float* cs);
+
 /* reference::compare (engine/h3-core/src/reference.rs:84-95): relative L2 error and cosine */
 void h3o_compare(const float* a, const float* b, int64_t n, double* rel, double* cos);
 

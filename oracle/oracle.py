@@ -66,6 +66,8 @@ _SIGS = {
     "h3o_quantize_act": (i32, [vp, i32, i64, i64, i32, i32, vp, vp]),
     "h3o_attention": (i32, [vp, vp, vp, i32, i64, i64, i64, i64, vp, i32, i32, vp, vp, vp, vp, vp]),
     "h3o_sage_quantize": (None, [vp, i32, i64, i64, i64, i64, vp, vp, vp]),
+    "h3o_adaln_tables": (None, [vp, vp, vp, i64, i64, i64, i64, vp]),
+    "h3o_rotations": (None, [vp, i64, vp, i64, vp]),
     "h3o_act": (f32, [f32, i32]),
     "h3o_compare": (None, [vp, vp, i64, vp, vp]),
     "h3o_last_error": (C.c_char_p, []),
@@ -312,6 +314,21 @@ def sage_quantize(src, dt, S, H, D, stride=None, mean=None):
     codes, scales = np.zeros(H * S * D, np.int8), np.zeros(H * nb, np.float32)
     lib().h3o_sage_quantize(_p(src), dt, S, H, D, stride, _p(mean), _p(codes), _p(scales))
     return codes, scales
+
+
+def adaln_tables(w, b, t_emb, R, t_dim, m, C_):
+    """the six AdaLN tables [6, R * m, C] of one block (dit.rs:155-174)"""
+    out = np.empty(6 * R * m * C_, np.float32)
+    lib().h3o_adaln_tables(_p(w), _p(b), _p(t_emb), R, t_dim, m, C_, _p(out))
+    return out
+
+
+def rotations(positions, S, inv_freq):
+    """(cos, sin) [S, 3 n, 2] of each token's three axes (dit.rs:188-203)"""
+    n = inv_freq.size
+    cs = np.empty(S * 3 * n * 2, np.float32)
+    lib().h3o_rotations(_p(np.ascontiguousarray(positions, np.float64)), S, _p(inv_freq), n, _p(cs))
+    return cs
 
 
 def norm_mod_act_gate(x, x_dt, M, C_, norm, weight, bias, eps, rows=None, scale=None, shift=None, gate=None,

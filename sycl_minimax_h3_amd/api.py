@@ -78,6 +78,8 @@ ADDITIONS = {
     "h3s_stream": (vp, [vp]),
     "h3s_norm_quant": (i32, [vp, vp, i32, i64, i64, vp, f32, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "h3s_swiglu_quant": (i32, [vp, vp, i32, i64, i64, i32, i32, i32, vp, vp]),
+    "h3s_adaln_tables": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, vp]),
+    "h3s_rotations": (i32, [vp, vp, i64, vp, i64, vp]),
     "h3s_norm_mod_act_gate": (i32, [vp, vp, i32, i64, i64, i32, vp, vp, f32, vp, vp, vp, vp, i32, i32, vp, i32, vp, i32]),
     "h3s_qk_rms_rope": (i32, [vp, vp, vp, i32, i64, i64, i64, i64, vp, vp, f32, vp, i32]),
     "h3s_int8_gemm_dequant": (i32, [vp, vp, vp, i64, i64, vp, i64, vp, i64, vp, i32, vp, i32]),

@@ -157,6 +157,33 @@ def attention_batch(q: Rows, k: Rows, v: Rows, seqs: int, out: Tensor) -> None:
                                       q.heads, q.dim, q.stride, out.ptr(), out.dtype.kernel_code()))
 
 
+def adaln_tables(w: Tensor, b: Tensor, t_emb: Tensor, modalities: int, out: Tensor) -> None:
+    """The six AdaLN tables of one block (dit.rs:155-174) on the device: w [6 m C, t_dim], b [6 m C], t_emb
+    [R, t_dim] float32; out float32 [6, R * m, C]."""
+    if not t_emb.shape or not w.shape or len(w.shape) != 2:
+        raise Error("adaln_tables: w [6 m C, t_dim] and t_emb [R, t_dim]")
+    t_dim = w.shape[1]
+    if t_emb.shape[-1] != t_dim or w.shape[0] % (6 * modalities) or b.elements() != w.shape[0]:
+        raise Error(f"adaln_tables: w {w.shape}, b {b.shape}, t_emb {t_emb.shape} for {modalities} modalities")
+    c = w.shape[0] // (6 * modalities)
+    r = t_emb.elements() // t_dim
+    if out.elements() != 6 * r * modalities * c or any(t.dtype != DType.F32 for t in (w, b, t_emb, out)):
+        raise Error(f"adaln_tables: out {out.shape} is not float32 [6, {r * modalities}, {c}]")
+    dev = _dev(out)
+    dev.check(dev.api.adaln_tables(dev.ctx, w.ptr(), b.ptr(), t_emb.ptr(), r, t_dim, modalities, c, out.ptr()))
+
+
+def rotations(positions: Tensor, inv_freq: Tensor, cs: Tensor) -> None:
+    """(cos, sin) of every token's three position axes (dit.rs:188-203) on the device: positions float64 [S, 3],
+    inv_freq float32 [n], cs float32 [S, 3 n, 2]."""
+    s = positions.elements() // 3
+    n = inv_freq.elements()
+    if positions.dtype != DType.F64 or inv_freq.dtype != DType.F32 or cs.dtype != DType.F32 or cs.elements() != s * 3 * n * 2:
+        raise Error(f"rotations: positions {positions.dtype} {positions.shape}, inv_freq {inv_freq.shape}, cs {cs.shape}")
+    dev = _dev(cs)
+    dev.check(dev.api.rotations(dev.ctx, positions.ptr(), s, inv_freq.ptr(), n, cs.ptr()))
+
+
 def swiglu(x: Tensor, out: Tensor) -> None:
     """out[r, i] = silu(x[r, i]) * x[r, C + i]: x [M, 2C], out [M, C] (ops.rs:349-360)."""
     if not out.shape:
