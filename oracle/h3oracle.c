@@ -754,6 +754,30 @@ int h3o_attention(const void* q, const void* k, const void* v, int dt, int64_t S
     return 0;
 }
 
+/* ---- plain linear layers: kernels/h3sycl.cpp:656-739 ---- */
+typedef struct { const void* x; int dt; int64_t K; const void* w; int64_t N; const float* bias; void* out; int out_dt; int acc; } lin_ctx;
+static void lin_rows(void* p, int64_t r0, int64_t r1) {
+    const lin_ctx* c = (const lin_ctx*) p;
+    for (int64_t r = r0; r < r1; ++r)
+        for (int64_t n = 0; n < c->N; ++n) {
+            double a = 0.0;
+            for (int64_t k = 0; k < c->K; ++k) a += (double) h3o_load(c->x, c->dt, r * c->K + k) * h3o_load(c->w, c->dt, n * c->K + k);
+            float v = (float) a;
+            if (c->bias) v = v + c->bias[n];
+            if (c->acc) v = v + h3o_load(c->out, c->out_dt, r * c->N + n);
+            h3o_store(c->out, c->out_dt, r * c->N + n, v);
+        }
+}
+void h3o_linear(const void* x, int dt, int64_t M, int64_t K, const void* w, int64_t N, const float* bias, void* out,
+                int out_dt, int acc) {
+    lin_ctx c = {x, dt, K, w, N, bias, out, out_dt, acc};
+    parallel_rows(M, lin_rows, &c);
+}
+void h3o_scale_rows(void* x, int dt, int64_t M, int64_t C, const float* s) {
+    for (int64_t r = 0; r < M; ++r)
+        for (int64_t i = 0; i < C; ++i) h3o_store(x, dt, r * C + i, h3o_load(x, dt, r * C + i) * s[r]);
+}
+
 /* ---- a step's tables: engine/h3-core/src/dit.rs:155-174 and 188-203 ---- */
 void h3o_adaln_tables(const float* w, const float* b, const float* t_emb, int64_t R, int64_t t_dim, int64_t m, int64_t C,
                       float* out) {

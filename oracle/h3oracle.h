@@ -142,6 +142,14 @@ int h3o_attention(const void* q, const void* k, const void* v, int dt, int64_t S
 void h3o_sage_quantize(const void* src, int dt, int64_t S, int64_t H, int64_t D, int64_t stride, const float* mean,
                        int8_t* codes, float* scales);
 
+/* ---- plain linear layers (kernels/h3sycl.h:87-93; kernels/h3sycl.cpp:656-739) ----
+ * out [M, N] = x [M, K] . w^T (w [N, K]) + bias, x and w in dt, the products summed in float64 and rounded once to
+ * out_dt; acc != 0: out = round(product + bias + out) in dt (h3s_linear_acc). The reference's matmul is oneDNN's,
+ * whose accumulation order is not restated. scale_rows: x[r, i] = round(x[r, i] * s[r]). */
+void h3o_linear(const void* x, int dt, int64_t M, int64_t K, const void* w, int64_t N, const float* bias, void* out,
+                int out_dt, int acc);
+void h3o_scale_rows(void* x, int dt, int64_t M, int64_t C, const float* s);
+
 /* ---- a step's tables (engine/h3-core/src/dit.rs:155-203) ----
  * adaln_tables: the six AdaLN tables of one block for R timestep embeddings t_emb [R, t_dim]:
  *   out[ci][(r * m + mi) * C + i] = b[o] + sum_k fl(w[o * t_dim + k] * t[r * t_dim + k]), o = mi 6 C + ci C + i,

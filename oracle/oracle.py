@@ -67,6 +67,8 @@ _SIGS = {
     "h3o_attention": (i32, [vp, vp, vp, i32, i64, i64, i64, i64, vp, i32, i32, vp, vp, vp, vp, vp]),
     "h3o_sage_quantize": (None, [vp, i32, i64, i64, i64, i64, vp, vp, vp]),
     "h3o_adaln_tables": (None, [vp, vp, vp, i64, i64, i64, i64, vp]),
+    "h3o_linear": (None, [vp, i32, i64, i64, vp, i64, vp, vp, i32, i32]),
+    "h3o_scale_rows": (None, [vp, i32, i64, i64, vp]),
     "h3o_rotations": (None, [vp, i64, vp, i64, vp]),
     "h3o_act": (f32, [f32, i32]),
     "h3o_compare": (None, [vp, vp, i64, vp, vp]),
@@ -314,6 +316,19 @@ def sage_quantize(src, dt, S, H, D, stride=None, mean=None):
     codes, scales = np.zeros(H * S * D, np.int8), np.zeros(H * nb, np.float32)
     lib().h3o_sage_quantize(_p(src), dt, S, H, D, stride, _p(mean), _p(codes), _p(scales))
     return codes, scales
+
+
+def linear(x, dt, M, K, w, N, bias=None, out_dt=BF16, acc_into=None):
+    """out [M*N] = x w^T + bias in out_dt; acc_into: a previous output (dt) to accumulate into (h3s_linear_acc)"""
+    out = np.array(acc_into, copy=True) if acc_into is not None else np.empty(M * N, dtype=np_dtype(out_dt))
+    lib().h3o_linear(_p(x), dt, M, K, _p(w), N, _p(bias), _p(out), out_dt, int(acc_into is not None))
+    return out
+
+
+def scale_rows(x, dt, M, C_, s):
+    out = np.array(x, copy=True)
+    lib().h3o_scale_rows(_p(out), dt, M, C_, _p(s))
+    return out
 
 
 def adaln_tables(w, b, t_emb, R, t_dim, m, C_):

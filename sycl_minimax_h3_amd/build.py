@@ -54,7 +54,9 @@ def build(jobs: int = 8) -> str:
         for f in [ex.submit(_compile, s, o) for s, o in zip(srcs, objs)]:
             f.result()
     tmp = LIB + ".tmp"
-    r = subprocess.run([hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp], capture_output=True, text=True)
+    # rocBLAS: the plain float GEMMs of h3s_linear / h3s_linear_acc
+    libs = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
+    r = subprocess.run([hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp, *libs], capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"linking libh3hip.so failed:\n{r.stderr[-4000:]}")
     os.replace(tmp, LIB)

@@ -43,6 +43,9 @@ struct Ctx {
     int8_t* ak = nullptr; size_t ak_cap = 0;
     uint16_t* av = nullptr; size_t av_cap = 0;
     float* af = nullptr; size_t af_cap = 0;
+    // h3s_linear / h3s_linear_acc: the rocBLAS handle (on this context's stream) and the float32 product of a row chunk
+    void* blas = nullptr;
+    float* lin = nullptr; size_t lin_cap = 0;
     bool sage_want = true;                 // H3S_ATTN=onednn: false
     int64_t sage_min_s = 8192;             // H3S_SAGE_MIN_S
 
@@ -54,6 +57,9 @@ struct Ctx {
 Ctx* ctx_of(void* ctx, const char* fn);
 // the status of the last launch on this thread, as an error naming fn
 int launched(const char* fn);
+
+// frees the context's rocBLAS handle, if it has one (linear.hip)
+void release_blas(Ctx* c);
 
 // the quantizer of h3s_int8_linear (rownorm.hip): x [M, K] -> regular rotation per group (0: none) -> q, s
 int launch_quantize(Ctx* c, const void* x, int x_dt, int64_t M, int64_t K, int group, int8_t* q, float* s);
@@ -101,9 +107,15 @@ template <int N> __device__ __forceinline__ void wait_vm() {
 // as kernels/h3sycl.cpp:42-49; a NaN stays a NaN)
 __device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+// The float32 inputs of a 16-bit rounding are pinned in registers first (an empty asm): the compiler would otherwise
+// fold a producing multiply into a mixed-precision fma with one rounding (v_fma_mix), where the arithmetic rounds to
+// float32 and then to the 16-bit type.
+__device__ __forceinline__ void pin(float& a) { asm volatile("" : "+v"(a)); }
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
     typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
     typedef float f2 __attribute__((ext_vector_type(2)));
+    pin(a);
+    pin(b);
     f2 v = {a, b};
     bf2 r = __builtin_convertvector(v, bf2);
     uint32_t u;
@@ -116,13 +128,18 @@ __device__ __forceinline__ float f16_hi(uint32_t u) { return f16_lo(u >> 16); }
 __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     typedef float f2 __attribute__((ext_vector_type(2)));
+    pin(a);
+    pin(b);
     f2 v = {a, b};
     h2 r = __builtin_convertvector(v, h2);          // v_cvt_pk_f16_f32: both halves, round to nearest even
     uint32_t u;
     __builtin_memcpy(&u, &r, 4);
     return u;
 }
-__device__ __forceinline__ float round_f16(float v) { return (float) (_Float16) v; }
+__device__ __forceinline__ float round_f16(float v) {
+    pin(v);
+    return (float) (_Float16) v;
+}
 
 // a 16-byte vector of element type DT as floats (V = 8 for 16-bit types, 4 for float32)
 template <int DT> struct Vec;

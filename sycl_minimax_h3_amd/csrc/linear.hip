@@ -1,0 +1,155 @@
+// linear.hip - the plain (float) linear layers of kernels/h3sycl.h:87-93: h3s_linear (out = x w^T + bias),
+// h3s_linear_acc (out += x w^T + bias, a LoRA's second factor) and h3s_scale_rows (kernels/h3sycl.cpp:656-739).
+// The products run on rocBLAS (a plain library GEMM, float32 accumulation, on the context's stream) into a float32
+// scratch, a chunk of rows at a time; the epilogue kernel adds the bias (and the old output) in float32 and rounds
+// once to the output type, as the reference's matmul post-ops do.
+#include <rocblas/rocblas.h>
+
+#include "common.h"
+
+namespace h3 {
+
+void release_blas(Ctx* c) {
+    if (c->blas) (void) rocblas_destroy_handle((rocblas_handle) c->blas);
+    c->blas = nullptr;
+}
+
+static rocblas_handle blas_of(Ctx* c) {
+    if (!c->blas) {
+        rocblas_handle h = nullptr;
+        if (rocblas_create_handle(&h) != rocblas_status_success) { set_error("rocBLAS: no handle"); return nullptr; }
+        if (rocblas_set_stream(h, c->stream) != rocblas_status_success) {
+            (void) rocblas_destroy_handle(h);
+            set_error("rocBLAS: could not bind the context's stream");
+            return nullptr;
+        }
+        c->blas = h;
+    }
+    return (rocblas_handle) c->blas;
+}
+
+static rocblas_datatype blas_type(int dt) {
+    return dt == H3S_F32 ? rocblas_datatype_f32_r : dt == H3S_F16 ? rocblas_datatype_f16_r : rocblas_datatype_bf16_r;
+}
+
+template <int DT> __device__ __forceinline__ float lin_load(const void* p, int64_t i) {
+    if constexpr (DT == H3S_F32) return ((const float*) p)[i];
+    else if constexpr (DT == H3S_BF16) return bf16_lo(((const uint16_t*) p)[i]);
+    else return f16_lo(((const uint16_t*) p)[i]);
+}
+template <int DT> __device__ __forceinline__ void lin_store(void* p, int64_t i, float v) {
+    if constexpr (DT == H3S_F32) ((float*) p)[i] = v;
+    else if constexpr (DT == H3S_BF16) ((uint16_t*) p)[i] = (uint16_t) pack_bf16(v, 0.0f);
+    else ((uint16_t*) p)[i] = (uint16_t) pack_f16(v, 0.0f);
+}
+
+// out[r, n] = round(acc[r, n] [+ bias[n]] [+ out[r, n]]) over rows [0, M)
+template <int DT, bool ACC>
+__global__ __launch_bounds__(256) void lin_epilogue_kernel(const float* __restrict__ acc, int64_t M, int64_t N,
+                                                           const float* __restrict__ bias, void* out) {
+    const int64_t n = M * N;
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t) gridDim.x * 256) {
+        float v = acc[i];
+        if (bias) v = v + bias[i % N];
+        if constexpr (ACC) v = v + lin_load<DT>(out, i);
+        lin_store<DT>(out, i, v);
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void scale_rows_kernel(void* x, int64_t M, int64_t C, const float* __restrict__ s) {
+    const int64_t n = M * C;
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t) gridDim.x * 256)
+        lin_store<DT>(x, i, lin_load<DT>(x, i) * s[i / C]);
+}
+
+static unsigned grid_of(int64_t n, const Ctx& c) {
+    const int64_t b = (n + 255) / 256, cap = (int64_t) c.cus * 16;
+    return (unsigned) (b < cap ? (b > 0 ? b : 1) : cap);
+}
+
+template <bool ACC>
+static int launch_epilogue(Ctx* c, const float* acc, int64_t M, int64_t N, const float* bias, void* out, int out_dt) {
+    const unsigned g = grid_of(M * N, *c);
+    switch (out_dt) {
+        case H3S_F32: lin_epilogue_kernel<H3S_F32, ACC><<<g, 256, 0, c->stream>>>(acc, M, N, bias, out); break;
+        case H3S_F16: lin_epilogue_kernel<H3S_F16, ACC><<<g, 256, 0, c->stream>>>(acc, M, N, bias, out); break;
+        default: lin_epilogue_kernel<H3S_BF16, ACC><<<g, 256, 0, c->stream>>>(acc, M, N, bias, out); break;
+    }
+    return 0;
+}
+
+// the product x [M, K] . w^T (w [N, K]), both in dt, into out (or out +=) a chunk of rows at a time
+static int linear(Ctx* c, const char* fn, const void* x, int dt, int64_t M, int64_t K, const void* w, int64_t N,
+                  const float* bias, void* out, int out_dt, bool acc) {
+    if (K > 0x7fffffff || N > 0x7fffffff) return fail(std::string(fn) + ": K and N must be below 2^31");
+    rocblas_handle h = blas_of(c);
+    if (!h) return -1;
+    // rows a chunk: the float32 product of a chunk takes at most 256 MiB (and at most 8192 rows, as the reference)
+    int64_t rows = (int64_t) (256 << 20) / (N * 4);
+    rows = rows < 1 ? 1 : rows > 8192 ? 8192 : rows;
+    rows = rows < M ? rows : M;
+    float* tmp = c->grow(c->lin, c->lin_cap, (size_t) (rows * N));
+    if (!tmp) return -1;
+    const size_t xe = (size_t) elem_size(dt), oe = (size_t) elem_size(out_dt);
+    const float one = 1.0f, zero = 0.0f;
+    for (int64_t r0 = 0; r0 < M; r0 += rows) {
+        const int64_t m = M - r0 < rows ? M - r0 : rows;
+        // column-major view: tmp^T [N, m] = w [N, K] (stored as K x N, transposed) . x^T [K, m]
+        const rocblas_status st = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int) N,
+                                                  (rocblas_int) m, (rocblas_int) K, &one, w, blas_type(dt), (rocblas_int) K,
+                                                  (const char*) x + (size_t) (r0 * K) * xe, blas_type(dt), (rocblas_int) K,
+                                                  &zero, tmp, rocblas_datatype_f32_r, (rocblas_int) N, tmp,
+                                                  rocblas_datatype_f32_r, (rocblas_int) N, rocblas_datatype_f32_r,
+                                                  rocblas_gemm_algo_standard, 0, 0);
+        if (st != rocblas_status_success)
+            return fail(std::string(fn) + ": rocBLAS gemm_ex failed (" + rocblas_status_to_string(st) + ")");
+        char* o = (char*) out + (size_t) (r0 * N) * oe;
+        if (acc) launch_epilogue<true>(c, tmp, m, N, bias, o, out_dt);
+        else launch_epilogue<false>(c, tmp, m, N, bias, o, out_dt);
+        if (launched(fn)) return -1;
+    }
+    return 0;
+}
+
+}  // namespace h3
+
+using namespace h3;
+
+H3S_EXPORT int h3s_linear(void* ctx, const void* x, int dt, int64_t M, int64_t K, const void* w, int64_t N, const float* bias,
+                          void* out, int out_dt) try {
+    const char* fn = "h3s_linear";
+    if (M <= 0 || K <= 0 || N <= 0) return 0;
+    if (!dt_ok(dt) || !dt_ok(out_dt)) return fail(std::string(fn) + ": unknown element type");
+    if (!x || !w || !out) return fail(std::string(fn) + ": x, w and out are required");
+    Ctx* c = ctx_of(ctx, fn);
+    if (!c) return -1;
+    return linear(c, fn, x, dt, M, K, w, N, bias, out, out_dt, false);
+} catch (const std::exception& e) { return fail(e.what()); }
+
+H3S_EXPORT int h3s_linear_acc(void* ctx, const void* x, int dt, int64_t M, int64_t K, const void* w, int64_t N,
+                              const float* bias, void* out) try {
+    const char* fn = "h3s_linear_acc";
+    if (M <= 0 || K <= 0 || N <= 0) return 0;
+    if (!dt_ok(dt)) return fail(std::string(fn) + ": unknown element type");
+    if (!x || !w || !out) return fail(std::string(fn) + ": x, w and out are required");
+    Ctx* c = ctx_of(ctx, fn);
+    if (!c) return -1;
+    return linear(c, fn, x, dt, M, K, w, N, bias, out, dt, true);
+} catch (const std::exception& e) { return fail(e.what()); }
+
+H3S_EXPORT int h3s_scale_rows(void* ctx, void* x, int dt, int64_t M, int64_t C, const float* s) try {
+    const char* fn = "h3s_scale_rows";
+    if (M <= 0 || C <= 0) return 0;
+    if (!dt_ok(dt)) return fail(std::string(fn) + ": unknown element type");
+    if (!x || !s) return fail(std::string(fn) + ": x and s are required");
+    Ctx* c = ctx_of(ctx, fn);
+    if (!c) return -1;
+    const unsigned g = grid_of(M * C, *c);
+    switch (dt) {
+        case H3S_F32: scale_rows_kernel<H3S_F32><<<g, 256, 0, c->stream>>>(x, M, C, s); break;
+        case H3S_F16: scale_rows_kernel<H3S_F16><<<g, 256, 0, c->stream>>>(x, M, C, s); break;
+        default: scale_rows_kernel<H3S_BF16><<<g, 256, 0, c->stream>>>(x, M, C, s); break;
+    }
+    return launched(fn);
+} catch (const std::exception& e) { return fail(e.what()); }

@@ -260,8 +260,9 @@ H3S_EXPORT void h3s_destroy(void* ctx) {
     if (c->copy_stream) { (void) hipStreamSynchronize(c->copy_stream); (void) hipStreamDestroy(c->copy_stream); }
     if (c->xq) (void) hipFree(c->xq);
     if (c->rs) (void) hipFree(c->rs);
-    for (void* p : {(void*) c->aq, (void*) c->ak, (void*) c->av, (void*) c->af})
+    for (void* p : {(void*) c->aq, (void*) c->ak, (void*) c->av, (void*) c->af, (void*) c->lin})
         if (p) (void) hipFree(p);
+    release_blas(c);
     for (auto& kv : c->mem) (void) hipFree(kv.first);
     if (c->own_stream) (void) hipStreamDestroy(c->stream);
     delete c;
@@ -272,13 +273,6 @@ H3S_EXPORT void h3s_destroy(void* ctx) {
 #define H3S_NOT_HERE(name, what) \
     return fail(std::string(name) + ": not implemented in libh3hip (" what "); only the per-token layer kernels are")
 
-H3S_EXPORT int h3s_linear_acc(void*, const void*, int, int64_t, int64_t, const void*, int64_t, const float*, void*) {
-    H3S_NOT_HERE("h3s_linear_acc", "float GEMM");
-}
-H3S_EXPORT int h3s_scale_rows(void*, void*, int, int64_t, int64_t, const float*) { H3S_NOT_HERE("h3s_scale_rows", "weight preparation"); }
-H3S_EXPORT int h3s_linear(void*, const void*, int, int64_t, int64_t, const void*, int64_t, const float*, void*, int) {
-    H3S_NOT_HERE("h3s_linear", "float GEMM");
-}
 H3S_EXPORT int h3s_dequant(void*, const void*, int, int64_t, void*, int) { H3S_NOT_HERE("h3s_dequant", "k-quant weights"); }
 H3S_EXPORT int h3s_attention_causal(void*, const void*, const void*, const void*, int, int64_t, int64_t, int64_t, int64_t, int64_t,
                                     int64_t, void*) {

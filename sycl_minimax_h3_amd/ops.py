@@ -67,6 +67,58 @@ class Int8Linear:
 
 
 @dataclass
+class Linear:
+    """A plain linear layer (ops.rs:164-237): weight [N, K] in float32, half or bfloat16; bias float32 [N]."""
+
+    weight: Tensor
+    bias: Tensor | None = None
+
+    def inputs(self) -> int:
+        return self.weight.shape[1]
+
+    def outputs(self) -> int:
+        return self.weight.shape[0]
+
+    def forward(self, x: Tensor, out: Tensor) -> None:
+        """out = linear(x): x [M, K] in the weight's type, out [M, N] in out's type."""
+        n, k = self.outputs(), self.inputs()
+        m = x.elements() // k
+        if x.dtype != self.weight.dtype:
+            raise Error(f"linear: x is {x.dtype} and the weight {self.weight.dtype}; they must be the same type")
+        if x.elements() != m * k or out.elements() != m * n:
+            raise Error(f"linear: x {x.shape} and out {out.shape} do not fit a [{n}, {k}] weight")
+        bias = _floats(self.bias, "the bias", n) if self.bias is not None else None
+        dev = _dev(x)
+        dev.check(dev.api.linear(dev.ctx, x.ptr(), x.dtype.kernel_code(), m, k, self.weight.ptr(), n, bias, out.ptr(),
+                                 out.dtype.kernel_code()))
+
+    def forward_acc(self, x: Tensor, out: Tensor) -> None:
+        """out += linear(x) (bias included), x and out in the weight's type."""
+        n, k = self.outputs(), self.inputs()
+        m = x.elements() // k
+        if x.dtype != self.weight.dtype or out.dtype != x.dtype or x.elements() != m * k or out.elements() != m * n:
+            raise Error(f"linear_acc: x {x.dtype} {x.shape}, out {out.dtype} {out.shape}, weight [{n}, {k}] {self.weight.dtype}")
+        bias = _floats(self.bias, "the bias", n) if self.bias is not None else None
+        dev = _dev(x)
+        dev.check(dev.api.linear_acc(dev.ctx, x.ptr(), x.dtype.kernel_code(), m, k, self.weight.ptr(), n, bias, out.ptr()))
+
+    def scale_outputs(self, s: Tensor) -> None:
+        """Scales output row n of the weight by s[n] (float32 [N]) in place, on the device; the bias too (on the
+        host, as the reference does)."""
+        n, k = self.outputs(), self.inputs()
+        if s.elements() != n or s.dtype != DType.F32:
+            raise Error(f"scale_outputs: {s.elements()} factors for {n} outputs")
+        dev = _dev(self.weight)
+        dev.check(dev.api.scale_rows(dev.ctx, self.weight.ptr(), self.weight.dtype.kernel_code(), n, k, s.ptr()))
+        if self.bias is not None:
+            import numpy as np
+
+            b = self.bias.to_numpy().astype(np.float32) * s.to_numpy().astype(np.float32)
+            self.bias = Tensor.from_numpy(dev, DType.F32, [n], b)
+        dev.wait()
+
+
+@dataclass
 class Mod:
     """How a block's tokens are modulated: the row table and the scale/shift tables (ops.rs:239-245)."""
 

@@ -103,6 +103,8 @@ def test_empty_shapes_do_nothing(api):
 
 
 def test_out_of_scope_entry_points_refuse(api):
+    assert api.linear(None, None, 7, 1, 1, None, 1, None, None, 2) == -1
+    assert "element type" in api.error()
     assert api.attention_causal(None, None, None, None, 2, 1, 1, 1, 1, 1, 1, None) == -1
     assert "not implemented" in api.error()
     # attention's argument checks run before the context is looked at

@@ -425,3 +425,27 @@ def test_attention_against_dense_softmax():
     # and the sage result stays close to the exact attention (the quantization error of q and k)
     rel, cos = o.compare(out.astype(np.float32), dense(qh, kh, vh).astype(np.float32).ravel())
     assert rel < 0.05 and cos > 0.998
+
+
+# ---- plain linear layers (kernels/h3sycl.cpp:656-739) ----
+def test_linear_oracle_closed_forms():
+    """An identity weight gives x back (rounded once to out's type); the bias adds per column; accumulation adds the
+    previous output; scale_rows scales each row."""
+    M, K = 5, 16
+    x = o.to_bf16(np.random.default_rng(85).standard_normal((M, K)).astype(np.float32)).ravel()
+    eye = o.to_bf16(np.eye(K, dtype=np.float32)).ravel()
+    out = o.linear(x, o.BF16, M, K, eye, K, out_dt=o.BF16)
+    assert np.array_equal(out, x)
+    bias = np.arange(K, dtype=np.float32)
+    out = o.linear(x, o.BF16, M, K, eye, K, bias, out_dt=o.F32)
+    assert np.array_equal(out.reshape(M, K), o.from_dt(x, o.BF16).reshape(M, K) + bias[None, :])
+    acc = o.linear(x, o.BF16, M, K, eye, K, None, out_dt=o.BF16, acc_into=x)
+    assert np.array_equal(acc, o.to_bf16(2 * o.from_dt(x, o.BF16)))
+    s = np.array([1, 2, 0.5, -1, 0], np.float32)
+    sr = o.scale_rows(x, o.BF16, M, K, s)
+    assert np.array_equal(o.from_dt(sr, o.BF16).reshape(M, K), o.from_dt(x, o.BF16).reshape(M, K) * s[:, None])
+    # a general product against numpy's float64 matrix product
+    w = o.to_bf16(np.random.default_rng(86).standard_normal((7, K)).astype(np.float32)).ravel()
+    out = o.linear(x, o.BF16, M, K, w, 7, out_dt=o.F32)
+    want = (o.from_dt(x, o.BF16).reshape(M, K).astype(np.float64) @ o.from_dt(w, o.BF16).reshape(7, K).T.astype(np.float64))
+    assert np.allclose(out.reshape(M, 7), want, rtol=1e-6, atol=1e-6)
