@@ -11,19 +11,35 @@ template <int DT>
 static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S, int64_t Sp, int64_t H, int D,
                  int64_t stride, bool sage, int8_t* aq, int8_t* ak, uint16_t* av, float* qs, float* ks, float* km) {
     const unsigned blocks = (unsigned) (H * (Sp / kAttnRows));
+    // 16-byte rows: every tensor aligned and the stride a whole number of 16-byte vectors
+    const bool vec = aligned16(q) && aligned16(k) && aligned16(v) && (stride * elem_size(DT)) % 16 == 0;
+    auto qk = [&](const void* src, const float* mean, int8_t* dst, float* sc) {
+#define H3_QK(SG, DD) attn_qk_prep_vec_kernel<DT, SG, DD><<<blocks, 256, 0, c->stream>>>(src, S, Sp, stride, mean, dst, sc)
+        if (!vec) {
+            if (sage) attn_qk_prep_kernel<DT, true><<<blocks, 256, 0, c->stream>>>(src, S, Sp, D, stride, mean, dst, sc);
+            else attn_qk_prep_kernel<DT, false><<<blocks, 256, 0, c->stream>>>(src, S, Sp, D, stride, mean, dst, sc);
+        } else if (sage) {
+            if (D == 128) H3_QK(true, 128);
+            else H3_QK(true, 64);
+        } else {
+            if (D == 128) H3_QK(false, 128);
+            else H3_QK(false, 64);
+        }
+#undef H3_QK
+    };
     if (sage) {
         const int64_t hd = H * D;
-        if (aligned16(k) && (stride * elem_size(DT)) % 16 == 0)
-            attn_kmean_kernel<DT><<<(unsigned) (hd / 64), 256, 0, c->stream>>>(k, S, stride, km);
-        else
-            attn_kmean_rows_kernel<DT><<<(unsigned) ((hd + 255) / 256), 256, 0, c->stream>>>(k, S, hd, stride, km);
-        attn_qk_prep_kernel<DT, true><<<blocks, 256, 0, c->stream>>>(q, S, Sp, D, stride, nullptr, aq, qs);
-        attn_qk_prep_kernel<DT, true><<<blocks, 256, 0, c->stream>>>(k, S, Sp, D, stride, km, ak, ks);
+        if (vec) attn_kmean_kernel<DT><<<(unsigned) (hd / 64), 256, 0, c->stream>>>(k, S, stride, km);
+        else attn_kmean_rows_kernel<DT><<<(unsigned) ((hd + 255) / 256), 256, 0, c->stream>>>(k, S, hd, stride, km);
+        qk(q, nullptr, aq, qs);
+        qk(k, km, ak, ks);
     } else {
-        attn_qk_prep_kernel<DT, false><<<blocks, 256, 0, c->stream>>>(q, S, Sp, D, stride, nullptr, aq, nullptr);
-        attn_qk_prep_kernel<DT, false><<<blocks, 256, 0, c->stream>>>(k, S, Sp, D, stride, nullptr, ak, nullptr);
+        qk(q, nullptr, aq, nullptr);
+        qk(k, nullptr, ak, nullptr);
     }
-    attn_v_prep_kernel<DT><<<blocks, 256, 0, c->stream>>>(v, S, Sp, D, stride, av);
+    if (!vec) attn_v_prep_kernel<DT><<<blocks, 256, 0, c->stream>>>(v, S, Sp, D, stride, av);
+    else if (D == 128) attn_v_prep_vec_kernel<DT, 128><<<blocks, 256, 0, c->stream>>>(v, S, Sp, stride, av);
+    else attn_v_prep_vec_kernel<DT, 64><<<blocks, 256, 0, c->stream>>>(v, S, Sp, stride, av);
 }
 
 static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, const void* v, int dt, int64_t S, int64_t H,

@@ -157,6 +157,106 @@ __global__ __launch_bounds__(256) void attn_qk_prep_kernel(const void* __restric
     }
 }
 
+// The same two preparations with 16-byte loads, for rows that are 16-byte aligned (the tensor and the stride): a
+// thread holds its chunks (V values each) of the block's 64 rows in registers between the max and the codes.
+template <int DT, bool SAGE, int D>
+__global__ __launch_bounds__(256) void attn_qk_prep_vec_kernel(const void* __restrict__ src, int64_t S, int64_t Sp,
+                                                               int64_t stride, const float* __restrict__ mean,
+                                                               int8_t* __restrict__ dst, float* __restrict__ scales) {
+    constexpr int V = Vec<DT>::V, CPR = D / V, N = kAttnRows * CPR / 256;   // chunks a row, chunks a thread
+    __shared__ float red[4];
+    const int64_t nbp = Sp / kAttnRows, b = blockIdx.x % nbp, h = blockIdx.x / nbp, r0 = b * kAttnRows;
+    const int tid = threadIdx.x;
+    const char* base = reinterpret_cast<const char*>(src) + (r0 * stride + h * D) * (int64_t) (16 / V);
+    float v[N][V];
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const int u = tid + 256 * k, r = u / CPR, c = u % CPR;
+        uint4 raw = make_uint4(0, 0, 0, 0);
+        if (r0 + r < S) raw = *reinterpret_cast<const uint4*>(base + (int64_t) r * stride * (16 / V) + 16 * c);
+        Vec<DT>::unpack(raw, v[k]);
+    }
+    if constexpr (SAGE) {
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const int u = tid + 256 * k, r = u / CPR, c = u % CPR;
+            if (mean) {
+#pragma unroll
+                for (int e = 0; e < V; ++e) v[k][e] = v[k][e] - mean[h * D + c * V + e];
+            }
+            if (r0 + r < S)
+#pragma unroll
+                for (int e = 0; e < V; ++e) m = fmaxf(m, fabsf(v[k][e]));
+        }
+        m = wave_max<64>(m);
+        if ((tid & 63) == 0) red[tid >> 6] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+        if (tid == 0) scales[h * nbp + b] = m / 127.0f;
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const int u = tid + 256 * k, r = u / CPR, c = u % CPR;
+            uint32_t w[V / 4];
+#pragma unroll
+            for (int g = 0; g < V / 4; ++g) {
+                float q[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float cc = roundf(v[k][4 * g + e] * inv);
+                    cc = fminf(fmaxf(cc, -127.0f), 127.0f);
+                    q[e] = r0 + r < S ? cc : 0.0f;
+                }
+                w[g] = (uint32_t) ((int) q[0] & 255) | ((uint32_t) ((int) q[1] & 255) << 8) |
+                       ((uint32_t) ((int) q[2] & 255) << 16) | ((uint32_t) ((int) q[3] & 255) << 24);
+            }
+            int8_t* o = dst + (h * Sp + r0 + r) * D + c * V;
+            if constexpr (V == 8) *reinterpret_cast<uint2*>(o) = make_uint2(w[0], w[1]);
+            else *reinterpret_cast<uint32_t*>(o) = w[0];
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const int u = tid + 256 * k, r = u / CPR, c = u % CPR;
+            uint32_t w[V / 2];
+#pragma unroll
+            for (int g = 0; g < V / 2; ++g) w[g] = pack_f16(v[k][2 * g], v[k][2 * g + 1]);
+            uint16_t* o = reinterpret_cast<uint16_t*>(dst) + (h * Sp + r0 + r) * D + c * V;
+            if constexpr (V == 8) *reinterpret_cast<uint4*>(o) = make_uint4(w[0], w[1], w[2], w[3]);
+            else *reinterpret_cast<uint2*>(o) = make_uint2(w[0], w[1]);
+        }
+    }
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void attn_v_prep_vec_kernel(const void* __restrict__ v, int64_t S, int64_t Sp,
+                                                              int64_t stride, uint16_t* __restrict__ vt) {
+    constexpr int V = Vec<DT>::V, CPR = D / V, N = kAttnRows * CPR / 256, PITCH = kAttnRows + 8;
+    __shared__ uint16_t tile[D * PITCH];                     // [feature][token], half bits
+    const int64_t nbp = Sp / kAttnRows, b = blockIdx.x % nbp, h = blockIdx.x / nbp, t0 = b * kAttnRows;
+    const int tid = threadIdx.x;
+    const char* base = reinterpret_cast<const char*>(v) + (t0 * stride + h * D) * (int64_t) (16 / V);
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const int u = tid + 256 * k, t = u / CPR, c = u % CPR;
+        uint4 raw = make_uint4(0, 0, 0, 0);
+        if (t0 + t < S) raw = *reinterpret_cast<const uint4*>(base + (int64_t) t * stride * (16 / V) + 16 * c);
+        float f[V];
+        Vec<DT>::unpack(raw, f);
+#pragma unroll
+        for (int e = 0; e < V; ++e) tile[(c * V + e) * PITCH + t] = half_bits(f[e]);
+    }
+    __syncthreads();
+    // output row d holds the 64 tokens: 8 chunks of 16 bytes
+#pragma unroll
+    for (int k = 0; k < D * 8 / 256; ++k) {
+        const int u = tid + 256 * k, d = u / 8, c = u % 8;
+        const uint4 val = *reinterpret_cast<const uint4*>(tile + d * PITCH + 8 * c);
+        *reinterpret_cast<uint4*>(vt + (h * D + d) * Sp + t0 + 8 * c) = val;
+    }
+}
+
 // v of one head and 64 tokens to half, transposed: vt [H, D, Sp]; tokens past S become zeros
 template <int DT>
 __global__ __launch_bounds__(256) void attn_v_prep_kernel(const void* __restrict__ v, int64_t S, int64_t Sp, int D,
