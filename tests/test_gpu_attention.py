@@ -80,6 +80,20 @@ def test_attention(dev_sage, dev_16, sage, dt, out_dt, S, H, D, pad):
 
 
 @pytest.mark.parametrize("sage", [True, False])
+@pytest.mark.parametrize("S,pad", [(1, 0), (63, 2), (65, 0), (200, 6), (129, 1)])
+def test_attention_edges(dev_sage, dev_16, sage, S, pad):
+    """One token, tiles cut short by one key either side of 64, and row strides that are not whole 16-byte vectors
+    (the element-wise preparation)."""
+    H, D = 2, 64
+    stride = H * D + pad
+    q, k, v = qkv(75 + S, S, H, D, o.BF16, stride)
+    want = o.attention(q, k, v, o.BF16, S, H, D, stride, out_dt=o.F32, sage=sage)
+    want = want[0] if sage else want
+    got = run(dev_sage if sage else dev_16, q, k, v, o.BF16, S, H, D, stride, o.F32)
+    check(got, want, o.F32, f"edge S={S} pad={pad}")
+
+
+@pytest.mark.parametrize("sage", [True, False])
 def test_attention_peaked_and_shifted(dev_sage, dev_16, sage):
     """Large score spreads (the online max moves a lot, most weights underflow) and a large common offset in k (the
     int8 form takes k's mean out)."""
