@@ -243,14 +243,18 @@ def main() -> int:
     if copy:
         line["copy_probe"] = copy
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(x2, r2, tab)
+        line["cpu_baseline"] = cpu_baseline(x2, r2, tab, {"x1": x1, "g1": g1, "q3": q3, "k3": k3, "wq": wq, "wk": wk,
+                                                          "cs": cs, "x4": x4, "x5": x5, "sc5": sc5, "sh5": sh5,
+                                                          "q4": q4, "s4": s4, "w5": w5, "ws5": ws5})
     print(json.dumps(line), flush=True)
     return 0
 
 
-def cpu_baseline(x2, r2, tab):
+def cpu_baseline(x2, r2, tab, t):
     """The CPU oracle (oracle/h3oracle.c, C restatement of the reference arithmetic, row-parallel with contiguous row
-    chunks as engine/h3-core/src/reference.rs:43-80) on the headline workload, on this host."""
+    chunks as engine/h3-core/src/reference.rs:43-80) on this host: the headline workload, and under `kernels` the other
+    configurations on their full inputs (the GEMM on its first 1024 rows, scaled linearly), each the median of a few
+    runs (about 10 s in all for the headline, a few runs for the others)."""
     import numpy as np
     import torch
 
@@ -258,28 +262,64 @@ def cpu_baseline(x2, r2, tab):
 
     threads = min(16, os.cpu_count() or 1)
     o.set_threads(threads)
-    x = x2.view(torch.int16).cpu().numpy().view(np.uint16).ravel()
-    r = r2.view(torch.int16).cpu().numpy().view(np.uint16).ravel()
-    t = [a.view(torch.int16).cpu().numpy().view(np.uint16).ravel() for a in tab]
-    run = lambda: o.norm_mod_act_gate(x, o.BF16, M2, C, o.NORM_LAYER, None, None, 1e-5, None, t[0], t[1], t[2], o.BF16,  # noqa: E731
-                                      o.ACT_GELU_TANH, r, o.BF16, o.BF16)
-    run()
-    times = []
-    t_end = time.perf_counter() + 10.0
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    gbs = bytes_cfg()["cfg2_ln_mod_gelu_gate_16896"] / med / 1e9
+    u16 = lambda a: a.view(torch.int16).cpu().numpy().view(np.uint16).ravel()   # noqa: E731
+    f32 = lambda a: a.float().cpu().numpy().ravel()                              # noqa: E731
+
+    def median_time(fn, budget, least=3, most=50):
+        fn()
+        times = []
+        t_end = time.perf_counter() + budget
+        while len(times) < least or (time.perf_counter() < t_end and len(times) < most):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times)), len(times)
+
+    x, r = u16(x2), u16(r2)
+    tb = [u16(a) for a in tab]
+    med, n = median_time(lambda: o.norm_mod_act_gate(x, o.BF16, M2, C, o.NORM_LAYER, None, None, 1e-5, None, tb[0], tb[1],
+                                                     tb[2], o.BF16, o.ACT_GELU_TANH, r, o.BF16, o.BF16), 10.0)
+    B = bytes_cfg()
+    gbs = B["cfg2_ln_mod_gelu_gate_16896"] / med / 1e9
     cpu = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
             cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
     except Exception:
         pass
-    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"the full 16896 x 4096 workload, median of {len(times)} runs ({med * 1e3:.1f} ms each) on {cpu}"}
+    out = {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+           "sample": f"the full 16896 x 4096 workload, median of {n} runs ({med * 1e3:.1f} ms each) on {cpu}"}
+
+    # the other configurations, on the same tensors the GPU ran
+    per = {}
+    x1, g1 = u16(t["x1"]), f32(t["g1"])
+    m, _ = median_time(lambda: o.norm_quant(x1, o.BF16, 2159, C, g1, 1e-6), 2.0)
+    per["cfg1_rmsnorm_quant_2159"] = m
+    q3, k3, wq, wk, cs = u16(t["q3"]), u16(t["k3"]), f32(t["wq"]), f32(t["wk"]), f32(t["cs"])
+    m, _ = median_time(lambda: (o.rms_rope(q3, o.BF16, M2, 32, 128, 4096, wq, 1e-5, cs, 128),
+                                o.rms_rope(k3, o.BF16, M2, 32, 128, 4096, wk, 1e-5, cs, 128)), 2.0)
+    per["cfg3_qk_rmsnorm_rope3d_16896"] = m
+    x4 = u16(t["x4"])
+    m, _ = median_time(lambda: o.norm_quant(x4, o.BF16, M4, C, g1, 1e-6, rot=o.ROT_SYLVESTER, group=128), 2.0)
+    per["cfg4_rmsnorm_wht128_quant_47104"] = m
+    x5, sc5, sh5 = u16(t["x5"]), u16(t["sc5"]), u16(t["sh5"])
+    m, _ = median_time(lambda: o.norm_quant(x5, o.BF16, M4, C, g1, 1e-6, None, sc5, sh5, o.BF16), 2.0)
+    per["cfg5a_rmsnorm_mod_quant_47104"] = m
+    rows = 1024
+    q4 = t["q4"][:rows].cpu().numpy().ravel()
+    s4 = t["s4"][:rows].cpu().numpy().ravel()
+    w5, ws5 = t["w5"].cpu().numpy().ravel(), f32(t["ws5"])
+    m, _ = median_time(lambda: o.gemm_dequant(q4, s4, rows, C, w5, 16384, ws5, act=o.ACT_SILU), 2.0, least=2)
+    per["cfg5b_int8_gemm_silu_47104x16384"] = m * M4 / rows
+    kernels = {}
+    for k, sec in per.items():
+        e = {"ms": round(sec * 1e3, 3), "GB/s": round(B[k] / sec / 1e9, 2)}
+        if k.startswith("cfg5b"):
+            e["TOPS_i8"] = round(2 * M4 * C * 16384 / sec / 1e12, 3)
+            e["sample"] = f"the first {rows} of {M4} rows, time scaled by {M4 / rows:.1f}"
+        kernels[k] = e
+    out["kernels"] = kernels
+    return out
 
 
 if __name__ == "__main__":
