@@ -11,8 +11,8 @@
 // wavefront owns 32 queries and walks all keys 64 at a time. Per 64-key tile:
 //   S^T = K Q^T:  v_mfma_i32_32x32x32_i8 (or f32_32x32x16_f16) with K as the first operand, so every lane ends with
 //                 scores of one query (lane % 32) for 32 of the 64 keys (the other 32 in lane ^ 32);
-//   softmax:      the row max needs one exchange with lane ^ 32 (v_permlane32_swap); the row sum stays a per-lane
-//                 partial until the end;
+//   softmax:      the row max needs one exchange with lane ^ 32 (v_permlane32_swap); the exponents' reference
+//                 point moves only when a tile max passes it by 2^8; the row sum stays a per-lane partial until the end;
 //   O^T += V^T P^T: v_mfma_f32_32x32x16_f16 with V^T as the first operand; P's registers become the second operand
 //                 after one v_permlane32_swap per register pair (each lane then holds 8 consecutive keys).
 // K and V^T tiles go global -> LDS by direct loads (global_load_lds_dwordx4) into two stages, the next tile in flight
@@ -399,20 +399,24 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
 #pragma unroll
         for (int i = 1; i < 32; ++i) mx = fmaxf(mx, x[i]);
         mx = attn_pair_max(mx) * f;
-        const float mn = fmaxf(m, mx);
-        const float alpha = __builtin_amdgcn_exp2f(m - mn);
-        m = mn;
+        // The reference point m of the exponents moves only when some lane's tile max passes it by more than 8 (in
+        // base 2): the weights then stay at most 2^8, exact in half's range, and O / l does not depend on m. O and l
+        // are rescaled only then (the empty asm keeps the compiler from running the 64 multiplies unconditionally).
+        if (__any(mx > m + 8.0f)) {
+            asm volatile("" ::: "memory");
+            const float mn = fmaxf(m, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m - mn);
+            m = mn;
+            l = l * alpha;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) x[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], f, -mn));
+            for (int dt = 0; dt < NDT; ++dt) o[dt] = o[dt] * alpha;
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], f, -m));
         if constexpr (TAIL) {
 #pragma unroll
             for (int i = 0; i < 32; ++i)
                 if (!live(i)) x[i] = 0.0f;
-        }
-        // O and l carry the scale of the running max; rescale only when some lane's max moved
-        if (__any(alpha != 1.0f)) {
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) o[dt] = o[dt] * alpha;
         }
         float ls = 0.0f;
 
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, vf), pb, o[dt], 0, 0, 0);
             }
         }
-        l = __builtin_fmaf(l, alpha, ls);
+        l = l + ls;
     };
     issue(0, 0);
     const int full = (int) (S / kAttnRows);                    // tiles with no key past S
