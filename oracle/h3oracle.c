@@ -754,6 +754,45 @@ int h3o_attention(const void* q, const void* k, const void* v, int dt, int64_t S
     return 0;
 }
 
+/* ---- causal attention: kernels/h3sycl.cpp:873-898 ---- */
+typedef struct { const void *q, *k, *v; int dt; int64_t L, Hq, Hkv, D, qs, kvs; void* out; } causal_ctx;
+static void causal_rows(void* p, int64_t r0, int64_t r1) {
+    const causal_ctx* c = (const causal_ctx*) p;
+    const int64_t D = c->D;
+    double* sc = (double*) malloc((size_t) c->L * sizeof(double));
+    double* acc = (double*) malloc((size_t) D * sizeof(double));
+    const double scale = 1.0f / sqrtf((float) D);
+    for (int64_t t = r0; t < r1; ++t) {
+        const int64_t i = t / c->Hq, h = t % c->Hq, g = h / (c->Hq / c->Hkv);
+        double mx = -1e300;
+        for (int64_t j = 0; j <= i; ++j) {
+            double a = 0.0;
+            for (int64_t d = 0; d < D; ++d)
+                a += (double) h3o_load(c->q, c->dt, i * c->qs + h * D + d) * h3o_load(c->k, c->dt, j * c->kvs + g * D + d);
+            sc[j] = a * scale;
+            if (sc[j] > mx) mx = sc[j];
+        }
+        double l = 0.0;
+        for (int64_t d = 0; d < D; ++d) acc[d] = 0.0;
+        for (int64_t j = 0; j <= i; ++j) {
+            const double w = exp(sc[j] - mx);
+            l += w;
+            for (int64_t d = 0; d < D; ++d) acc[d] += w * h3o_load(c->v, c->dt, j * c->kvs + g * D + d);
+        }
+        for (int64_t d = 0; d < D; ++d) h3o_store(c->out, c->dt, (i * c->Hq + h) * D + d, (float) (acc[d] / l));
+    }
+    free(sc);
+    free(acc);
+}
+int h3o_attention_causal(const void* q, const void* k, const void* v, int dt, int64_t L, int64_t Hq, int64_t Hkv, int64_t D,
+                         int64_t qs, int64_t kvs, void* out) {
+    if (L <= 0) return 0;
+    if (Hq % Hkv != 0) return fail("attention_causal: Hq a multiple of Hkv");
+    causal_ctx c = {q, k, v, dt, L, Hq, Hkv, D, qs, kvs, out};
+    parallel_rows(L * Hq, causal_rows, &c);
+    return 0;
+}
+
 /* ---- plain linear layers: kernels/h3sycl.cpp:656-739 ---- */
 typedef struct { const void* x; int dt; int64_t K; const void* w; int64_t N; const float* bias; void* out; int out_dt; int acc; } lin_ctx;
 static void lin_rows(void* p, int64_t r0, int64_t r1) {

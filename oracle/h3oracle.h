@@ -138,6 +138,11 @@ float h3o_act(float v, int act);
  * and kmean [H, D] when those are not NULL. */
 int h3o_attention(const void* q, const void* k, const void* v, int dt, int64_t S, int64_t H, int64_t D, int64_t stride,
                   void* out, int out_dt, int sage, int8_t* iq, int8_t* ik, float* qs, float* ks, float* kmean);
+/* causal attention with grouped key/value heads (kernels/h3sycl.cpp:873-898): query i of head h sees keys 0 .. i of
+ * kv head h / (Hq / Hkv); q rows of stride qs, k and v rows of stride kvs, all in dt; out [L, Hq * D] in dt; the
+ * softmax in float64 on the dt values, one rounding to dt. */
+int h3o_attention_causal(const void* q, const void* k, const void* v, int dt, int64_t L, int64_t Hq, int64_t Hkv, int64_t D,
+                         int64_t qs, int64_t kvs, void* out);
 /* the sage form's quantization of one tensor: mean NULL for q; codes [H, S, D], scales [H, ceil(S / 64)] */
 void h3o_sage_quantize(const void* src, int dt, int64_t S, int64_t H, int64_t D, int64_t stride, const float* mean,
                        int8_t* codes, float* scales);

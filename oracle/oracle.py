@@ -66,6 +66,7 @@ _SIGS = {
     "h3o_quantize_act": (i32, [vp, i32, i64, i64, i32, i32, vp, vp]),
     "h3o_attention": (i32, [vp, vp, vp, i32, i64, i64, i64, i64, vp, i32, i32, vp, vp, vp, vp, vp]),
     "h3o_sage_quantize": (None, [vp, i32, i64, i64, i64, i64, vp, vp, vp]),
+    "h3o_attention_causal": (i32, [vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, vp]),
     "h3o_adaln_tables": (None, [vp, vp, vp, i64, i64, i64, i64, vp]),
     "h3o_linear": (None, [vp, i32, i64, i64, vp, i64, vp, vp, i32, i32]),
     "h3o_scale_rows": (None, [vp, i32, i64, i64, vp]),
@@ -308,6 +309,15 @@ def attention(q, k, v, dt, S, H, D, stride=None, out_dt=BF16, sage=True):
     _check(lib().h3o_attention(_p(q), _p(k), _p(v), dt, S, H, D, stride, _p(out), out_dt, int(sage), _p(iq), _p(ik),
                                _p(qs), _p(ks), _p(km)))
     return (out, iq, ik, qs, ks, km) if sage else out
+
+
+def attention_causal(q, k, v, dt, L, Hq, Hkv, D, qs=None, kvs=None):
+    """causal softmax(q k^T / sqrt(D)) v with kv heads shared by Hq / Hkv query heads -> out [L * Hq * D] in dt"""
+    qs = Hq * D if qs is None else qs
+    kvs = Hkv * D if kvs is None else kvs
+    out = np.empty(L * Hq * D, dtype=np_dtype(dt))
+    _check(lib().h3o_attention_causal(_p(q), _p(k), _p(v), dt, L, Hq, Hkv, D, qs, kvs, _p(out)))
+    return out
 
 
 def sage_quantize(src, dt, S, H, D, stride=None, mean=None):

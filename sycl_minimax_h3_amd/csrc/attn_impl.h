@@ -287,6 +287,8 @@ struct AttnArgs {
     void* out;                // [S, H * D]
     int out_dt;
     int nqb;                  // blocks of 128 queries per head
+    int kvdiv;                // query heads per key/value head: head h reads k and v of head h / kvdiv
+    int64_t Spk;              // rows of the prepared k and v^T (Sp unless they come from another sequence)
 };
 
 // the chunk of row r (rows of CPR 16-byte chunks) where logical chunk c is stored
@@ -302,7 +304,7 @@ __device__ __forceinline__ float attn_pair_sum(float x) {
     return __int_as_float(r[0]) + __int_as_float(r[1]);
 }
 
-template <bool SAGE, int D>
+template <bool SAGE, int D, bool CAUSAL = false>
 __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
     constexpr int ESZ = SAGE ? 1 : 2, RB = D * ESZ, CPR = RB / 16, NQF = RB / 32;
     constexpr int KTB = kAttnRows * RB, VTB = D * kAttnRows * 2, STAGE = KTB + VTB;
@@ -312,7 +314,9 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
     const int64_t h = blockIdx.x / P.nqb, qb = blockIdx.x % P.nqb, Sp = P.Sp, S = P.S;
     const int64_t q0 = qb * kAttnQBlock + 32 * wave;          // this wavefront's first query
     const int64_t nbp = Sp / kAttnRows;
-    const int ntiles = (int) ((S + kAttnRows - 1) / kAttnRows);
+    // CAUSAL: query i sees keys 0 .. i, so the block stops at its last query
+    const int64_t kend = CAUSAL ? (qb * kAttnQBlock + kAttnQBlock < S ? qb * kAttnQBlock + kAttnQBlock : S) : S;
+    const int ntiles = (int) ((kend + kAttnRows - 1) / kAttnRows);
 
     // this lane's query fragments (second operand of the score products), held for the whole key walk
     v4i_a qf[NQF];
@@ -324,24 +328,25 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
     const float fq = SAGE ? P.qs[h * nbp + q0 / kAttnRows] * P.c : P.c;
 
     // direct loads of key tile t into stage st: the K rows (64 x RB bytes) and the V^T rows (D x 128 bytes)
-    const int8_t* kbase = P.k + h * Sp * RB;
-    const uint16_t* vbase = P.vt + h * D * Sp;
+    const int64_t g = h / P.kvdiv, Spk = P.Spk;              // the key/value head and its rows
+    const int8_t* kbase = P.k + g * Spk * RB;
+    const uint16_t* vbase = P.vt + g * D * Spk;
     auto issue = [&](int t, int st) {
         int8_t* s = lds + st * STAGE;
         constexpr int KI = CPR / 4;                            // K instructions a wavefront
 #pragma unroll
         for (int j = 0; j < KI; ++j) {
             const int i = wave * KI + j, u = 64 * i + lane, r = u / CPR, c = attn_swz<CPR>(r, u % CPR);
-            const int8_t* g = kbase + ((int64_t) t * kAttnRows + r) * RB + 16 * c;
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) g,
+            const int8_t* gk = kbase + ((int64_t) t * kAttnRows + r) * RB + 16 * c;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) gk,
                                              (__attribute__((address_space(3))) void*) (s + 1024 * i), 16, 0, 0);
         }
         constexpr int VI = D / 32;                              // V^T instructions a wavefront (D * 8 units / 64 / 4)
 #pragma unroll
         for (int j = 0; j < VI; ++j) {
             const int i = wave * VI + j, u = 64 * i + lane, r = u / 8, c = attn_swz<8>(r, u % 8);
-            const uint16_t* g = vbase + (int64_t) r * Sp + (int64_t) t * kAttnRows + 8 * c;
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) g,
+            const uint16_t* gv = vbase + (int64_t) r * Spk + (int64_t) t * kAttnRows + 8 * c;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) gv,
                                              (__attribute__((address_space(3))) void*) (s + KTB + 1024 * i), 16, 0, 0);
         }
     };
@@ -386,9 +391,13 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
         }
         // register i of half j holds key 32 j + 8 (i / 4) + 4 hl + i % 4 of the tile. The scale f > 0 is applied after
         // the max (max(a f) = f max(a)) and inside the exponent: p = 2^(a f - m) with one fused multiply-add.
-        const float f = SAGE ? fq * P.ks[h * nbp + t] : fq;
-        // key of register i, less than `lim` for the keys inside the sequence
-        const int lim = (int) (S - (int64_t) t * kAttnRows) - 4 * hl;
+        const float f = SAGE ? fq * P.ks[g * nbp + t] : fq;
+        // register i holds key 64 t + 4 hl + off(i); it is live below S and, CAUSAL, up to this lane's query
+        int lim = (int) (S - (int64_t) t * kAttnRows) - 4 * hl;
+        if constexpr (CAUSAL) {
+            const int qlim = (int) (q0 + ql - (int64_t) t * kAttnRows) - 4 * hl + 1;
+            lim = lim < qlim ? lim : qlim;
+        }
         auto live = [&](int i) { return 32 * (i / 16) + 8 * ((i % 16) / 4) + i % 4 < lim; };
         if constexpr (TAIL) {
 #pragma unroll
@@ -449,9 +458,11 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
         l = l + ls;
     };
     issue(0, 0);
-    const int full = (int) (S / kAttnRows);                    // tiles with no key past S
+    // tiles with no key past S (and, CAUSAL, none past the block's first query) need no mask
+    int full = (int) (S / kAttnRows);
+    if constexpr (CAUSAL) full = full < (int) (qb * kAttnQBlock / kAttnRows) ? full : (int) (qb * kAttnQBlock / kAttnRows);
     for (int t = 0; t < full; ++t) step(t, std::false_type{});
-    if (full < ntiles) step(full, std::true_type{});
+    for (int t = full; t < ntiles; ++t) step(t, std::true_type{});
 
     // ---- out = O / l, rounded to half, in out's type ----
     const float inv = 1.0f / attn_pair_sum(l);
@@ -466,7 +477,9 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
                 // registers 4 g .. 4 g + 3 of o[dt]: features 32 dt + 8 g + 4 hl + (0..3)
                 float v[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = round_f16(o[dt][4 * g + i] * inv);
+                // the reference's result buffer is half for the two forms of h3s_attention; its causal kernel stores
+                // acc / l straight into out's type
+                for (int i = 0; i < 4; ++i) v[i] = CAUSAL ? o[dt][4 * g + i] * inv : round_f16(o[dt][4 * g + i] * inv);
                 char* at = orow + (32 * dt + 8 * g + 4 * hl) * esz;
                 if (P.out_dt == H3S_F32) *reinterpret_cast<float4*>(at) = make_float4(v[0], v[1], v[2], v[3]);
                 else if (P.out_dt == H3S_BF16) *reinterpret_cast<uint2*>(at) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));

@@ -274,10 +274,6 @@ H3S_EXPORT void h3s_destroy(void* ctx) {
     return fail(std::string(name) + ": not implemented in libh3hip (" what "); only the per-token layer kernels are")
 
 H3S_EXPORT int h3s_dequant(void*, const void*, int, int64_t, void*, int) { H3S_NOT_HERE("h3s_dequant", "k-quant weights"); }
-H3S_EXPORT int h3s_attention_causal(void*, const void*, const void*, const void*, int, int64_t, int64_t, int64_t, int64_t, int64_t,
-                                    int64_t, void*) {
-    H3S_NOT_HERE("h3s_attention_causal", "attention");
-}
 H3S_EXPORT int h3s_conv3d(void*, const void*, int, int64_t, int64_t, int64_t, int64_t, const void*, int64_t, int64_t, const float*, void*) {
     H3S_NOT_HERE("h3s_conv3d", "convolution");
 }

@@ -196,6 +196,18 @@ def attention(q: Rows, k: Rows, v: Rows, out: Tensor) -> None:
                                 q.stride, out.ptr(), out.dtype.kernel_code()))
 
 
+def attention_causal(q: Rows, k: Rows, v: Rows, out: Tensor) -> None:
+    """The text encoder's causal attention: query i sees keys 0 .. i; q has Hq heads, k and v Hkv (head h reads kv
+    head h / (Hq / Hkv)); out [tokens, Hq * dim] in q's type (te.rs:342-347)."""
+    if k.layout() != v.layout() or q.tokens != k.tokens or q.dim != k.dim or q.t.dtype != k.t.dtype or k.t.dtype != v.t.dtype:
+        raise Error("attention_causal: k and v must share a layout, and q their tokens, head size and type")
+    if out.elements() != q.tokens * q.heads * q.dim or out.dtype != q.t.dtype:
+        raise Error(f"attention_causal: out {out.dtype} {out.shape} for {q.tokens} tokens of {q.heads} x {q.dim}")
+    dev = _dev(out)
+    dev.check(dev.api.attention_causal(dev.ctx, q.ptr(), k.ptr(), v.ptr(), q.t.dtype.kernel_code(), q.tokens, q.heads,
+                                       k.heads, q.dim, q.stride, k.stride, out.ptr()))
+
+
 def attention_batch(q: Rows, k: Rows, v: Rows, seqs: int, out: Tensor) -> None:
     """attention over `seqs` equal sequences of the rows, each on its own (ops.rs:405-434)."""
     if q.layout() != k.layout() or q.layout() != v.layout():

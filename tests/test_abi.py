@@ -105,8 +105,10 @@ def test_empty_shapes_do_nothing(api):
 def test_out_of_scope_entry_points_refuse(api):
     assert api.linear(None, None, 7, 1, 1, None, 1, None, None, 2) == -1
     assert "element type" in api.error()
-    assert api.attention_causal(None, None, None, None, 2, 1, 1, 1, 1, 1, 1, None) == -1
+    assert api.conv3d(None, None, 2, 1, 1, 1, 1, None, 1, 3, None, None) == -1
     assert "not implemented" in api.error()
+    assert api.attention_causal(None, None, None, None, 2, 4, 3, 2, 64, 192, 128, None) == -1
+    assert "multiple" in api.error()
     # attention's argument checks run before the context is looked at
     assert api.attention(None, None, None, None, 2, 1, 1, 96, 96, None, 2) == -1
     assert "64 or 128" in api.error()

@@ -138,6 +138,23 @@ def test_attention_batch(dev_16):
         check(got[b], want, o.BF16, f"sequence {b}")
 
 
+@pytest.mark.parametrize("dt", [o.F16, o.BF16, o.F32])
+@pytest.mark.parametrize("L,Hq,Hkv,D", [(1, 2, 1, 128), (37, 8, 2, 128), (130, 4, 4, 64), (300, 6, 2, 128), (257, 8, 1, 64)])
+def test_attention_causal(dev, dt, L, Hq, Hkv, D):
+    """The text encoder's causal attention with grouped kv heads (kernels/h3sycl.cpp:873-898), q and kv in buffers of
+    wider rows."""
+    qs, kvs = Hq * D + 8, 2 * Hkv * D
+    g = np.random.default_rng(97 + L)
+    q = o.to_dt(g.standard_normal(L * qs).astype(np.float32), dt)
+    kv = o.to_dt(g.standard_normal(L * kvs).astype(np.float32), dt)
+    k, v = kv, kv[Hkv * D:]                                           # k and v interleaved in one buffer
+    want = o.attention_causal(q, k, v, dt, L, Hq, Hkv, D, qs, kvs)
+    qt, kvt = up(dev, q, DTS[dt], [L, qs]), up(dev, kv, DTS[dt], [L, kvs])
+    out = new(dev, DTS[dt], [L, Hq * D])
+    ops.attention_causal(ops.Rows(qt, 0, qs, L, Hq, D), ops.Rows(kvt, 0, kvs, L, Hkv, D), ops.Rows(kvt, Hkv * D, kvs, L, Hkv, D), out)
+    check(out.to_numpy().ravel(), want, dt, f"causal L={L} Hq={Hq} Hkv={Hkv}")
+
+
 def test_attention_refuses(dev):
     p = new(dev, "BF16", [64, 96])
     with pytest.raises(Error, match="64 or 128"):

@@ -371,6 +371,6 @@ def test_errors_are_reported(dev):
     with pytest.raises(Error, match="rot_dim"):
         dev.check(dev.api.rms_rope(dev.ctx, xt.ptr(), 2, M, 32, 128, 4096, s.ptr(), 1e-5, s.ptr(), 127))
     with pytest.raises(Error, match="not implemented"):
-        dev.check(dev.api.attention_causal(dev.ctx, xt.ptr(), xt.ptr(), xt.ptr(), 2, M, 32, 32, 128, 4096, 4096, xt.ptr()))
+        dev.check(dev.api.conv3d(dev.ctx, xt.ptr(), 2, 1, 1, 1, 8, xt.ptr(), 8, 3, None, xt.ptr()))
     assert dev.api.rms_norm_mod(dev.ctx, xt.ptr(), 2, 0, C, s.ptr(), 1e-6, None, None, None, xt.ptr(), 2) == 0
     dev.wait()

@@ -449,3 +449,23 @@ def test_linear_oracle_closed_forms():
     out = o.linear(x, o.BF16, M, K, w, 7, out_dt=o.F32)
     want = (o.from_dt(x, o.BF16).reshape(M, K).astype(np.float64) @ o.from_dt(w, o.BF16).reshape(7, K).T.astype(np.float64))
     assert np.allclose(out.reshape(M, 7), want, rtol=1e-6, atol=1e-6)
+
+
+def test_attention_causal_oracle():
+    """Row 0 sees only key 0 (out = v[0]); with one kv head shared by all query heads, each head is the non-causal
+    attention over the prefix; the last row equals the full (non-causal) attention of the 16-bit form on f32 inputs."""
+    L, Hq, Hkv, D = 40, 4, 2, 64
+    g = np.random.default_rng(95)
+    q = g.standard_normal((L, Hq * D)).astype(np.float32)
+    k = g.standard_normal((L, Hkv * D)).astype(np.float32)
+    v = g.standard_normal((L, Hkv * D)).astype(np.float32)
+    out = o.attention_causal(q.ravel(), k.ravel(), v.ravel(), o.F32, L, Hq, Hkv, D).reshape(L, Hq, D)
+    for h in range(Hq):
+        gkv = h // (Hq // Hkv)
+        assert np.allclose(out[0, h], v[0, gkv * D:(gkv + 1) * D], rtol=1e-6, atol=1e-6)
+        # an independent dense formulation with the causal mask
+        s = (q[:, h * D:(h + 1) * D].astype(np.float64) @ k[:, gkv * D:(gkv + 1) * D].T.astype(np.float64)) / np.sqrt(np.float32(D))
+        s[np.triu_indices(L, 1)] = -np.inf
+        p = np.exp(s - s.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        assert np.allclose(out[:, h], p @ v[:, gkv * D:(gkv + 1) * D], rtol=1e-5, atol=1e-5)
