@@ -45,6 +45,7 @@ def bytes_cfg():
         "cfg5b_int8_gemm_silu_47104x16384": M4 * C + 16384 * C + M4 * 4 + 16384 * 4 + M4 * 16384 * 2,
         "mlp_swiglu_quant_g256_47104x8192": M4 * 16384 * 2 + M4 * 8192 + M4 * 4,
         "attn_sage_16896x32x128": 4 * M2 * 4096 * 2,     # q, k, v read, out written (the products are the bound)
+        "attn_sage_47104x32x128": 4 * M4 * 4096 * 2,
     }
 
 
@@ -196,6 +197,14 @@ def main() -> int:
     QKV7, O7 = T(qkv7), T(o7)
     rows7 = [ops.Rows(QKV7, i * 4096, 3 * 4096, M2, 32, 128) for i in range(3)]
     run("attn_sage_16896x32x128", lambda: ops.attention(*rows7, O7), 10)
+    del qkv7, o7, QKV7, O7, rows7
+    # the same at 47104 tokens (the 47k configurations' sequence)
+    qkv8 = bf16(M4, 3 * 4096)
+    o8 = torch.empty(M4, 4096, dtype=torch.bfloat16, device=dev_t)
+    QKV8, O8 = T(qkv8), T(o8)
+    rows8 = [ops.Rows(QKV8, i * 4096, 3 * 4096, M4, 32, 128) for i in range(3)]
+    run("attn_sage_47104x32x128", lambda: ops.attention(*rows8, O8), 3)
+    del qkv8, o8, QKV8, O8, rows8
 
     copy = None
     if args.copy_probe:
@@ -214,7 +223,8 @@ def main() -> int:
             e.update({"TOPS_i8": round(tops, 1), "frac_i8_peak": round(tops / PEAK_I8_TOPS, 4)})
         if k.startswith("attn"):
             # q k^T on the i8 cores (5 POPS) and P v on the f16 cores (2.5 PFLOP/s): the time both take at peak
-            half_ops = 2.0 * M2 * M2 * 4096
+            S_ = M2 if "16896" in k else M4
+            half_ops = 2.0 * S_ * S_ * 4096
             t_peak = half_ops / (PEAK_I8_TOPS * 1e12) + half_ops / (PEAK_F16_TFLOPS * 1e12)
             e.update({"TOPS": round(2 * half_ops / (ms * 1e-3) / 1e12, 1), "frac_mfma_peak": round(t_peak / (ms * 1e-3), 4)})
         per[k] = e
