@@ -48,6 +48,7 @@ struct Ctx {
     float* lin = nullptr; size_t lin_cap = 0;
     bool sage_want = true;                 // H3S_ATTN=onednn: false
     int64_t sage_min_s = 8192;             // H3S_SAGE_MIN_S
+    int64_t quant_wave_min = 8192;         // H3S_QUANT_WAVE_MIN_ROWS: fewest rows for the one-wavefront-a-row quantizer
 
     // A scratch buffer of at least n elements, counted against the cap; NULL with the reason on failure.
     template <typename T> T* grow(T*& p, size_t& cap, size_t n);
@@ -101,6 +102,19 @@ constexpr int kWave = 64;
 template <int N> __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt");
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// A workgroup barrier that orders LDS only: the LDS accesses before it are complete (lgkmcnt) and no access moves
+// across it (the clobber). __syncthreads would also wait for every global load in flight, draining the rows a
+// kernel has prefetched at each row statistic.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// A value equal on every lane of the wavefront, taken from the first lane: the compiler then keeps it, and what is
+// computed from it, in scalar registers (loop control as scalar branches, loads indexed by it as scalar addresses).
+__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) v);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) ((uint64_t) v >> 32));
+    return (int64_t) (((uint64_t) hi << 32) | lo);
 }
 
 // bf16 <-> f32: widen by shifting; narrow with the hardware's round-to-nearest-even (finite values: the same bits

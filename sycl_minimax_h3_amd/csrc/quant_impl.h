@@ -401,11 +401,254 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
     }
 }
 
+// ---- one wavefront a row, for rows of 256 to 512 16-byte chunks of a 16-bit type (2048 to 4096 features) ----
+// The same arithmetic as quant_kernel, laid out so that the row's scalar work is done once: quant_kernel spreads
+// such a row over four wavefronts, each of which repeats the row's statistics (the butterflies, the LDS combine
+// and its barrier, the divisions and the square root). Here lane t of the wavefront holds chunks t + 64 j
+// (j < CPL), and the row statistics keep the order of the 256-lane layout that the oracle restates: chunk slot j
+// belongs to canonical wavefront j % 4 (chunk t + 64 j is canonical lane (t + 64 j) % 256), so a lane keeps four
+// partial sums, each summed over the wavefront by the butterfly and then combined as (w0 + w2) + (w1 + w3).
+//
+// Rows are dealt out grid-stride by wavefront: wavefront w of block b takes rows g, g + U, g + 2U, ... with
+// g = b NW + w and U = NW x the blocks, so the rows in flight across the device form one contiguous window (a
+// contiguous run per wavefront streams measurably slower), and at step k the block's wavefronts hold the
+// neighbouring rows b NW + k U + [0, NW). The next row's x is in registers while a row is computed.
+//
+// The side inputs every wavefront of the block shares live in LDS, laid out [j][half][lane][4 floats] so that a
+// wavefront's 16-byte reads are consecutive: the weight, and one decoded table row (1 + scale and shift), the
+// table row of the block's first row at the current step. When that changes (a segment boundary of rows[]), the
+// block re-decodes it between two barriers (every wavefront computes the same condition); a row whose own table
+// row differs from the cached one decodes its values from memory.
+template <int CPL> constexpr size_t quant_wave_side_bytes(int f) {
+    return (size_t) ((f & ROW_W) ? 1 : 0) * CPL * 2048 + (size_t) ((f & ROW_TAB) ? 2 : 0) * CPL * 2048;
+}
+template <int XDT, int CPL, int ROT, int F>
+__global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
+    static_assert(XDT != H3S_F32 && !(F & (ROW_DYN | ROW_SWIGLU)), "quant_wave_kernel: 16-bit x, exact side inputs");
+    constexpr int V = 8;
+    constexpr bool ROTATED = ROT != H3S_ROT_NONE;
+    constexpr bool NORM = !(F & ROW_RAW);
+    constexpr bool HASW = F & ROW_W;
+    constexpr bool TAB = F & ROW_TAB;
+    constexpr int TDT = (F & ROW_TAB32) ? H3S_F32 : H3S_BF16;
+    constexpr int WOFF = 0, SOFF = HASW ? CPL * 512 : 0, HOFF = SOFF + CPL * 512;     // float offsets in side
+    extern __shared__ __align__(16) float side[];
+    const int lane = (int) (threadIdx.x & 63), NW = (int) (blockDim.x >> 6);
+    const int wave = (int) wave_uniform(threadIdx.x >> 6);
+    const int64_t C = A.C, nch = C / V;
+    const int64_t b0 = (int64_t) blockIdx.x * NW, U = (int64_t) gridDim.x * NW, M = A.M;
+    if (b0 >= M) return;                                    // the whole block
+    int64_t cc[CPL];
+    bool ok[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int64_t c = lane + 64 * j;
+        ok[j] = c < nch;
+        cc[j] = ok[j] ? c : nch - 1;
+    }
+    // the side values of chunk j: 8 floats at ((j * 2 + half) * 64 + lane) * 4 of an array
+    auto side_at = [&](int off, int j, int h) { return side + off + ((j * 2 + h) * 64 + lane) * 4; };
+    auto put8 = [&](int off, int j, const float* f) {
+        *reinterpret_cast<float4*>(side_at(off, j, 0)) = make_float4(f[0], f[1], f[2], f[3]);
+        *reinterpret_cast<float4*>(side_at(off, j, 1)) = make_float4(f[4], f[5], f[6], f[7]);
+    };
+    auto get8 = [&](int off, int j, float* f) {
+        const float4 a = *reinterpret_cast<const float4*>(side_at(off, j, 0));
+        const float4 b = *reinterpret_cast<const float4*>(side_at(off, j, 1));
+        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    };
+    // one table row's 1 + scale and shift for chunk j, decoded from memory
+    auto table8 = [&](int64_t trow, int j, float* s1, float* sh) {
+        Raw<V, TDT == H3S_F32> sr, hr;
+        fetch(sr, A.scale, TDT, trow * C + cc[j] * V);
+        fetch(hr, A.shift, TDT, trow * C + cc[j] * V);
+        decode(sr, TDT, s1);
+        decode(hr, TDT, sh);
+#pragma unroll
+        for (int e = 0; e < V; ++e) s1[e] = 1.0f + s1[e];
+    };
+    // the block's side values (the weight with W, the table row trow): wavefront w decodes chunk slots w, w + NW, ...
+    auto fill = [&](int64_t trow, bool with_w) {
+        for (int j = wave; j < CPL; j += NW) {
+#pragma unroll
+            for (int jj = 0; jj < CPL; ++jj) {
+                if (jj != j) continue;                       // a constant slot index for the register arrays
+                if constexpr (HASW) {
+                    if (with_w) {
+                        Raw<V, true> wr;
+                        fetch(wr, A.w, H3S_F32, cc[jj] * V);
+                        float f[V];
+                        decode(wr, H3S_F32, f);
+                        put8(WOFF, jj, f);
+                    }
+                }
+                if constexpr (TAB) {
+                    float s1[V], sh[V];
+                    table8(trow, jj, s1, sh);
+                    put8(SOFF, jj, s1);
+                    put8(HOFF, jj, sh);
+                }
+            }
+        }
+    };
+    int64_t tcache = TAB && A.rows ? A.rows[b0] : 0;
+    if constexpr (HASW || TAB) {
+        fill(tcache, true);
+        lds_barrier();
+    }
+
+    const float cgs = ROT == H3S_ROT_SYLVESTER ? A.cg * syl_sign<V>(lane, A.group) : A.cg;
+    auto load_row = [&](uint4 (&xr)[CPL], int64_t row) {
+        const uint4* xp = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * 2);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) xr[j] = xp[cc[j]];
+    };
+    // The table row indices of this wavefront's rows and of the block's first row at each step, 64 steps at a time,
+    // one a lane (taken out with readlane): rows[] is read once per 64 steps, and waited for there, not once per row
+    // with a wait that would drain the next row's x.
+    int tix = 0, gix = 0;
+    int64_t kbase = -64;
+    auto table_rows = [&](int64_t k, int64_t& own, int64_t& first) {
+        if (k - kbase >= 64) {
+            kbase = k;
+            const int64_t rf = b0 + U * (k + lane), ro = rf + wave;
+            tix = ro < M ? A.rows[ro] : 0;
+            gix = rf < M ? A.rows[rf] : 0;
+            wait_vm<0>();
+        }
+        own = __builtin_amdgcn_readlane(tix, (int) (k - kbase));
+        first = __builtin_amdgcn_readlane(gix, (int) (k - kbase));
+    };
+    uint4 x0[CPL];
+    int64_t row = b0 + wave;
+    // rows left to this wavefront and to the block's first wavefront: the block steps while its first row exists
+    if (row < M) load_row(x0, row);
+    for (int64_t k = 0, first = b0; first < M; row += U, first += U, ++k) {
+        int64_t trow = 0;
+        if constexpr (TAB) {
+            if (A.rows) {
+                int64_t tfirst;
+                table_rows(k, trow, tfirst);
+                if (tfirst != tcache) {                      // the same on every wavefront of the block
+                    lds_barrier();                           // every wavefront is done with the cached row
+                    fill(tfirst, false);
+                    lds_barrier();
+                    tcache = tfirst;
+                }
+            }
+        }
+        if (row >= M) continue;                              // past the end: only the barriers above remain to keep
+        uint4 x1[CPL];
+        if (row + U < M) load_row(x1, row + U);
+        float v[CPL][V];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(x0[j], v[j]);
+
+        // ---- rms_norm_mod into bfloat16 (the reference's scratch h) ----
+        if constexpr (NORM) {
+            float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+                if (ok[j])
+#pragma unroll
+                    for (int e = 0; e < V; ++e) ss[j % 4] = __builtin_fmaf(v[j][e], v[j][e], ss[j % 4]);
+            float w4[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) w4[g] = wave_sum<64>(ss[g]);
+            const float inv = inv_root((w4[0] + w4[2]) + (w4[1] + w4[3]), (float) C, A.eps);
+            const bool cached = trow == tcache;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                if constexpr (HASW) {
+                    float w[V];
+                    get8(WOFF, j, w);
+#pragma unroll
+                    for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * inv * w[e];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * inv;
+                }
+                if constexpr (TAB) {
+                    float s1[V], sh[V];
+                    if (cached) {
+                        get8(SOFF, j, s1);
+                        get8(HOFF, j, sh);
+                    } else {
+                        table8(trow, j, s1, sh);
+                    }
+#pragma unroll
+                    for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * s1[e] + sh[e];
+                }
+#pragma unroll
+                for (int e = 0; e < V; e += 2) {
+                    const uint32_t p = pack_bf16(v[j][e], v[j][e + 1]);
+                    v[j][e] = bf16_lo(p);
+                    v[j][e + 1] = bf16_hi(p);
+                }
+            }
+        }
+
+        // ---- the block rotation, then the row's absolute maximum ----
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            if constexpr (ROTATED) {
+                if constexpr (ROT == H3S_ROT_SYLVESTER) sylvester<V>(v[j], lane, A.group);
+                else regular<V>(v[j], A.group);
+#pragma unroll
+                for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * cgs;
+            }
+            if (ok[j])
+#pragma unroll
+                for (int e = 0; e < V; ++e) m = fmaxf(m, fabsf(v[j][e]));
+        }
+        m = wave_max<64>(m);
+        const float sc = fmaxf(m / 127.0f, 1e-30f), r = 1.0f / sc;
+        if (lane == 0) A.s[row] = sc;
+
+        // ---- the codes, 8 bytes a chunk ----
+        int8_t* qrow = A.q + row * C;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            if (!ok[j]) continue;
+            const float* o = v[j];
+            const uint32_t lo = bytes4(code_of(o[0], sc, r), code_of(o[1], sc, r), code_of(o[2], sc, r), code_of(o[3], sc, r));
+            const uint32_t hi = bytes4(code_of(o[4], sc, r), code_of(o[5], sc, r), code_of(o[6], sc, r), code_of(o[7], sc, r));
+            st_nt(qrow + cc[j] * 8, make_uint2(lo, hi));
+        }
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) x0[j] = x1[j];
+    }
+}
+
 // The side-input masks compiled exactly for 16-bit inputs: none (h3s_int8_linear's quantizer), the weight
 // (configs 1 and 4), the weight with 16-bit or float32 tables (config 5's front pass, the DiT's AdaLN). Every other
 // call shape runs the ROW_DYN instantiation.
 constexpr int kQuantNone = 0, kQuantW = ROW_W, kQuantWTab = ROW_W | ROW_TAB, kQuantWTab32 = ROW_W | ROW_TAB | ROW_TAB32,
               kQuantRaw = ROW_RAW, kQuantSwiglu = ROW_SWIGLU;
+
+// The launch of quant_wave_kernel: blocks of 4 wavefronts (8 with tables, so one LDS copy of the side values
+// serves more rows), as many as the device holds at once (at most one wavefront a row).
+template <int XDT, int CPL, int ROT, int F> int quant_wave_one(Ctx* c, const char* fn, const QuantArgs& A) {
+    const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F>;
+    const int threads = (F & ROW_TAB) ? 512 : 256;
+    const size_t lds = quant_wave_side_bytes<CPL>(F);
+    const int64_t blocks = std::min<int64_t>((int64_t) c->cus * blocks_per_cu(k, threads, lds), (A.M + threads / 64 - 1) / (threads / 64));
+    quant_wave_kernel<XDT, CPL, ROT, F><<<(unsigned) blocks, threads, lds, c->stream>>>(A);
+    return launched(fn);
+}
+template <int XDT, int CPL> int quant_wave_launch(Ctx* c, const char* fn, const QuantArgs& A, int f) {
+#define H3_QW(RR)                                                                          \
+    if (f == kQuantNone) return quant_wave_one<XDT, CPL, RR, kQuantNone>(c, fn, A);         \
+    if (f == kQuantW) return quant_wave_one<XDT, CPL, RR, kQuantW>(c, fn, A);               \
+    if (f == kQuantWTab) return quant_wave_one<XDT, CPL, RR, kQuantWTab>(c, fn, A);         \
+    if (f == kQuantWTab32) return quant_wave_one<XDT, CPL, RR, kQuantWTab32>(c, fn, A);     \
+    return quant_wave_one<XDT, CPL, RR, kQuantRaw>(c, fn, A);
+    if (A.rot == H3S_ROT_SYLVESTER) { H3_QW(H3S_ROT_SYLVESTER) }
+    if (A.rot == H3S_ROT_REGULAR) { H3_QW(H3S_ROT_REGULAR) }
+    H3_QW(H3S_ROT_NONE)
+#undef H3_QW
+}
 
 // what the quantizer runs on: rms_norm_mod of x, x itself, or swiglu of x
 enum QuantMode { QUANT_NORM, QUANT_RAW, QUANT_SWIGLU };
@@ -434,6 +677,16 @@ template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, 
     }                                                                                                \
     H3_QUANT_F(CC, RR, ROW_DYN);                                                                     \
     return launched(fn);
+    // rows of 256 to 512 chunks of a 16-bit type with the exact side inputs, and enough of them (the context's
+    // quant_wave_min, 8192) to give every wavefront several rows: one wavefront a row (fewer rows: four wavefronts
+    // share each, which shortens a short launch)
+    if constexpr (XDT != H3S_F32) {
+        if ((f == kQuantNone || f == kQuantW || f == kQuantWTab || f == kQuantWTab32 || f == kQuantRaw) && p.L == 256 &&
+            p.cpl <= 2 && A.C / 8 >= 256 && A.M >= c->quant_wave_min) {
+            if (A.C / 8 == 256) return quant_wave_launch<XDT, 4>(c, fn, A, f);
+            return quant_wave_launch<XDT, 8>(c, fn, A, f);
+        }
+    }
 #define H3_QUANT_CPL(CC)                                                      \
     if (p.cpl == CC) {                                                        \
         if (A.rot == H3S_ROT_SYLVESTER) { H3_QUANT_R(CC, H3S_ROT_SYLVESTER) }  \

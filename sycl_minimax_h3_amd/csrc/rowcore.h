@@ -44,8 +44,9 @@ inline RowLaunch row_launch(int64_t M, RowPlan p) {
     r.lshift = __builtin_ctz((unsigned) p.L);
     return r;
 }
-// blocks of a kernel that fit one compute unit at once, asked of the runtime once per kernel and block size
-int blocks_per_cu(const void* kernel, int threads);
+// blocks of a kernel that fit one compute unit at once (with lds bytes of dynamic LDS each), asked of the runtime
+// once per kernel, block size and LDS size
+int blocks_per_cu(const void* kernel, int threads, size_t lds = 0);
 
 // A launch of row units (blocks of L >= 256 lanes, wavefronts of 64); unit u takes rows [u rpu, (u + 1) rpu). With
 // `keep` (side inputs worth holding in registers across rows: table rows) twice as many units as the device holds
@@ -90,7 +91,7 @@ __device__ __forceinline__ RowPos row_pos(int lshift, int64_t M) {
 __device__ __forceinline__ float row_combine_sum(float s, float* red, int W) {
     if (W > 1) {
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-        __syncthreads();
+        lds_barrier();
         if (W == 4) s = (red[0] + red[2]) + (red[1] + red[3]);
         else s = ((red[0] + red[4]) + (red[2] + red[6])) + ((red[1] + red[5]) + (red[3] + red[7]));
     }
@@ -101,7 +102,7 @@ __device__ __forceinline__ float row_max(float m, float* red, int W) {
     m = wave_max<64>(m);
     if (W > 1) {
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-        __syncthreads();
+        lds_barrier();
         m = red[0];
         for (int k = 1; k < W; ++k) m = fmaxf(m, red[k]);
     }

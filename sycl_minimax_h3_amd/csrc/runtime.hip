@@ -4,6 +4,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <map>
+#include <tuple>
 
 #include "common.h"
 
@@ -21,15 +22,15 @@ Ctx* ctx_of(void* ctx, const char* fn) {
     return c;
 }
 
-int blocks_per_cu(const void* kernel, int threads) {
+int blocks_per_cu(const void* kernel, int threads, size_t lds) {
     static std::mutex mu;
-    static std::map<std::pair<const void*, int>, int> known;
+    static std::map<std::tuple<const void*, int, size_t>, int> known;
     std::lock_guard<std::mutex> l(mu);
-    const auto key = std::make_pair(kernel, threads);
+    const auto key = std::make_tuple(kernel, threads, lds);
     const auto it = known.find(key);
     if (it != known.end()) return it->second;
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n < 1) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, lds) != hipSuccess || n < 1) {
         (void) hipGetLastError();
         n = 1;
     }
@@ -61,6 +62,8 @@ static void init(Ctx& c) {
     // H3S_SAGE_MIN_S sets the shortest sequence that takes the int8 (SageAttention) form
     if (const char* e = std::getenv("H3S_ATTN")) c.sage_want = std::strcmp(e, "onednn") != 0;
     if (const char* e = std::getenv("H3S_SAGE_MIN_S")) c.sage_min_s = std::max<int64_t>(0, std::atoll(e));
+    // the row quantizer's layout: one wavefront a row from this many rows on (four wavefronts a row below)
+    if (const char* e = std::getenv("H3S_QUANT_WAVE_MIN_ROWS")) c.quant_wave_min = std::max<int64_t>(0, std::atoll(e));
 }
 
 static Ctx* open_on(int index) {

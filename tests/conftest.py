@@ -29,3 +29,22 @@ def dev():
     d = Device.open()
     yield d
     d.close()
+
+
+@pytest.fixture(scope="session")
+def dev_wave():
+    """A context whose row quantizer takes the one-wavefront-a-row layout at every size (H3S_QUANT_WAVE_MIN_ROWS=0)
+    where the row shape allows it, so small parity cases reach the layout long inputs use."""
+    from sycl_minimax_h3_amd import Device
+
+    old = os.environ.get("H3S_QUANT_WAVE_MIN_ROWS")
+    os.environ["H3S_QUANT_WAVE_MIN_ROWS"] = "0"
+    try:
+        d = Device.open()
+    finally:
+        if old is None:
+            del os.environ["H3S_QUANT_WAVE_MIN_ROWS"]
+        else:
+            os.environ["H3S_QUANT_WAVE_MIN_ROWS"] = old
+    yield d
+    d.close()

@@ -196,7 +196,9 @@ def test_qk_rms_rope_in_a_qkv_buffer(dev):
                                        (o.ROT_REGULAR, 256), (o.ROT_REGULAR, 64), (o.ROT_REGULAR, 16), (o.ROT_REGULAR, 4)])
 @pytest.mark.parametrize("x_dt,C", [(o.BF16, 4096), (o.BF16, 5376), (o.F32, 1024), (o.BF16, 1024), (o.BF16, 16384), (o.F32, 4096),
                                     (o.F16, 2048)])
-def test_norm_quant(dev, rot, group, x_dt, C):
+@pytest.mark.parametrize("layout", ["four", "wave"])
+def test_norm_quant(request, layout, rot, group, x_dt, C):
+    dev = request.getfixturevalue("dev" if layout == "four" else "dev_wave")
     if group and C % group:
         pytest.skip("group does not divide C")
     if rot == o.ROT_SYLVESTER and group > 64 * (16 // (4 if x_dt == o.F32 else 2)):
@@ -216,7 +218,9 @@ def test_norm_quant(dev, rot, group, x_dt, C):
 @pytest.mark.parametrize("tab_dt", [o.F32, o.BF16])
 @pytest.mark.parametrize("with_rows", [False, True])
 @pytest.mark.parametrize("h_dt", [o.BF16, o.F32, o.F16])
-def test_norm_quant_modulated(dev, tab_dt, with_rows, h_dt):
+@pytest.mark.parametrize("layout", ["four", "wave"])
+def test_norm_quant_modulated(request, layout, tab_dt, with_rows, h_dt):
+    dev = request.getfixturevalue("dev" if layout == "four" else "dev_wave")
     M, C, R = 29, 4096, 3
     x = inputs(24, M * C, o.BF16)
     w = weight(25, C)
@@ -233,8 +237,10 @@ def test_norm_quant_modulated(dev, tab_dt, with_rows, h_dt):
     codes_close(q.to_numpy(), want_q, "codes")
 
 
-def test_norm_quant_edge_rows(dev):
+@pytest.mark.parametrize("layout", ["four", "wave"])
+def test_norm_quant_edge_rows(request, layout):
     """A zero row (scale 1e-30, codes 0), a constant row, huge and tiny rows, and a row count not a multiple of 4."""
+    dev = request.getfixturevalue("dev" if layout == "four" else "dev_wave")
     M, C = 6, 4096
     x = np.random.default_rng(28).standard_normal((M, C)).astype(np.float32)
     x[0] = 0.0
@@ -249,6 +255,25 @@ def test_norm_quant_edge_rows(dev):
     assert_bits_equal(s.to_numpy(), want_s, "scales")
     codes_close(q.to_numpy(), want_q, "codes")
     assert s.to_numpy()[0] == np.float32(1e-30) and not q.to_numpy()[0].any()
+
+
+def test_norm_quant_long_segments(dev):
+    """A long input at the default settings (the one-wavefront-a-row layout): 8200 rows in three table segments, so
+    blocks meet a segment boundary between their steps (the cached table row is re-decoded) and inside a step (rows
+    that decode their own table row), with the Sylvester rotation of config 4."""
+    M, C = 8200, 4096
+    x = inputs(30, M * C, o.BF16)
+    w = weight(31, C)
+    rows = np.where(np.arange(M) < 1500, 0, np.where(np.arange(M) < 5000, 2, 1)).astype(np.int32)
+    sc = o.to_dt(0.5 * np.random.default_rng(32).standard_normal(3 * C).astype(np.float32), o.BF16)
+    sh = o.to_dt(0.5 * np.random.default_rng(33).standard_normal(3 * C).astype(np.float32), o.BF16)
+    want_q, want_s = o.norm_quant(x, o.BF16, M, C, w, 1e-6, rows, sc, sh, o.BF16, o.BF16, rot=o.ROT_SYLVESTER, group=128)
+    q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+    tb = ops.Tables(scale=up(dev, sc, "BF16", [3, C]), shift=up(dev, sh, "BF16", [3, C]), rows=up(dev, rows, "I32", [M]))
+    ops.norm_quant(up(dev, x, "BF16", [M, C]), up(dev, w, "F32", [C]), 1e-6, tb, q, s, rot=o.ROT_SYLVESTER, group=128,
+                   h_dtype=DType.BF16)
+    assert_bits_equal(s.to_numpy(), want_s, "scales")
+    codes_close(q.to_numpy(), want_q, "codes")
 
 
 # ---- h3s_swiglu_quant: swiglu -> the MLP's act scratch -> fc2's quantizer, in one pass ----
@@ -325,7 +350,9 @@ def test_norm_mod_act_gate_float32_and_affine(dev):
 @pytest.mark.parametrize("M,K,N", [(1, 64, 5), (300, 256, 300), (257, 4096, 129), (64, 1024, 512)])
 @pytest.mark.parametrize("group", [0, 4, 16, 64, 256])
 @pytest.mark.parametrize("per_n,bias,out_dt", [(False, False, o.BF16), (True, True, o.BF16), (True, False, o.F32)])
-def test_int8_linear(dev, M, K, N, group, per_n, bias, out_dt):
+@pytest.mark.parametrize("layout", ["four", "wave"])
+def test_int8_linear(request, layout, M, K, N, group, per_n, bias, out_dt):
+    dev = request.getfixturevalue("dev" if layout == "four" else "dev_wave")
     if group and K % group:
         pytest.skip("group does not divide K")
     rng = np.random.default_rng(M * 7 + K + N + group)
