@@ -438,13 +438,14 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
     const int64_t C = A.C, nch = C / V;
     const int64_t b0 = (int64_t) blockIdx.x * NW, U = (int64_t) gridDim.x * NW, M = A.M;
     if (b0 >= M) return;                                    // the whole block
-    int64_t cc[CPL];
+    // chunk slot j: chunk lane + 64 j, clamped to the row's last for lanes past it (32-bit: a row has < 2^31 chunks)
+    int cc[CPL];
     bool ok[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int64_t c = lane + 64 * j;
+        const int c = lane + 64 * j;
         ok[j] = c < nch;
-        cc[j] = ok[j] ? c : nch - 1;
+        cc[j] = ok[j] ? c : (int) nch - 1;
     }
     // the side values of chunk j: 8 floats at ((j * 2 + half) * 64 + lane) * 4 of an array
     auto side_at = [&](int off, int j, int h) { return side + off + ((j * 2 + h) * 64 + lane) * 4; };
@@ -460,8 +461,8 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
     // one table row's 1 + scale and shift for chunk j, decoded from memory
     auto table8 = [&](int64_t trow, int j, float* s1, float* sh) {
         Raw<V, TDT == H3S_F32> sr, hr;
-        fetch(sr, A.scale, TDT, trow * C + cc[j] * V);
-        fetch(hr, A.shift, TDT, trow * C + cc[j] * V);
+        fetch(sr, A.scale, TDT, trow * C + (int64_t) cc[j] * V);
+        fetch(hr, A.shift, TDT, trow * C + (int64_t) cc[j] * V);
         decode(sr, TDT, s1);
         decode(hr, TDT, sh);
 #pragma unroll
@@ -476,7 +477,7 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
                 if constexpr (HASW) {
                     if (with_w) {
                         Raw<V, true> wr;
-                        fetch(wr, A.w, H3S_F32, cc[jj] * V);
+                        fetch(wr, A.w, H3S_F32, (int64_t) cc[jj] * V);
                         float f[V];
                         decode(wr, H3S_F32, f);
                         put8(WOFF, jj, f);
