@@ -44,6 +44,11 @@ def bytes_cfg():
         "cfg5a_rmsnorm_mod_quant_47104": M4 * C * 2 + M4 * C + M4 * 4,
         "cfg5b_int8_gemm_silu_47104x16384": M4 * C + 16384 * C + M4 * 4 + 16384 * 4 + M4 * 16384 * 2,
         "mlp_swiglu_quant_g256_47104x8192": M4 * 16384 * 2 + M4 * 8192 + M4 * 4,
+        # the other token count of the north star's pair (16.8k and 47k tokens x 4096) for configs 2-5a
+        "cfg2_ln_mod_gelu_gate_47104": 3 * M4 * C * 2,
+        "cfg3_qk_rmsnorm_rope3d_47104": 4 * M4 * 32 * 128 * 2 + M4 * 64 * 2 * 4,
+        "cfg4_rmsnorm_wht128_quant_16896": M2 * C * 2 + M2 * C + M2 * 4,
+        "cfg5a_rmsnorm_mod_quant_16896": M2 * C * 2 + M2 * C + M2 * 4,
         "attn_sage_16896x32x128": 4 * M2 * 4096 * 2,     # q, k, v read, out written (the products are the bound)
         "attn_sage_47104x32x128": 4 * M4 * 4096 * 2,
     }
@@ -190,6 +195,21 @@ def main() -> int:
     q6, s6 = torch.empty(M4, 8192, dtype=torch.int8, device=dev_t), torch.empty(M4, device=dev_t)
     X6, Q6, S6 = O5, T(q6), T(s6)    # the GEMM's output rows are [gate | up] halves of 8192
     run("mlp_swiglu_quant_g256_47104x8192", lambda: ops.swiglu_quant(X6, Q6, S6, rot=A.ROT_REGULAR, group=256))
+
+    # ---- configs 2-5a at the other token count: 47104 tokens (grid T46 x H32 x W32) for 2 and 3, 16896 for 4 and 5a ----
+    x2b, r2b, o2b = bf16(M4, C), bf16(M4, C), torch.empty(M4, C, dtype=torch.bfloat16, device=dev_t)
+    X2b, R2b, O2b = T(x2b), T(r2b), T(o2b)
+    run("cfg2_ln_mod_gelu_gate_47104", lambda: ops.norm_mod_act_gate(X2b, A.NORM_LAYER, None, None, 1e-5, tb2, A.ACT_GELU_TANH, R2b, O2b))
+    del x2b, r2b, o2b, X2b, R2b, O2b
+    q3b, k3b = bf16(M4, 32 * 128), bf16(M4, 32 * 128)
+    cs3b = torch.from_numpy(rope_table(46, 32, 32)).to(dev_t)
+    Q3b, K3b, CS3b = T(q3b), T(k3b), T(cs3b)
+    run("cfg3_qk_rmsnorm_rope3d_47104", lambda: ops.qk_rms_rope(ops.Rows(Q3b, 0, 4096, M4, 32, 128), ops.Rows(K3b, 0, 4096, M4, 32, 128),
+                                                                 WQ, WK, 1e-5, CS3b, 128))
+    del q3b, k3b, cs3b, Q3b, K3b, CS3b
+    X4s, Q4s, S4s, X5s = T(x4[:M2]), T(q4[:M2]), T(s4[:M2]), T(x5[:M2])
+    run("cfg4_rmsnorm_wht128_quant_16896", lambda: ops.norm_quant(X4s, G1, 1e-6, None, Q4s, S4s, rot=A.ROT_SYLVESTER, group=128))
+    run("cfg5a_rmsnorm_mod_quant_16896", lambda: ops.norm_quant(X5s, G1, 1e-6, tb5, Q4s, S4s))
 
     # ---- attention of the 16896-token grid, 32 heads of 128 (the int8 form: S >= 8192) ----
     qkv7 = bf16(M2, 3 * 4096)
