@@ -33,7 +33,7 @@ static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S,
     };
     if (sage) {
         const int64_t hd = Hkv * D;
-        if (vec) attn_kmean_kernel<DT><<<(unsigned) (hd / 64), 256, 0, c->stream>>>(k, S, kv_stride, km);
+        if (vec) attn_kmean_kernel<DT><<<(unsigned) (hd / kKmeanFeat), 256, 0, c->stream>>>(k, S, kv_stride, km);
         else attn_kmean_rows_kernel<DT><<<(unsigned) ((hd + 255) / 256), 256, 0, c->stream>>>(k, S, hd, kv_stride, km);
         qk(q, qs_stride, qblocks, nullptr, aq, qs);
         qk(k, kv_stride, kvblocks, km, ak, ks);

@@ -50,53 +50,105 @@ __device__ __forceinline__ uint16_t half_bits(float x) {
     return b;
 }
 
-// k's mean over the sequence per (head, feature): a float32 sum in token order, / S (h3sycl.cpp:1729-1733). A block
-// takes 64 features: all 256 threads stage 32 KiB of rows at a time into LDS with 16-byte loads (the next stage in
-// flight), and the first wavefront runs the 64 sums, one feature a lane, in token order. Needs the rows 16-byte
-// aligned (k and the stride); attn_kmean_rows_kernel is the general form.
+// k's mean over the sequence per (head, feature): a float32 sum in token order, / S (h3sycl.cpp:1732-1737). Each
+// feature's sum is one serial chain of S additions, so the kernel is built to run that chain at the adder's latency:
+// a block takes 32 features (128 blocks at 4096 features); all its wavefronts fill a ring of four 16 KiB row chunks
+// with direct loads (global_load_lds_dwordx4, three chunks in flight), and the first wavefront runs the 32 sums, one
+// feature a lane, reading 16 rows ahead of the additions. Needs the rows 16-byte aligned (k and the stride);
+// attn_kmean_rows_kernel is the general form.
+constexpr int kKmeanFeat = 32, kKmeanStages = 4, kKmeanChunk = 16384;
 template <int DT>
 __global__ __launch_bounds__(256) void attn_kmean_kernel(const void* __restrict__ k, int64_t S, int64_t stride,
                                                          float* __restrict__ mean) {
-    constexpr int ESZ = DT == H3S_F32 ? 4 : 2, ROWS = 32768 / (64 * ESZ), CPR = 64 * ESZ / 16, LOADS = ROWS * CPR / 256;
-    __shared__ uint4 buf[2][ROWS * CPR];
-    const int tid = threadIdx.x;
-    const int64_t c0 = (int64_t) blockIdx.x * 64, nch = (S + ROWS - 1) / ROWS;
+    constexpr int ESZ = DT == H3S_F32 ? 4 : 2, RB = kKmeanFeat * ESZ;          // bytes of a row's 32 features
+    constexpr int SEG = RB / 16, ROWS = kKmeanChunk / RB, LPT = kKmeanChunk / (256 * 16);
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kKmeanStages * kKmeanChunk];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t c0 = (int64_t) blockIdx.x * kKmeanFeat, nch = (S + ROWS - 1) / ROWS;
     const char* base = reinterpret_cast<const char*>(k) + c0 * ESZ;
-    uint4 reg[LOADS];
-    auto load = [&](int64_t ch) {
+    // load i of this thread: unit u = tid + 256 i of the chunk (row u / SEG, 16-byte segment u % SEG), landing at
+    // byte 16 u of the stage: the chunk is row-major, RB bytes a row
+    auto issue = [&](int64_t ch) {
+        uint8_t* st = ring + (ch % kKmeanStages) * kKmeanChunk;
 #pragma unroll
-        for (int i = 0; i < LOADS; ++i) {
-            const int u = tid + 256 * i, r = u / CPR, cc = u % CPR;
-            const int64_t row = ch * ROWS + r;
-            reg[i] = row < S ? *reinterpret_cast<const uint4*>(base + row * stride * ESZ + 16 * cc) : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < LPT; ++i) {
+            const int u = tid + 256 * i;
+            int64_t row = ch * ROWS + u / SEG;
+            row = row < S ? row : S - 1;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) (base + row * stride * ESZ + 16 * (u % SEG)),
+                                             (__attribute__((address_space(3))) void*) (st + (4 * i + wave) * 1024), 16, 0, 0);
         }
     };
-    auto store = [&](int st) {
-#pragma unroll
-        for (int i = 0; i < LOADS; ++i) buf[st][tid + 256 * i] = reg[i];
-    };
     float sum = 0.0f;
-    load(0);
-    store(0);
-    __syncthreads();
+    for (int64_t ch = 0; ch < kKmeanStages - 1 && ch < nch; ++ch) issue(ch);
     for (int64_t ch = 0; ch < nch; ++ch) {
-        if (ch + 1 < nch) load(ch + 1);
-        if (tid < 64) {
+        // this chunk has landed once the loads of the (at most two) chunks issued after it are all that is left
+        const int64_t after = (nch - 1 - ch) < kKmeanStages - 2 ? nch - 1 - ch : kKmeanStages - 2;
+        if (after >= 2) wait_vm<2 * LPT>();
+        else if (after == 1) wait_vm<LPT>();
+        else wait_vm<0>();
+        lds_barrier();                       // every wavefront's loads of chunk ch are in; chunk ch - 1 is summed
+        if (ch + kKmeanStages - 1 < nch) issue(ch + kKmeanStages - 1);   // into chunk ch - 1's stage
+        if (wave == 0 && lane < kKmeanFeat) {
+            const uint32_t at = (uint32_t) (uintptr_t) (ring + (ch % kKmeanStages) * kKmeanChunk) + lane * ESZ;
             const int rows = S - ch * ROWS < ROWS ? (int) (S - ch * ROWS) : ROWS;
-            const char* b = reinterpret_cast<const char*>(buf[ch & 1]) + tid * ESZ;
-            for (int r = 0; r < rows; ++r) {
-                const char* e = b + r * 64 * ESZ;
+            // rows read in asm, 16 at a time and 16 rows ahead of the additions, with a wait tied to the values (the
+            // compiler would otherwise wait for every direct load in flight before a read of the ring)
+            auto read16 = [&](uint32_t (&v)[16], uint32_t a) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    if constexpr (ESZ == 2) asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v[i]) : "v"(a), "i"(i * RB) : "memory");
+                    else asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v[i]) : "v"(a), "i"(i * RB) : "memory");
+                }
+            };
+            auto wait16 = [&](uint32_t (&v)[16]) {
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                             "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]),
+                             "+v"(v[14]), "+v"(v[15]));
+            };
+            auto add16 = [&](const uint32_t (&v)[16]) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    float x;
+                    if constexpr (DT == H3S_F32) x = __uint_as_float(v[i]);
+                    else if constexpr (DT == H3S_BF16) x = bf16_lo(v[i]);
+                    else x = f16_lo(v[i]);
+                    sum = sum + x;
+                }
+            };
+            const int full = rows / 16 * 16;
+            uint32_t va[16], vb[16];
+            if (full > 0) {
+                read16(va, at);
+                wait16(va);
+            }
+            int r = 0;
+            for (; r < full; r += 32) {
+                const bool b1 = r + 16 < full, b2 = r + 32 < full;
+                if (b1) read16(vb, at + (r + 16) * RB);
+                add16(va);
+                if (b1) {
+                    wait16(vb);
+                    if (b2) read16(va, at + (r + 32) * RB);
+                    add16(vb);
+                    if (b2) wait16(va);
+                }
+            }
+            r = full;
+            for (; r < rows; ++r) {
+                const uint8_t* e = ring + (ch % kKmeanStages) * kKmeanChunk + r * RB + lane * ESZ;
+                uint32_t v;
+                if constexpr (ESZ == 2) asm volatile("ds_read_u16 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"((uint32_t) (uintptr_t) e) : "memory");
+                else asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"((uint32_t) (uintptr_t) e) : "memory");
                 float x;
-                if constexpr (DT == H3S_F32) x = *reinterpret_cast<const float*>(e);
-                else if constexpr (DT == H3S_BF16) x = bf16_lo(*reinterpret_cast<const uint16_t*>(e));
-                else x = f16_lo(*reinterpret_cast<const uint16_t*>(e));
+                if constexpr (DT == H3S_F32) x = __uint_as_float(v);
+                else if constexpr (DT == H3S_BF16) x = bf16_lo(v);
+                else x = f16_lo(v);
                 sum = sum + x;
             }
         }
-        if (ch + 1 < nch) store((ch + 1) & 1);
-        __syncthreads();
     }
-    if (tid < 64) mean[c0 + tid] = sum / (float) S;
+    if (wave == 0 && lane < kKmeanFeat) mean[c0 + lane] = sum / (float) S;
 }
 // the same sums with element loads, for rows that are not 16-byte aligned
 template <int DT>
