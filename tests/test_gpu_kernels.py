@@ -257,14 +257,19 @@ def test_norm_quant_edge_rows(request, layout):
     assert s.to_numpy()[0] == np.float32(1e-30) and not q.to_numpy()[0].any()
 
 
-def test_norm_quant_long_segments(dev):
-    """A long input at the default settings (the one-wavefront-a-row layout): 8200 rows in three table segments, so
-    blocks meet a segment boundary between their steps (the cached table row is re-decoded) and inside a step (rows
-    that decode their own table row), with the Sylvester rotation of config 4."""
+@pytest.mark.parametrize("pattern", ["segments", "random"])
+def test_norm_quant_long_segments(dev, pattern):
+    """A long input at the default settings (the one-wavefront-a-row layout), 8200 rows, with the Sylvester rotation
+    of config 4. segments: three table segments, so blocks meet a segment boundary between their steps (the cached
+    table row is re-decoded) and inside a step (rows that decode their own table row); random: a table row drawn per
+    row, so the cached row changes at almost every step."""
     M, C = 8200, 4096
     x = inputs(30, M * C, o.BF16)
     w = weight(31, C)
-    rows = np.where(np.arange(M) < 1500, 0, np.where(np.arange(M) < 5000, 2, 1)).astype(np.int32)
+    if pattern == "segments":
+        rows = np.where(np.arange(M) < 1500, 0, np.where(np.arange(M) < 5000, 2, 1)).astype(np.int32)
+    else:
+        rows = np.random.default_rng(34).integers(0, 3, M).astype(np.int32)
     sc = o.to_dt(0.5 * np.random.default_rng(32).standard_normal(3 * C).astype(np.float32), o.BF16)
     sh = o.to_dt(0.5 * np.random.default_rng(33).standard_normal(3 * C).astype(np.float32), o.BF16)
     want_q, want_s = o.norm_quant(x, o.BF16, M, C, w, 1e-6, rows, sc, sh, o.BF16, o.BF16, rot=o.ROT_SYLVESTER, group=128)
