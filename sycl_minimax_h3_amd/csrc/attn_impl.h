@@ -421,22 +421,21 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int r = 32 * j + ql;
+            // the half's NQF fragments of K read together, then its NQF products
+            v4i_a kf[NQF];
+#pragma unroll
+            for (int kk = 0; kk < NQF; ++kk) kf[kk] = *reinterpret_cast<const v4i_a*>(st + (r * CPR + attn_swz<CPR>(r, 2 * kk + hl)) * 16);
             if constexpr (SAGE) {
                 v16i_a a = (v16i_a) 0;
 #pragma unroll
-                for (int kk = 0; kk < NQF; ++kk) {
-                    const v4i_a kf = *reinterpret_cast<const v4i_a*>(st + (r * CPR + attn_swz<CPR>(r, 2 * kk + hl)) * 16);
-                    a = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[kk], a, 0, 0, 0);
-                }
+                for (int kk = 0; kk < NQF; ++kk) a = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[kk], qf[kk], a, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 16; ++i) x[16 * j + i] = (float) a[i];
             } else {
                 v16f_a a = (v16f_a) 0.0f;
 #pragma unroll
-                for (int kk = 0; kk < NQF; ++kk) {
-                    const v4i_a kf = *reinterpret_cast<const v4i_a*>(st + (r * CPR + attn_swz<CPR>(r, 2 * kk + hl)) * 16);
-                    a = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, kf), __builtin_bit_cast(v8h_a, qf[kk]), a, 0, 0, 0);
-                }
+                for (int kk = 0; kk < NQF; ++kk)
+                    a = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, kf[kk]), __builtin_bit_cast(v8h_a, qf[kk]), a, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 16; ++i) x[16 * j + i] = a[i];
             }
@@ -500,12 +499,16 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
             v4i_a pf;
             pf[0] = (int) a0; pf[1] = (int) a1; pf[2] = (int) b0; pf[3] = (int) b1;
             const v8h_a pb = __builtin_bit_cast(v8h_a, pf);
+            // the step's NDT fragments of V^T read together, then its NDT products
+            v4i_a vf[NDT];
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
                 const int r = 32 * dt + ql;
-                const v4i_a vf = *reinterpret_cast<const v4i_a*>(st + KTB + (r * 8 + attn_swz<8>(r, 2 * s + hl)) * 16);
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, vf), pb, o[dt], 0, 0, 0);
+                vf[dt] = *reinterpret_cast<const v4i_a*>(st + KTB + (r * 8 + attn_swz<8>(r, 2 * s + hl)) * 16);
             }
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, vf[dt]), pb, o[dt], 0, 0, 0);
         }
         l = l + ls;
     };
