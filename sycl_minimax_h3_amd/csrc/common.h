@@ -216,8 +216,8 @@ template <int TDT> __device__ __forceinline__ void load_tab(const void* p, int64
 }
 
 // ---- cross-lane exchanges inside a 64-wide wavefront ----
-// value of lane (lane ^ OFF). 1, 2: quad permutes; 4: two row shifts, each for half of the lanes; 8: a row rotate;
-// 16: a swizzle inside each half of the wave; 32: a permute through the LDS crossbar.
+// value of lane (lane ^ OFF). 1, 2: quad permutes; 4: two row shifts, each for half of the lanes; 7: the half-row
+// mirror; 8: a row rotate; 16: a swizzle inside each half of the wave; 32: a permute through the LDS crossbar.
 template <int OFF> __device__ __forceinline__ float xor_lane(float v) {
     const int x = __float_as_int(v);
     int r;
@@ -226,7 +226,8 @@ template <int OFF> __device__ __forceinline__ float xor_lane(float v) {
     else if constexpr (OFF == 4) {
         const int t = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0x5, false);                   // row_shl:4, lanes 0-3, 8-11
         r = __builtin_amdgcn_update_dpp(t, x, 0x114, 0xF, 0xA, false);                             // row_shr:4, lanes 4-7, 12-15
-    } else if constexpr (OFF == 8) r = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);  // row_ror:8
+    } else if constexpr (OFF == 7) r = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    else if constexpr (OFF == 8) r = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);    // row_ror:8
     else if constexpr (OFF == 16) r = __builtin_amdgcn_ds_swizzle(x, 0x401F);                     // xor 16 within 32
     else {
         static_assert(OFF == 32, "xor_lane: offsets 1..32");
@@ -235,12 +236,15 @@ template <int OFF> __device__ __forceinline__ float xor_lane(float v) {
     return __int_as_float(r);
 }
 
-// the canonical butterfly over the lanes of a wave (offsets L/2 .. 1); every lane ends with the same sum
-template <int L> __device__ __forceinline__ float wave_sum(float s) {
+// the canonical butterfly over the lanes of a wave (offsets L/2 .. 1); every lane ends with the same sum. With SW
+// the lanes hold their values at the positions l ^ 3 bit2(l) (an involution inside each run of 8 lanes): the
+// position's partner 4 away is then the lane 7 away, and the others are unmoved, so the same tree of additions
+// over positions is formed.
+template <int L, bool SW = false> __device__ __forceinline__ float wave_sum(float s) {
     if constexpr (L >= 64) s = s + xor_lane<32>(s);
     if constexpr (L >= 32) s = s + xor_lane<16>(s);
     if constexpr (L >= 16) s = s + xor_lane<8>(s);
-    if constexpr (L >= 8) s = s + xor_lane<4>(s);
+    if constexpr (L >= 8) s = s + xor_lane<SW ? 7 : 4>(s);
     if constexpr (L >= 4) s = s + xor_lane<2>(s);
     if constexpr (L >= 2) s = s + xor_lane<1>(s);
     return s;

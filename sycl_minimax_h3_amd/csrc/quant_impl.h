@@ -68,15 +68,23 @@ template <int V, int H> __device__ __forceinline__ void syl_in(float (&v)[V]) {
             v[e + H] = a - b;
         }
 }
-// The stages across lanes keep each lane's values up to a sign fixed by the lane: at the stage S lanes apart the
-// lower lane forms own + partner and the upper lane own - partner, which is the negation of the a - b it owes.
-// Both partners carry the same sign from the earlier stages (they differ only in lane bit S), and rounding to
+// The stages across lanes keep each lane's values up to a sign fixed by the lane: at the stage S chunks apart the
+// lower chunk forms own + partner and the upper chunk own - partner, which is the negation of the a - b it owes.
+// Both partners carry the same sign from the earlier stages (they differ only in chunk bit S), and rounding to
 // nearest is symmetric, so every value stays exactly +-(the value of the plain butterfly); the sign is
-// (-1)^popcount(lane & (G/V - 1)), folded into the final multiply by fl(1/sqrt(G)). One fused multiply-add with the
-// partner's value taken straight from a neighbouring lane (own + partner * (+-1)) per value and stage.
-// For partners 1, 2 or 8 lanes away the partner's value comes through the DPP operand of v_fmac_f32 itself (one
-// instruction a value); s_nop 1 gives the two wait states a DPP read needs after the VALU write of the previous stage.
-#define H3_FMAC_DPP8(CTRL)                                                                                      \
+// (-1)^popcount(pos & (G/V - 1)) for the lane's chunk position pos in its group, folded into the final multiply by
+// fl(1/sqrt(G)). One fused multiply-add with the partner's value taken straight from a neighbouring lane
+// (own + partner * (+-1)) per value and stage.
+// Chunk positions: in the plain layout (SW false) lane l holds position l of its run of 16 lanes, so the partner S
+// chunks away is lane l ^ S. In the swapped layout (SW true) lane l holds position swap3(l) = l ^ 3 bit2(l), an
+// involution that leaves the partners 1, 2, 8, 16 and 32 chunks away at lanes l ^ 1, l ^ 2, l ^ 8, l ^ 16 and
+// l ^ 32, and moves the partner 4 chunks away to lane l ^ 7, which DPP's row_half_mirror reaches in one instruction
+// (l ^ 4 takes two).
+// For partners 1, 2 or 8 lanes away (and 7 in the swapped layout) the partner's value comes through the DPP operand
+// of v_fmac_f32 itself (one instruction a value); s_nop 1 gives the two wait states a DPP read needs after the VALU
+// write of the previous stage.
+__device__ __forceinline__ int swap3(int l) { return l ^ (((l >> 2) & 1) * 3); }
+#define H3_FMAC_DPP8(CTRL, SRC)                                                                                 \
     asm volatile("s_nop 1\n"                                                                                    \
                  "v_fmac_f32_dpp %0, %8, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                             \
                  "v_fmac_f32_dpp %1, %9, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                             \
@@ -87,15 +95,18 @@ template <int V, int H> __device__ __forceinline__ void syl_in(float (&v)[V]) {
                  "v_fmac_f32_dpp %6, %14, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                            \
                  "v_fmac_f32_dpp %7, %15, %16 " CTRL " row_mask:0xf bank_mask:0xf"                               \
                  : "=v"(o[0]), "=v"(o[1]), "=v"(o[2]), "=v"(o[3]), "=v"(o[4]), "=v"(o[5]), "=v"(o[6]), "=v"(o[7]) \
-                 : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]), "v"(sg), \
-                   "0"(v[0]), "1"(v[1]), "2"(v[2]), "3"(v[3]), "4"(v[4]), "5"(v[5]), "6"(v[6]), "7"(v[7]))
-template <int V, int S> __device__ __forceinline__ void syl_x(float (&v)[V], int lane) {
-    const float sg = (lane & S) ? -1.0f : 1.0f;
-    if constexpr (V == 8 && (S == 1 || S == 2 || S == 8)) {
+                 : "v"(SRC[0]), "v"(SRC[1]), "v"(SRC[2]), "v"(SRC[3]), "v"(SRC[4]), "v"(SRC[5]), "v"(SRC[6]),      \
+                   "v"(SRC[7]), "v"(sg), "0"(v[0]), "1"(v[1]), "2"(v[2]), "3"(v[3]), "4"(v[4]), "5"(v[5]),       \
+                   "6"(v[6]), "7"(v[7]))
+template <int V, int S, bool SW> __device__ __forceinline__ void syl_x(float (&v)[V], int pos) {
+    static_assert(!SW || V == 8, "syl_x: the swapped layout has 8 values a chunk");
+    const float sg = (pos & S) ? -1.0f : 1.0f;
+    if constexpr (V == 8 && (S == 1 || S == 2 || S == 8 || (S == 4 && SW))) {
         float o[8];
-        if constexpr (S == 1) H3_FMAC_DPP8("quad_perm:[1,0,3,2]");
-        else if constexpr (S == 2) H3_FMAC_DPP8("quad_perm:[2,3,0,1]");
-        else H3_FMAC_DPP8("row_ror:8");
+        if constexpr (S == 1) H3_FMAC_DPP8("quad_perm:[1,0,3,2]", v);
+        else if constexpr (S == 2) H3_FMAC_DPP8("quad_perm:[2,3,0,1]", v);
+        else if constexpr (S == 4) H3_FMAC_DPP8("row_half_mirror", v);
+        else H3_FMAC_DPP8("row_ror:8", v);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = o[e];
     } else if constexpr (V == 8 && S == 4) {
@@ -103,18 +114,7 @@ template <int V, int S> __device__ __forceinline__ void syl_x(float (&v)[V], int
         float x[8], o[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[e]), 0x1B, 0xF, 0xF, true));
-        asm volatile("s_nop 1\n"
-                     "v_fmac_f32_dpp %0, %8, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
-                     "v_fmac_f32_dpp %1, %9, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
-                     "v_fmac_f32_dpp %2, %10, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
-                     "v_fmac_f32_dpp %3, %11, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
-                     "v_fmac_f32_dpp %4, %12, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
-                     "v_fmac_f32_dpp %5, %13, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
-                     "v_fmac_f32_dpp %6, %14, %16 row_half_mirror row_mask:0xf bank_mask:0xf\n"
-                     "v_fmac_f32_dpp %7, %15, %16 row_half_mirror row_mask:0xf bank_mask:0xf"
-                     : "=v"(o[0]), "=v"(o[1]), "=v"(o[2]), "=v"(o[3]), "=v"(o[4]), "=v"(o[5]), "=v"(o[6]), "=v"(o[7])
-                     : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(sg),
-                       "0"(v[0]), "1"(v[1]), "2"(v[2]), "3"(v[3]), "4"(v[4]), "5"(v[5]), "6"(v[6]), "7"(v[7]));
+        H3_FMAC_DPP8("row_half_mirror", x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = o[e];
     } else {
@@ -123,22 +123,22 @@ template <int V, int S> __device__ __forceinline__ void syl_x(float (&v)[V], int
     }
 }
 #undef H3_FMAC_DPP8
-// the sign the cross-lane stages leave on this lane's values
-template <int V> __device__ __forceinline__ float syl_sign(int lane, int G) {
+// the sign the cross-lane stages leave on the values of the chunk at position pos
+template <int V> __device__ __forceinline__ float syl_sign(int pos, int G) {
     const int span = G / V;                               // lanes of a group (1 when the group is inside a chunk)
-    return span > 1 && (__builtin_popcount((unsigned) (lane & (span - 1))) & 1) ? -1.0f : 1.0f;
+    return span > 1 && (__builtin_popcount((unsigned) (pos & (span - 1))) & 1) ? -1.0f : 1.0f;
 }
-template <int V> __device__ __forceinline__ void sylvester(float (&v)[V], int lane, int G) {
+template <int V, bool SW = false> __device__ __forceinline__ void sylvester(float (&v)[V], int pos, int G) {
     if (G > 1) syl_in<V, 1>(v);
     if (G > 2) syl_in<V, 2>(v);
     if constexpr (V == 8)
         if (G > 4) syl_in<V, 4>(v);
-    if (G > V) syl_x<V, 1>(v, lane);
-    if (G > 2 * V) syl_x<V, 2>(v, lane);
-    if (G > 4 * V) syl_x<V, 4>(v, lane);
-    if (G > 8 * V) syl_x<V, 8>(v, lane);
-    if (G > 16 * V) syl_x<V, 16>(v, lane);
-    if (G > 32 * V) syl_x<V, 32>(v, lane);
+    if (G > V) syl_x<V, 1, SW>(v, pos);
+    if (G > 2 * V) syl_x<V, 2, SW>(v, pos);
+    if (G > 4 * V) syl_x<V, 4, SW>(v, pos);
+    if (G > 8 * V) syl_x<V, 8, SW>(v, pos);
+    if (G > 16 * V) syl_x<V, 16, SW>(v, pos);
+    if (G > 32 * V) syl_x<V, 32, SW>(v, pos);
 }
 
 // ---- regular: one base-4 digit at a time, low digit first (kernels/h3sycl.cpp:433-459); for the four values
@@ -191,6 +191,14 @@ template <int V> __device__ __forceinline__ void regular(float (&v)[V], int G) {
     }
 }
 
+// A kernel's ROT template value: the rotation kind (H3S_ROT_NONE, H3S_ROT_REGULAR or H3S_ROT_SYLVESTER) in the low
+// four bits, and above them a group size fixed at compile time (0: the group size of the call). A fixed group turns
+// the butterfly's stage tests into constants, so the stages run as one straight block with no register copies at
+// the joins of skipped stages.
+constexpr int rot_kind(int rot) { return rot & 15; }
+constexpr int rot_fixed(int rot) { return rot >> 4; }
+constexpr int rot_with(int kind, int group) { return kind | (group << 4); }
+
 struct QuantArgs {
     const void* x;
     int64_t M, C;
@@ -219,7 +227,7 @@ struct QuantArgs {
 // while this one is computed.
 template <int XDT, int CPL, int ROT, int F>
 __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int64_t rpu) {
-    constexpr bool ROTATED = ROT != H3S_ROT_NONE;
+    constexpr bool ROTATED = rot_kind(ROT) != H3S_ROT_NONE;
     constexpr int V = Vec<XDT>::V;
     constexpr bool DYN = F & ROW_DYN;
     constexpr bool TW = DYN || (F & ROW_TAB32);
@@ -302,7 +310,8 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
     };
 
     // the normalization of a rotated group, with the sign the Sylvester cross-lane stages leave on this lane
-    const float cgs = ROT == H3S_ROT_SYLVESTER ? A.cg * syl_sign<V>(lane, A.group) : A.cg;
+    const int G = rot_fixed(ROT) ? rot_fixed(ROT) : A.group;
+    const float cgs = rot_kind(ROT) == H3S_ROT_SYLVESTER ? A.cg * syl_sign<V>(lane, G) : A.cg;
     int slot = 0;   // consecutive reductions use alternate LDS slots
     for (int64_t row = r0; row < r1; ++row) {
         // the next row's x and table row index, in flight during this row
@@ -364,8 +373,8 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             if constexpr (ROTATED) {
-                if constexpr (ROT == H3S_ROT_SYLVESTER) sylvester<V>(v[j], lane, A.group);
-                else regular<V>(v[j], A.group);
+                if constexpr (rot_kind(ROT) == H3S_ROT_SYLVESTER) sylvester<V>(v[j], lane, G);
+                else regular<V>(v[j], G);
 #pragma unroll
                 for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * cgs;
             }
@@ -401,11 +410,11 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
     }
 }
 
-// ---- one wavefront a row, for rows of 256 to 512 16-byte chunks of a 16-bit type (2048 to 4096 features) ----
+// ---- one wavefront a row, for rows of exactly 64 CPL 16-byte chunks of a 16-bit type (2048 or 4096 features) ----
 // The same arithmetic as quant_kernel, laid out so that the row's scalar work is done once: quant_kernel spreads
 // such a row over four wavefronts, each of which repeats the row's statistics (the butterflies, the LDS combine
 // and its barrier, the divisions and the square root). Here lane t of the wavefront holds chunks t + 64 j
-// (j < CPL), and the row statistics keep the order of the 256-lane layout that the oracle restates: chunk slot j
+// (j < CPL), every one inside the row, and the row statistics keep the order of the 256-lane layout that the oracle restates: chunk slot j
 // belongs to canonical wavefront j % 4 (chunk t + 64 j is canonical lane (t + 64 j) % 256), so a lane keeps four
 // partial sums, each summed over the wavefront by the butterfly and then combined as (w0 + w2) + (w1 + w3).
 //
@@ -426,7 +435,7 @@ template <int XDT, int CPL, int ROT, int F>
 __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
     static_assert(XDT != H3S_F32 && !(F & (ROW_DYN | ROW_SWIGLU)), "quant_wave_kernel: 16-bit x, exact side inputs");
     constexpr int V = 8;
-    constexpr bool ROTATED = ROT != H3S_ROT_NONE;
+    constexpr bool ROTATED = rot_kind(ROT) != H3S_ROT_NONE;
     constexpr bool NORM = !(F & ROW_RAW);
     constexpr bool HASW = F & ROW_W;
     constexpr bool TAB = F & ROW_TAB;
@@ -435,18 +444,16 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
     extern __shared__ __align__(16) float side[];
     const int lane = (int) (threadIdx.x & 63), NW = (int) (blockDim.x >> 6);
     const int wave = (int) wave_uniform(threadIdx.x >> 6);
-    const int64_t C = A.C, nch = C / V;
+    const int64_t C = 64 * CPL * V;                         // the launch checks A.C against this
     const int64_t b0 = (int64_t) blockIdx.x * NW, U = (int64_t) gridDim.x * NW, M = A.M;
     if (b0 >= M) return;                                    // the whole block
-    // chunk slot j: chunk lane + 64 j, clamped to the row's last for lanes past it (32-bit: a row has < 2^31 chunks)
+    // chunk slot j: chunk 64 j + pos, pos = the lane (swap3 of the lane for the Sylvester rotation, whose stage 4
+    // chunks apart then pairs lanes 7 apart: one DPP operand instead of two)
+    constexpr bool SW = rot_kind(ROT) == H3S_ROT_SYLVESTER;
+    const int pos = SW ? swap3(lane) : lane;
     int cc[CPL];
-    bool ok[CPL];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int c = lane + 64 * j;
-        ok[j] = c < nch;
-        cc[j] = ok[j] ? c : (int) nch - 1;
-    }
+    for (int j = 0; j < CPL; ++j) cc[j] = pos + 64 * j;
     // the side values of chunk j: 8 floats at ((j * 2 + half) * 64 + lane) * 4 of an array
     auto side_at = [&](int off, int j, int h) { return side + off + ((j * 2 + h) * 64 + lane) * 4; };
     auto put8 = [&](int off, int j, const float* f) {
@@ -498,7 +505,8 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
         lds_barrier();
     }
 
-    const float cgs = ROT == H3S_ROT_SYLVESTER ? A.cg * syl_sign<V>(lane, A.group) : A.cg;
+    const int G = rot_fixed(ROT) ? rot_fixed(ROT) : A.group;
+    const float cgs = SW ? A.cg * syl_sign<V>(pos, G) : A.cg;
     auto load_row = [&](uint4 (&xr)[CPL], int64_t row) {
         const uint4* xp = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * 2);
 #pragma unroll
@@ -520,11 +528,9 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
         own = __builtin_amdgcn_readlane(tix, (int) (k - kbase));
         first = __builtin_amdgcn_readlane(gix, (int) (k - kbase));
     };
-    uint4 x0[CPL];
-    int64_t row = b0 + wave;
-    // rows left to this wavefront and to the block's first wavefront: the block steps while its first row exists
-    if (row < M) load_row(x0, row);
-    for (int64_t k = 0, first = b0; first < M; row += U, first += U, ++k) {
+    // One row: x of this row in xc, the next row's x loaded into xn. (Alternating two buffers instead of the copy
+    // at the end of each row needs two copies of this code and more registers than the copy costs.)
+    auto step = [&](uint4 (&xc)[CPL], uint4 (&xn)[CPL], int64_t k, int64_t row) {
         int64_t trow = 0;
         if constexpr (TAB) {
             if (A.rows) {
@@ -538,24 +544,22 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
                 }
             }
         }
-        if (row >= M) continue;                              // past the end: only the barriers above remain to keep
-        uint4 x1[CPL];
-        if (row + U < M) load_row(x1, row + U);
+        if (row >= M) return;                                // past the end: only the barriers above remain to keep
+        if (row + U < M) load_row(xn, row + U);
         float v[CPL][V];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(x0[j], v[j]);
+        for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(xc[j], v[j]);
 
         // ---- rms_norm_mod into bfloat16 (the reference's scratch h) ----
         if constexpr (NORM) {
             float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < CPL; ++j)
-                if (ok[j])
 #pragma unroll
-                    for (int e = 0; e < V; ++e) ss[j % 4] = __builtin_fmaf(v[j][e], v[j][e], ss[j % 4]);
+                for (int e = 0; e < V; ++e) ss[j % 4] = __builtin_fmaf(v[j][e], v[j][e], ss[j % 4]);
             float w4[4];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) w4[g] = wave_sum<64>(ss[g]);
+            for (int g = 0; g < 4; ++g) w4[g] = wave_sum<64, SW>(ss[g]);
             const float inv = inv_root((w4[0] + w4[2]) + (w4[1] + w4[3]), (float) C, A.eps);
             const bool cached = trow == tcache;
 #pragma unroll
@@ -594,14 +598,13 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             if constexpr (ROTATED) {
-                if constexpr (ROT == H3S_ROT_SYLVESTER) sylvester<V>(v[j], lane, A.group);
-                else regular<V>(v[j], A.group);
+                if constexpr (SW) sylvester<V, true>(v[j], pos, G);
+                else regular<V>(v[j], G);
 #pragma unroll
                 for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * cgs;
             }
-            if (ok[j])
 #pragma unroll
-                for (int e = 0; e < V; ++e) m = fmaxf(m, fabsf(v[j][e]));
+            for (int e = 0; e < V; ++e) m = fmaxf(m, fabsf(v[j][e]));
         }
         m = wave_max<64>(m);
         const float sc = fmaxf(m / 127.0f, 1e-30f), r = 1.0f / sc;
@@ -611,14 +614,20 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
         int8_t* qrow = A.q + row * C;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            if (!ok[j]) continue;
             const float* o = v[j];
             const uint32_t lo = bytes4(code_of(o[0], sc, r), code_of(o[1], sc, r), code_of(o[2], sc, r), code_of(o[3], sc, r));
             const uint32_t hi = bytes4(code_of(o[4], sc, r), code_of(o[5], sc, r), code_of(o[6], sc, r), code_of(o[7], sc, r));
             st_nt(qrow + cc[j] * 8, make_uint2(lo, hi));
         }
+    };
+    uint4 xa[CPL], xb[CPL];
+    int64_t row = b0 + wave;
+    // rows left to this wavefront and to the block's first wavefront: the block steps while its first row exists
+    if (row < M) load_row(xa, row);
+    for (int64_t k = 0, first = b0; first < M; row += U, first += U, ++k) {
+        step(xa, xb, k, row);
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) x0[j] = x1[j];
+        for (int j = 0; j < CPL; ++j) xa[j] = xb[j];
     }
 }
 
@@ -649,6 +658,7 @@ template <int XDT, int CPL> int quant_wave_launch(Ctx* c, const char* fn, const 
     if (f == kQuantWTab) return quant_wave_one<XDT, CPL, RR, kQuantWTab>(c, fn, A);         \
     if (f == kQuantWTab32) return quant_wave_one<XDT, CPL, RR, kQuantWTab32>(c, fn, A);     \
     return quant_wave_one<XDT, CPL, RR, kQuantRaw>(c, fn, A);
+    if (A.rot == H3S_ROT_SYLVESTER && A.group == 128) { H3_QW(rot_with(H3S_ROT_SYLVESTER, 128)) }
     if (A.rot == H3S_ROT_SYLVESTER) { H3_QW(H3S_ROT_SYLVESTER) }
     if (A.rot == H3S_ROT_REGULAR) { H3_QW(H3S_ROT_REGULAR) }
     H3_QW(H3S_ROT_NONE)
@@ -672,6 +682,10 @@ template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, 
     }
 #define H3_QUANT_R(CC, RR)                                                                           \
     if (f == kQuantRaw) { H3_QUANT_F(CC, RR, kQuantRaw); return launched(fn); }                     \
+    if (f == kQuantSwiglu && A.rot == H3S_ROT_REGULAR && A.group == 256) {                           \
+        H3_QUANT_F(CC, rot_with(H3S_ROT_REGULAR, 256), kQuantSwiglu);                                \
+        return launched(fn);                                                                         \
+    }                                                                                                \
     if (f == kQuantSwiglu) { H3_QUANT_F(CC, RR, kQuantSwiglu); return launched(fn); }               \
     if (f == (ROW_SWIGLU | ROW_DYN)) { H3_QUANT_F(CC, RR, ROW_SWIGLU | ROW_DYN); return launched(fn); } \
     if constexpr (XDT != H3S_F32) {                                                                  \
@@ -682,13 +696,13 @@ template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, 
     }                                                                                                \
     H3_QUANT_F(CC, RR, ROW_DYN);                                                                     \
     return launched(fn);
-    // rows of 256 to 512 chunks of a 16-bit type with the exact side inputs, and enough of them (the context's
+    // rows of 2048 or 4096 features of a 16-bit type with the exact side inputs, and enough of them (the context's
     // quant_wave_min, 8192) to give every wavefront several rows: one wavefront a row (fewer rows: four wavefronts
     // share each, which shortens a short launch)
     if constexpr (XDT != H3S_F32) {
-        if ((f == kQuantNone || f == kQuantW || f == kQuantWTab || f == kQuantWTab32 || f == kQuantRaw) && p.L == 256 &&
-            p.cpl <= 2 && A.C / 8 >= 256 && A.M >= c->quant_wave_min) {
-            if (A.C / 8 == 256) return quant_wave_launch<XDT, 4>(c, fn, A, f);
+        if ((f == kQuantNone || f == kQuantW || f == kQuantWTab || f == kQuantWTab32 || f == kQuantRaw) &&
+            (A.C == 2048 || A.C == 4096) && A.M >= c->quant_wave_min) {
+            if (A.C == 2048) return quant_wave_launch<XDT, 4>(c, fn, A, f);
             return quant_wave_launch<XDT, 8>(c, fn, A, f);
         }
     }
