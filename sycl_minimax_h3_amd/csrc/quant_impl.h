@@ -431,9 +431,13 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
 template <int CPL> constexpr size_t quant_wave_side_bytes(int f) {
     return (size_t) ((f & ROW_W) ? 1 : 0) * CPL * 2048 + (size_t) ((f & ROW_TAB) ? 2 : 0) * CPL * 2048;
 }
-template <int XDT, int CPL, int ROT, int F>
+// ONE: the grid has a wavefront for every row, so each takes one row and nothing is prefetched (no registers are
+// held for a next row: 108 instead of 147 for config 4's kernel, four wavefronts a SIMD instead of three); else the
+// grid strides over the rows with the next row's x in flight.
+template <int XDT, int CPL, int ROT, int F, bool ONE>
 __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
     static_assert(XDT != H3S_F32 && !(F & (ROW_DYN | ROW_SWIGLU)), "quant_wave_kernel: 16-bit x, exact side inputs");
+    static_assert(!(ONE && (F & ROW_TAB)), "quant_wave_kernel: tables are cached by a grid-strided block");
     constexpr int V = 8;
     constexpr bool ROTATED = rot_kind(ROT) != H3S_ROT_NONE;
     constexpr bool NORM = !(F & ROW_RAW);
@@ -545,7 +549,7 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
             }
         }
         if (row >= M) return;                                // past the end: only the barriers above remain to keep
-        if (row + U < M) load_row(xn, row + U);
+        if (!ONE && row + U < M) load_row(xn, row + U);
         float v[CPL][V];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(xc[j], v[j]);
@@ -622,6 +626,13 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
     };
     uint4 xa[CPL], xb[CPL];
     int64_t row = b0 + wave;
+    if constexpr (ONE) {
+        if (row < M) {
+            load_row(xa, row);
+            step(xa, xb, 0, row);
+        }
+        return;
+    }
     // rows left to this wavefront and to the block's first wavefront: the block steps while its first row exists
     if (row < M) load_row(xa, row);
     for (int64_t k = 0, first = b0; first < M; row += U, first += U, ++k) {
@@ -640,15 +651,17 @@ constexpr int kQuantNone = 0, kQuantW = ROW_W, kQuantWTab = ROW_W | ROW_TAB, kQu
 // The launch of quant_wave_kernel: blocks of 4 wavefronts (8 with tables, so one LDS copy of the side values
 // serves more rows).
 template <int XDT, int CPL, int ROT, int F> int quant_wave_one(Ctx* c, const char* fn, const QuantArgs& A) {
-    const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F>;
+    constexpr bool ONE = !(F & ROW_TAB);
+    const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, ONE>;
     const int threads = (F & ROW_TAB) ? 512 : 256;
     const size_t lds = quant_wave_side_bytes<CPL>(F);
     // with tables, as many blocks as the device holds (each decodes its table row once); without, one row a
-    // wavefront (measured faster: 125 against 130 us for config 4; with tables 147 against 112 us for config 5a)
+    // wavefront and nothing prefetched (config 4 at 47104 rows: 106 us, against 119 us grid-strided with the next
+    // row in flight; with tables, one row a wavefront measured 147 against 112 us for config 5a)
     const int64_t rows_blocks = (A.M + threads / 64 - 1) / (threads / 64);
     const int64_t blocks = (F & ROW_TAB) ? std::min<int64_t>((int64_t) c->cus * blocks_per_cu(k, threads, lds), rows_blocks)
                                          : rows_blocks;
-    quant_wave_kernel<XDT, CPL, ROT, F><<<(unsigned) blocks, threads, lds, c->stream>>>(A);
+    quant_wave_kernel<XDT, CPL, ROT, F, ONE><<<(unsigned) blocks, threads, lds, c->stream>>>(A);
     return launched(fn);
 }
 template <int XDT, int CPL> int quant_wave_launch(Ctx* c, const char* fn, const QuantArgs& A, int f) {
