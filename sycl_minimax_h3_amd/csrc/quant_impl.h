@@ -431,11 +431,16 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
 template <int CPL> constexpr size_t quant_wave_side_bytes(int f) {
     return (size_t) ((f & ROW_W) ? 1 : 0) * CPL * 2048 + (size_t) ((f & ROW_TAB) ? 2 : 0) * CPL * 2048;
 }
-// ONE: the grid has a wavefront for every row, so each takes one row and nothing is prefetched (no registers are
-// held for a next row: 108 instead of 147 for config 4's kernel, four wavefronts a SIMD instead of three); else the
-// grid strides over the rows with the next row's x in flight.
+// wavefronts a block: 8 with tables (one LDS copy of the side values serves more rows), else 4
+constexpr int quant_wave_nw(int f) { return (f & ROW_TAB) ? 8 : 4; }
+// ONE: the grid has a wavefront for every row, so each takes one row (108 registers for config 4's kernel, four
+// wavefronts a SIMD); else the grid strides over the rows, with nothing prefetched either: four wavefronts a SIMD
+// hide the loads (the registers of a prefetched next row would leave room for three). With tables and no rotation
+// the kernel is held to four wavefronts a SIMD (120 registers, no spills).
 template <int XDT, int CPL, int ROT, int F, bool ONE>
-__global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
+__global__ __launch_bounds__(512)
+__attribute__((amdgpu_waves_per_eu((F & ROW_TAB) && rot_kind(ROT) == H3S_ROT_NONE ? 4 : 1)))
+void quant_wave_kernel(QuantArgs A) {
     static_assert(XDT != H3S_F32 && !(F & (ROW_DYN | ROW_SWIGLU)), "quant_wave_kernel: 16-bit x, exact side inputs");
     static_assert(!(ONE && (F & ROW_TAB)), "quant_wave_kernel: tables are cached by a grid-strided block");
     constexpr int V = 8;
@@ -446,7 +451,8 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
     constexpr int TDT = (F & ROW_TAB32) ? H3S_F32 : H3S_BF16;
     constexpr int WOFF = 0, SOFF = HASW ? CPL * 512 : 0, HOFF = SOFF + CPL * 512;     // float offsets in side
     extern __shared__ __align__(16) float side[];
-    const int lane = (int) (threadIdx.x & 63), NW = (int) (blockDim.x >> 6);
+    constexpr int NW = quant_wave_nw(F);
+    const int lane = (int) (threadIdx.x & 63);
     const int wave = (int) wave_uniform(threadIdx.x >> 6);
     const int64_t C = 64 * CPL * V;                         // the launch checks A.C against this
     const int64_t b0 = (int64_t) blockIdx.x * NW, U = (int64_t) gridDim.x * NW, M = A.M;
@@ -511,48 +517,44 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
 
     const int G = rot_fixed(ROT) ? rot_fixed(ROT) : A.group;
     const float cgs = SW ? A.cg * syl_sign<V>(pos, G) : A.cg;
+    // a row's x: a base the whole wavefront shares (the row is the wavefront's) and a 32-bit unsigned byte offset
+    // a lane, so the loads and stores take the scalar-base form and hold no 64-bit address registers (the row
+    // passes through readfirstlane, which keeps the compiler from turning each chunk's address into an induction
+    // variable of its own across the grid-stride loop)
     auto load_row = [&](uint4 (&xr)[CPL], int64_t row) {
-        const uint4* xp = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * 2);
+        const char* xp = reinterpret_cast<const char*>(A.x) + wave_uniform(row) * C * 2;
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) xr[j] = xp[cc[j]];
+        for (int j = 0; j < CPL; ++j) xr[j] = *reinterpret_cast<const uint4*>(xp + (uint32_t) (cc[j] * 16));
     };
-    // The table row indices of this wavefront's rows and of the block's first row at each step, 64 steps at a time,
-    // one a lane (taken out with readlane): rows[] is read once per 64 steps, and waited for there, not once per row
-    // with a wait that would drain the next row's x.
+    // The table rows of each step's group of NW rows (rows g + [0, NW), g = b0 + k U, one a wavefront), 64 steps
+    // at a time, one step a lane, taken out with readlane: the group's first row's (gix), this wavefront's (tix),
+    // and a bit of uni set when the whole group shares one table row. rows[] is read once per 64 steps.
     int tix = 0, gix = 0;
+    uint64_t uni = ~0ull;
     int64_t kbase = -64;
-    auto table_rows = [&](int64_t k, int64_t& own, int64_t& first) {
+    auto group_rows = [&](int64_t k) {
         if (k - kbase >= 64) {
             kbase = k;
-            const int64_t rf = b0 + U * (k + lane), ro = rf + wave;
-            tix = ro < M ? A.rows[ro] : 0;
-            gix = rf < M ? A.rows[rf] : 0;
-            wait_vm<0>();
-        }
-        own = __builtin_amdgcn_readlane(tix, (int) (k - kbase));
-        first = __builtin_amdgcn_readlane(gix, (int) (k - kbase));
-    };
-    // One row: x of this row in xc, the next row's x loaded into xn. (Alternating two buffers instead of the copy
-    // at the end of each row needs two copies of this code and more registers than the copy costs.)
-    auto step = [&](uint4 (&xc)[CPL], uint4 (&xn)[CPL], int64_t k, int64_t row) {
-        int64_t trow = 0;
-        if constexpr (TAB) {
-            if (A.rows) {
-                int64_t tfirst;
-                table_rows(k, trow, tfirst);
-                if (tfirst != tcache) {                      // the same on every wavefront of the block
-                    lds_barrier();                           // every wavefront is done with the cached row
-                    fill(tfirst, false);
-                    lds_barrier();
-                    tcache = tfirst;
-                }
+            const int64_t g = b0 + U * (k + lane);
+            gix = g < M ? A.rows[g] : 0;
+            tix = gix;
+            bool same = true;
+#pragma unroll
+            for (int r = 1; r < NW; ++r) {
+                const int t = g + r < M ? A.rows[g + r] : gix;
+                same = same && t == gix;
+                if (r == wave) tix = t;
             }
+            uni = __builtin_amdgcn_ballot_w64(same);
         }
-        if (row >= M) return;                                // past the end: only the barriers above remain to keep
-        if (!ONE && row + U < M) load_row(xn, row + U);
+    };
+    // One row, with the table row cached in LDS.
+    auto process = [&](int64_t row) {
+        uint4 x[CPL];
+        load_row(x, row);
         float v[CPL][V];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(xc[j], v[j]);
+        for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(x[j], v[j]);
 
         // ---- rms_norm_mod into bfloat16 (the reference's scratch h) ----
         if constexpr (NORM) {
@@ -565,7 +567,6 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) w4[g] = wave_sum<64, SW>(ss[g]);
             const float inv = inv_root((w4[0] + w4[2]) + (w4[1] + w4[3]), (float) C, A.eps);
-            const bool cached = trow == tcache;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 if constexpr (HASW) {
@@ -579,12 +580,8 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
                 }
                 if constexpr (TAB) {
                     float s1[V], sh[V];
-                    if (cached) {
-                        get8(SOFF, j, s1);
-                        get8(HOFF, j, sh);
-                    } else {
-                        table8(trow, j, s1, sh);
-                    }
+                    get8(SOFF, j, s1);
+                    get8(HOFF, j, sh);
 #pragma unroll
                     for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * s1[e] + sh[e];
                 }
@@ -594,6 +591,8 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
                     v[j][e] = bf16_lo(p);
                     v[j][e + 1] = bf16_hi(p);
                 }
+                // with tables, one chunk's LDS reads at a time: the registers stay within four wavefronts a SIMD
+                if constexpr (TAB) __builtin_amdgcn_sched_barrier(0);
             }
         }
 
@@ -615,30 +614,56 @@ __global__ __launch_bounds__(512) void quant_wave_kernel(QuantArgs A) {
         if (lane == 0) A.s[row] = sc;
 
         // ---- the codes, 8 bytes a chunk ----
-        int8_t* qrow = A.q + row * C;
+        int8_t* qrow = A.q + wave_uniform(row) * C;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const float* o = v[j];
             const uint32_t lo = bytes4(code_of(o[0], sc, r), code_of(o[1], sc, r), code_of(o[2], sc, r), code_of(o[3], sc, r));
             const uint32_t hi = bytes4(code_of(o[4], sc, r), code_of(o[5], sc, r), code_of(o[6], sc, r), code_of(o[7], sc, r));
-            st_nt(qrow + cc[j] * 8, make_uint2(lo, hi));
+            st_nt(qrow + (uint32_t) (cc[j] * 8), make_uint2(lo, hi));
         }
     };
-    uint4 xa[CPL], xb[CPL];
     int64_t row = b0 + wave;
     if constexpr (ONE) {
-        if (row < M) {
-            load_row(xa, row);
-            step(xa, xb, 0, row);
-        }
+        if (row < M) process(row);
         return;
     }
-    // rows left to this wavefront and to the block's first wavefront: the block steps while its first row exists
-    if (row < M) load_row(xa, row);
-    for (int64_t k = 0, first = b0; first < M; row += U, first += U, ++k) {
-        step(xa, xb, k, row);
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) xa[j] = xb[j];
+    for (int64_t k = 0, g = b0; g < M; row += U, g += U, ++k) {
+        if constexpr (TAB) {
+            int64_t first = 0, own = 0;
+            bool same = true;
+            if (A.rows) {
+                group_rows(k);
+                const int i = (int) (k - kbase);
+                first = __builtin_amdgcn_readlane(gix, i);
+                own = __builtin_amdgcn_readlane(tix, i);
+                same = (uni >> i) & 1;
+            }
+            // One round for each distinct table row of the group, in the order of the group's rows: the block
+            // refills its cached table row between barriers when it changes, and the wavefronts whose rows use it
+            // run them. A group that shares one table row (every group but those a segment boundary cuts) is one
+            // round; the others read their table rows again, as scalar loads. Every wavefront of the block takes
+            // the same rounds and barriers.
+            for (int r = 0; r < NW; ++r) {
+                int64_t t = first;
+                if (r > 0) {
+                    if (same || g + r >= M) break;
+                    t = A.rows[g + r];
+                    bool seen = false;
+                    for (int q = 0; q < r; ++q) seen = seen || A.rows[g + q] == t;
+                    if (seen) continue;
+                }
+                if (t != tcache) {
+                    lds_barrier();                           // every wavefront is done with the cached row
+                    fill(t, false);
+                    lds_barrier();
+                    tcache = t;
+                }
+                if (row < M && own == t) process(row);
+            }
+        } else {
+            if (row < M) process(row);
+        }
     }
 }
 
@@ -653,7 +678,7 @@ constexpr int kQuantNone = 0, kQuantW = ROW_W, kQuantWTab = ROW_W | ROW_TAB, kQu
 template <int XDT, int CPL, int ROT, int F> int quant_wave_one(Ctx* c, const char* fn, const QuantArgs& A) {
     constexpr bool ONE = !(F & ROW_TAB);
     const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, ONE>;
-    const int threads = (F & ROW_TAB) ? 512 : 256;
+    const int threads = 64 * quant_wave_nw(F);
     const size_t lds = quant_wave_side_bytes<CPL>(F);
     // with tables, as many blocks as the device holds (each decodes its table row once); without, one row a
     // wavefront and nothing prefetched (config 4 at 47104 rows: 106 us, against 119 us grid-strided with the next
