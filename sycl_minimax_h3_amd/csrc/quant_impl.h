@@ -223,8 +223,8 @@ struct QuantArgs {
 //
 // A unit (one block for rows of 256 or 512 lanes, one wavefront for 64-lane rows) quantizes the rows
 // [unit * rpu, (unit + 1) * rpu). A lane works on the same chunks of every row, so the weight and the table row are
-// decoded into registers once (the table row again only when rows[] changes), and the next row's x is in flight
-// while this one is computed.
+// decoded into registers once (the table row again only when rows[] changes), and with tables the next row's x is
+// in flight while this one is computed.
 template <int XDT, int CPL, int ROT, int F>
 __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int64_t rpu) {
     constexpr bool ROTATED = rot_kind(ROT) != H3S_ROT_NONE;
@@ -233,6 +233,10 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
     constexpr bool TW = DYN || (F & ROW_TAB32);
     constexpr bool SWI = F & ROW_SWIGLU;
     constexpr bool NORM = !(F & (ROW_RAW | ROW_SWIGLU));
+    // a launch without tables gives each unit one row (persistent_launch keeps units only for table rows), so only
+    // a kernel with tables holds registers for the next row's x: the others run at more wavefronts a SIMD (86
+    // registers instead of 113 for the swiglu quantizer of 8192 features)
+    constexpr bool PF = (F & (ROW_TAB | ROW_DYN)) != 0;
     __shared__ float red[2][8];
     const bool has_w = DYN ? A.w != nullptr : (F & ROW_W) != 0;
     const bool has_tab = DYN ? A.scale != nullptr : (F & ROW_TAB) != 0;
@@ -317,7 +321,7 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
         // the next row's x and table row index, in flight during this row
         uint4 x1[CPL], u1[CPL];
         int64_t t1 = 0;
-        if (row + 1 < r1) {
+        if (PF && row + 1 < r1) {
             load_row(x1, u1, row + 1);
             if (has_tab && A.rows) t1 = A.rows[row + 1];
         }
@@ -401,10 +405,14 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
                 st_nt(qrow + cc[j] * 4, b0);
             }
         }
+        if constexpr (PF) {
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            x0[j] = x1[j];
-            if constexpr (SWI) u0[j] = u1[j];
+            for (int j = 0; j < CPL; ++j) {
+                x0[j] = x1[j];
+                if constexpr (SWI) u0[j] = u1[j];
+            }
+        } else if (row + 1 < r1) {
+            load_row(x0, u0, row + 1);
         }
         t0 = t1;
     }
