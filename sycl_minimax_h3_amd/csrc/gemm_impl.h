@@ -7,16 +7,18 @@
 //   then + bias[n], then the activation, rounded once to out's type.
 //
 // Block: 256 threads (four wavefronts, 2 x 2), a 256 x 256 tile of out; each wavefront 128 x 128 as 4 x 4
-// v_mfma_i32_32x32x32_i8 accumulators (256 registers, one wavefront per SIMD). K advances 64 bytes a step
-// through a ring of four LDS stages (32 KiB each: the A and W slices of the step), filled by direct global->LDS
-// loads (global_load_lds_dwordx4) up to four steps ahead, so no registers hold operands in flight. Each step publishes the
-// next stage (one barrier), reads that stage's fragments into registers, and runs its own products beside those
-// reads; the buffer whose fragments are already in registers is refilled right after the barrier.
+// v_mfma_i32_32x32x32_i8 accumulators (256 registers, one wavefront per SIMD). K advances 128 bytes a step (four
+// 32-deep slices) through two LDS stages (64 KiB each: the A and W rows of the step), filled by direct
+// global->LDS loads (global_load_lds_dwordx4), so no registers hold operands in flight; each load instruction reads
+// 8 rows x 128 bytes, whole lines (a 64-byte step, half lines per instruction and the other halves a step later,
+// measured 4 % slower with four stages). Each step runs its four slices' products with the next slice's fragment
+// reads between them, waits for the next stage and publishes it (one barrier), refills the stage it just finished,
+// and reads the next stage's first slice beside its last products.
 //
-// LDS layout of an operand slice: 256 rows x 4 16-byte chunks; chunk c of row r at unit 4 r + (c ^ ((r / 4) % 4)).
+// LDS layout of an operand slice: 256 rows x 8 16-byte chunks; chunk c of row r at unit 8 r + (c ^ ((r / 2) % 8)).
 // A fragment read (32 consecutive rows, one chunk each) then touches 16 distinct 4-bank groups in each 16-lane
-// half. The direct loads write 64 consecutive units per instruction, so each lane fetches the (row, chunk) that its
-// unit holds: four lanes cover one row's 64 bytes.
+// quarter. The direct loads write 64 consecutive units per instruction, so each lane fetches the (row, chunk) that
+// its unit holds: eight lanes cover one row's 128 bytes.
 //
 // Tile order: the 8 XCDs take blocks round robin; blocks are renumbered so that each XCD works on a contiguous
 // run of tiles, grouped 8 tiles high so that the resident blocks of an XCD share A and W panels in its L2.
@@ -30,8 +32,8 @@
 
 namespace h3 {
 
-constexpr int kGemmBM = 256, kGemmBN = 256, kGemmBK = 64, kGemmStages = 4;
-constexpr int kGemmStageBytes = (kGemmBM + kGemmBN) * kGemmBK;   // 32 KiB
+constexpr int kGemmBM = 256, kGemmBN = 256, kGemmBK = 128, kGemmStages = 2;
+constexpr int kGemmStageBytes = (kGemmBM + kGemmBN) * kGemmBK;   // 64 KiB
 constexpr int kGemmLds = kGemmStages * kGemmStageBytes;          // 128 KiB
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -50,7 +52,7 @@ struct GemmArgs {
     int tm, tn;               // tiles along M and N
 };
 
-__device__ __forceinline__ int gemm_unit(int r, int c) { return (r << 2) | (c ^ ((r >> 2) & 3)); }
+__device__ __forceinline__ int gemm_unit(int r, int c) { return (r << 3) | (c ^ ((r >> 1) & 7)); }
 
 // the tile of block b: XCD-contiguous renumbering, then 8-high groups of tiles
 __device__ __forceinline__ void gemm_tile(int b, int tm, int tn, int* im, int* in) {
@@ -83,28 +85,33 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
     // (lane % 4) ^ ((r / 4) % 4) = (lane % 4) ^ ((lane / 16) % 4): a uniform block base plus a 32-bit lane offset
     const int8_t* baseA = P.A + m0 * K;
     const int8_t* baseW = P.W + n0 * K;
-    uint32_t offA_g[4], offW_g[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int r = 16 * (4 * wave + q) + (lane >> 2), c = (lane & 3) ^ ((lane >> 4) & 3);
-        const int64_t ra = m0 + r < P.M ? r : P.M - 1 - m0, rw = n0 + r < P.N ? r : P.N - 1 - n0;
-        offA_g[q] = (uint32_t) (ra * K + 16 * c);
-        offW_g[q] = (uint32_t) (rw * K + 16 * c);
-    }
+    // K steps of 128 bytes, the last one 64 when K is an odd multiple of 64 (its two slices only)
+    const int nk = (int) ((K + kGemmBK - 1) / kGemmBK);
+    const bool half_last = K % kGemmBK != 0;
+    // Instruction q of wavefront w fills units 64 (8 w + q) .. + 63: rows 8 (8 w + q) + lane / 8 (clamped into the
+    // matrix), each lane the chunk its unit holds, so one instruction reads 8 whole 128-byte segments. A half step's
+    // lanes of chunks 4-7 read chunks 0-3 again (inside the row; the slices that would read them are not run).
     auto issue = [&](int kt) {
         int8_t* st = lds + (kt % kGemmStages) * kGemmStageBytes;
         const int64_t k0 = (int64_t) kt * kGemmBK;
         const int8_t* a = baseA + k0;
         const int8_t* w = baseW + k0;
+        const int cmask = half_last && kt == nk - 1 ? 3 : 7;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) (a + offA_g[q]),
-                                             (__attribute__((address_space(3))) void*) (st + (4 * wave + q) * 1024), 16, 0, 0);
+        for (int q = 0; q < 8; ++q) {
+            const int r = 8 * (8 * wave + q) + (lane >> 3), c = ((lane & 7) ^ ((r >> 1) & 7)) & cmask;
+            const int64_t ra = m0 + r < P.M ? r : P.M - 1 - m0;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) (a + (uint32_t) (ra * K + 16 * c)),
+                                             (__attribute__((address_space(3))) void*) (st + (8 * wave + q) * 1024), 16, 0, 0);
+        }
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) (w + offW_g[q]),
-                                             (__attribute__((address_space(3))) void*) (st + kGemmBM * kGemmBK + (4 * wave + q) * 1024),
+        for (int q = 0; q < 8; ++q) {
+            const int r = 8 * (8 * wave + q) + (lane >> 3), c = ((lane & 7) ^ ((r >> 1) & 7)) & cmask;
+            const int64_t rw = n0 + r < P.N ? r : P.N - 1 - n0;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) (w + (uint32_t) (rw * K + 16 * c)),
+                                             (__attribute__((address_space(3))) void*) (st + kGemmBM * kGemmBK + (8 * wave + q) * 1024),
                                              16, 0, 0);
+        }
     };
 
     v16i acc[4][4];
@@ -113,25 +120,23 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = (v16i) 0;
 
-    // fragment offsets (bytes in a stage): row l % 32 of each 32-row tile, chunk 2 kk + l / 32
-    int offA[2][4], offW[2][4];
+    // fragment bases (bytes in a stage) of slice kk: row l % 32 of the wavefront's first 32-row tile, chunk
+    // 2 kk + l / 32; tile i is 4096 i further (32 rows of 128 bytes, the swizzle the same for every tile)
+    int offA[4], offW[4];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = 2 * kk + (lane >> 5);
-            offA[kk][i] = gemm_unit(wm * 128 + i * 32 + (lane & 31), c) * 16;
-            offW[kk][i] = kGemmBM * kGemmBK + gemm_unit(wn * 128 + i * 32 + (lane & 31), c) * 16;
-        }
+    for (int kk = 0; kk < 4; ++kk) {
+        const int c = 2 * kk + (lane >> 5);
+        offA[kk] = gemm_unit(wm * 128 + (lane & 31), c) * 16;
+        offW[kk] = kGemmBM * kGemmBK + gemm_unit(wn * 128 + (lane & 31), c) * 16;
+    }
 
-    const int nk = (int) (K / kGemmBK);
     // the fragments of one 32-deep slice kk of stage kt (four A and four W)
     auto read_half = [&](int kt, int kk, v4i (&a)[4], v4i (&b)[4]) {
         const int8_t* st = lds + (kt % kGemmStages) * kGemmStageBytes;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            a[i] = *reinterpret_cast<const v4i*>(st + offA[kk][i]);
-            b[i] = *reinterpret_cast<const v4i*>(st + offW[kk][i]);
+            a[i] = *reinterpret_cast<const v4i*>(st + offA[kk] + 4096 * i);
+            b[i] = *reinterpret_cast<const v4i*>(st + offW[kk] + 4096 * i);
         }
     };
     // W's fragment as the first operand: acc[i][j] holds rows (columns of out) from W tile j and columns (rows of
@@ -140,37 +145,32 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
         const int i = p / 4, j = p % 4;
         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[j], a[i], acc[i][j], 0, 0, 0);
     };
-    // stage kt has landed once at most the stages issued after it (8 loads each) are outstanding
-    auto wait_stage = [&](int kt, int issued) {
-        const int after = issued - 1 - kt;
-        if (after >= 3) wait_vm<24>();
-        else if (after == 2) wait_vm<16>();
-        else if (after == 1) wait_vm<8>();
-        else wait_vm<0>();
-    };
     int issued = 0;
     for (; issued < kGemmStages && issued < nk; ++issued) issue(issued);
-    v4i xa[4], xb[4], ya[4], yb[4];   // slice 0 and slice 1 fragments
-    wait_stage(0, issued);
+    v4i xa[4], xb[4], ya[4], yb[4];
+    if (issued > 1) wait_vm<16>(); else wait_vm<0>();
     block_barrier();
     read_half(0, 0, xa, xb);
-    // Step kt: the 16 products of slice 0 with slice 1's fragment reads between them; then four products of slice 1,
-    // this wavefront's fragment reads done (lgkmcnt), stage kt + 1 landed (vmcnt) and the barrier - after which no
-    // wavefront reads stage kt's buffer, so it is refilled with stage kt + 4 - and the last 12 products of slice 1
-    // with the reads of stage kt + 1's slice 0 between them.
-    for (int kt = 0; kt < nk - 1; ++kt) {
-        read_half(kt, 1, ya, yb);
+    auto body16 = [&](const v4i (&a)[4], const v4i (&b)[4]) {
 #pragma unroll
-        for (int p = 0; p < 16; ++p) mfma(xa, xb, p);
+        for (int p = 0; p < 16; ++p) mfma(a, b, p);
 #pragma unroll
         for (int g = 0; g < 8; ++g) {
-            __builtin_amdgcn_sched_group_barrier(0x0008, 2, 0);   // two products
-            __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // one fragment read
+            __builtin_amdgcn_sched_group_barrier(0x0008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);
         }
+    };
+    for (int kt = 0; kt < nk - 1; ++kt) {
+        read_half(kt, 1, ya, yb);
+        body16(xa, xb);
+        read_half(kt, 2, xa, xb);
+        body16(ya, yb);
+        read_half(kt, 3, ya, yb);
+        body16(xa, xb);
 #pragma unroll
         for (int p = 0; p < 4; ++p) mfma(ya, yb, p);
         __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-        wait_stage(kt + 1, issued);
+        wait_vm<0>();                         // stage kt + 1 landed (the only one in flight)
         block_barrier();
         if (issued < nk) issue(issued++);
         read_half(kt + 1, 0, xa, xb);
@@ -183,10 +183,15 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
         }
         __builtin_amdgcn_sched_group_barrier(0x0008, 8, 0);
     }
-    // the last step: its slice 1 read, no stage after it
+    // the last step: no stage after it; a half step has slices 0 and 1 only
     read_half(nk - 1, 1, ya, yb);
-#pragma unroll
-    for (int p = 0; p < 16; ++p) mfma(xa, xb, p);
+    body16(xa, xb);
+    if (!half_last) {
+        read_half(nk - 1, 2, xa, xb);
+        body16(ya, yb);
+        read_half(nk - 1, 3, ya, yb);
+        body16(xa, xb);
+    }
 #pragma unroll
     for (int p = 0; p < 16; ++p) mfma(ya, yb, p);
     wait_vm<0>();

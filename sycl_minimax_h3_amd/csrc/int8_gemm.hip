@@ -26,7 +26,7 @@ int launch_gemm(Ctx* c, const char* fn, const int8_t* q, const float* s, int64_t
 
 static int gemm_checks(const char* fn, int64_t K, int64_t N, int64_t n_wscale, int out_dt, const void* q, const void* w,
                        const void* out) {
-    if (K % kGemmBK != 0) return fail(std::string(fn) + ": K must be a multiple of 64");
+    if (K % 64 != 0) return fail(std::string(fn) + ": K must be a multiple of 64");
     if (K >= (int64_t) 1 << 24) return fail(std::string(fn) + ": K must be below 2^24");
     if (n_wscale != 1 && n_wscale != N) return fail(std::string(fn) + ": 1 or N weight scales");
     if (!dt_ok(out_dt)) return fail(std::string(fn) + ": unknown element type");

@@ -352,7 +352,7 @@ def test_norm_mod_act_gate_float32_and_affine(dev):
 
 
 # ---- h3s_int8_linear and h3s_int8_gemm_dequant (kernels/h3sycl.cpp:404-652) ----
-@pytest.mark.parametrize("M,K,N", [(1, 64, 5), (300, 256, 300), (257, 4096, 129), (64, 1024, 512)])
+@pytest.mark.parametrize("M,K,N", [(1, 64, 5), (300, 256, 300), (257, 4096, 129), (64, 1024, 512), (33, 320, 70)])
 @pytest.mark.parametrize("group", [0, 4, 16, 64, 256])
 @pytest.mark.parametrize("per_n,bias,out_dt", [(False, False, o.BF16), (True, True, o.BF16), (True, False, o.F32)])
 @pytest.mark.parametrize("layout", ["four", "wave"])
@@ -374,8 +374,9 @@ def test_int8_linear(request, layout, M, K, N, group, per_n, bias, out_dt):
 
 
 @pytest.mark.parametrize("act", [o.ACT_NONE, o.ACT_SILU])
-def test_int8_gemm_dequant(dev, act):
-    M, K, N = 515, 4096, 770
+@pytest.mark.parametrize("K", [4096, 320, 192])   # whole 128-byte K steps, and a last step of 64
+def test_int8_gemm_dequant(dev, act, K):
+    M, N = 515, 770
     rng = np.random.default_rng(40)
     q = rng.integers(-128, 128, M * K, dtype=np.int8)
     s = rng.uniform(0.001, 0.05, M).astype(np.float32)
