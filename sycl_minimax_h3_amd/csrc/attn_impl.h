@@ -93,11 +93,14 @@ __global__ __launch_bounds__(256) void attn_kmean_kernel(const void* __restrict_
             const uint32_t at = (uint32_t) (uintptr_t) (ring + (ch % kKmeanStages) * kKmeanChunk) + lane * ESZ;
             const int rows = S - ch * ROWS < ROWS ? (int) (S - ch * ROWS) : ROWS;
             // rows read in asm, 16 at a time and 16 rows ahead of the additions, with a wait tied to the values (the
-            // compiler would otherwise wait for every direct load in flight before a read of the ring)
+            // compiler would otherwise wait for every direct load in flight before a read of the ring). A bfloat16
+            // value is read into the high half of a register whose low half stays 0: the register is then the
+            // float32 value, and each row costs one read and one addition.
             auto read16 = [&](uint32_t (&v)[16], uint32_t a) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    if constexpr (ESZ == 2) asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v[i]) : "v"(a), "i"(i * RB) : "memory");
+                    if constexpr (DT == H3S_BF16) asm volatile("ds_read_u16_d16_hi %0, %1 offset:%2" : "+v"(v[i]) : "v"(a), "i"(i * RB) : "memory");
+                    else if constexpr (ESZ == 2) asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v[i]) : "v"(a), "i"(i * RB) : "memory");
                     else asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v[i]) : "v"(a), "i"(i * RB) : "memory");
                 }
             };
@@ -110,14 +113,15 @@ __global__ __launch_bounds__(256) void attn_kmean_kernel(const void* __restrict_
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     float x;
-                    if constexpr (DT == H3S_F32) x = __uint_as_float(v[i]);
-                    else if constexpr (DT == H3S_BF16) x = bf16_lo(v[i]);
+                    if constexpr (DT == H3S_F32 || DT == H3S_BF16) x = __uint_as_float(v[i]);
                     else x = f16_lo(v[i]);
                     sum = sum + x;
                 }
             };
             const int full = rows / 16 * 16;
             uint32_t va[16], vb[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) va[i] = vb[i] = 0u;        // the low halves the bfloat16 reads keep
             if (full > 0) {
                 read16(va, at);
                 wait16(va);
