@@ -12,8 +12,9 @@
 // global->LDS loads (global_load_lds_dwordx4), so no registers hold operands in flight; each load instruction reads
 // 8 rows x 128 bytes, whole lines (a 64-byte step, half lines per instruction and the other halves a step later,
 // measured 4 % slower with four stages). Each step runs its four slices' products with the next slice's fragment
-// reads between them, waits for the next stage and publishes it (one barrier), refills the stage it just finished,
-// and reads the next stage's first slice beside its last products.
+// reads between them, waits for the next stage and publishes it (one barrier), then refills the stage it just
+// finished and reads the next stage's first slice, both spread between its last products (the refill loads
+// issued in one burst left the matrix pipe idle at one wavefront per SIMD: 4 % slower).
 //
 // LDS layout of an operand slice: 256 rows x 8 16-byte chunks; chunk c of row r at unit 8 r + (c ^ ((r / 2) % 8)).
 // A fragment read (32 consecutive rows, one chunk each) then touches 16 distinct 4-bank groups in each 16-lane
@@ -160,7 +161,10 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
             __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);
         }
     };
-    for (int kt = 0; kt < nk - 1; ++kt) {
+    // a step with the refill of stage kt + 2 (all but the last two steps) or without it, so that the loads sit in
+    // the same scheduling region as the products they are interleaved with
+    auto step = [&](int kt, auto refill_tag) {
+        constexpr bool REFILL = decltype(refill_tag)::value;
         read_half(kt, 1, ya, yb);
         body16(xa, xb);
         read_half(kt, 2, xa, xb);
@@ -172,17 +176,30 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
         __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
         wait_vm<0>();                         // stage kt + 1 landed (the only one in flight)
         block_barrier();
-        if (issued < nk) issue(issued++);
+        if constexpr (REFILL) issue(kt + 2);
         read_half(kt + 1, 0, xa, xb);
 #pragma unroll
         for (int p = 4; p < 16; ++p) mfma(ya, yb, p);
+        if constexpr (REFILL) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x0100, 2, 0);
+            for (int g = 0; g < 8; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);   // one product
+                __builtin_amdgcn_sched_group_barrier(0x0020, 2, 0);   // two direct loads
+                __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // one fragment read
+            }
+            __builtin_amdgcn_sched_group_barrier(0x0008, 4, 0);
+        } else {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x0100, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x0008, 8, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x0008, 8, 0);
-    }
+    };
+    int kt = 0;
+    for (; kt < nk - 2; ++kt) step(kt, std::true_type{});
+    for (; kt < nk - 1; ++kt) step(kt, std::false_type{});
     // the last step: no stage after it; a half step has slices 0 and 1 only
     read_half(nk - 1, 1, ya, yb);
     body16(xa, xb);
