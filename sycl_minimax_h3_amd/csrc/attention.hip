@@ -7,36 +7,6 @@
 
 namespace h3 {
 
-// The stream for work forked off the context's stream: the context's second stream, made on first use, after it
-// waits for everything queued on the context's stream so far; the context's stream itself when the second stream or
-// its events cannot be made (the same order, serialized).
-static hipStream_t side_stream(Ctx* c) {
-    if (!c->side_stream) {
-        hipStream_t s = nullptr;
-        hipEvent_t f = nullptr, j = nullptr;
-        if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess ||
-            hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
-            hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
-            if (s) (void) hipStreamDestroy(s);
-            if (f) (void) hipEventDestroy(f);
-            (void) hipGetLastError();
-            return c->stream;
-        }
-        c->side_stream = s; c->side_fork = f; c->side_join = j;
-    }
-    if (hipEventRecord(c->side_fork, c->stream) != hipSuccess || hipStreamWaitEvent(c->side_stream, c->side_fork, 0) != hipSuccess) {
-        (void) hipGetLastError();
-        return c->stream;
-    }
-    return c->side_stream;
-}
-// the context's stream waits for the work queued on side
-static void side_join(Ctx* c, hipStream_t side) {
-    if (side == c->stream) return;
-    if (hipEventRecord(c->side_join, side) != hipSuccess || hipStreamWaitEvent(c->stream, c->side_join, 0) != hipSuccess)
-        (void) hipStreamSynchronize(side);   // the order still holds, at the cost of a host wait
-}
-
 // q of Hq heads (row stride qs) and k, v of Hkv heads (row stride kvs) prepared into aq [Hq, Sp, D], ak [Hkv, Sp, D]
 // (int8 codes with their scales for SAGE, else half) and av [Hkv, D, Sp] (half)
 template <int DT>
@@ -47,12 +17,11 @@ static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S,
     // 16-byte rows: every tensor aligned and the strides whole numbers of 16-byte vectors
     const bool vec = aligned16(q) && aligned16(k) && aligned16(v) && (qs_stride * elem_size(DT)) % 16 == 0 &&
                      (kv_stride * elem_size(DT)) % 16 == 0;
-    auto qk = [&](const void* src, int64_t stride, unsigned blocks, const float* mean, int8_t* dst, float* sc,
-                  hipStream_t st) {
-#define H3_QK(SG, DD) attn_qk_prep_vec_kernel<DT, SG, DD><<<blocks, 256, 0, st>>>(src, S, Sp, stride, mean, dst, sc)
+    auto qk = [&](const void* src, int64_t stride, unsigned blocks, const float* mean, int8_t* dst, float* sc) {
+#define H3_QK(SG, DD) attn_qk_prep_vec_kernel<DT, SG, DD><<<blocks, 256, 0, c->stream>>>(src, S, Sp, stride, mean, dst, sc)
         if (!vec) {
-            if (sage) attn_qk_prep_kernel<DT, true><<<blocks, 256, 0, st>>>(src, S, Sp, D, stride, mean, dst, sc);
-            else attn_qk_prep_kernel<DT, false><<<blocks, 256, 0, st>>>(src, S, Sp, D, stride, mean, dst, sc);
+            if (sage) attn_qk_prep_kernel<DT, true><<<blocks, 256, 0, c->stream>>>(src, S, Sp, D, stride, mean, dst, sc);
+            else attn_qk_prep_kernel<DT, false><<<blocks, 256, 0, c->stream>>>(src, S, Sp, D, stride, mean, dst, sc);
         } else if (sage) {
             if (D == 128) H3_QK(true, 128);
             else H3_QK(true, 64);
@@ -62,26 +31,19 @@ static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S,
         }
 #undef H3_QK
     };
-    hipStream_t side = c->stream;
     if (sage) {
-        // k's mean is a serial sum per feature (one block per 32 features: half the device stays idle for it), so
-        // it and k's preparation, which needs it, run on a second stream beside q's and v's preparation. The fork
-        // event orders them after everything queued before this call (the previous call's reads of the scratch
-        // they write); the join event orders the main kernel after them.
-        side = side_stream(c);
         const int64_t hd = Hkv * D;
-        if (vec) attn_kmean_kernel<DT><<<(unsigned) (hd / kKmeanFeat), 256, 0, side>>>(k, S, kv_stride, km);
-        else attn_kmean_rows_kernel<DT><<<(unsigned) ((hd + 255) / 256), 256, 0, side>>>(k, S, hd, kv_stride, km);
-        qk(k, kv_stride, kvblocks, km, ak, ks, side);
-        qk(q, qs_stride, qblocks, nullptr, aq, qs, c->stream);
+        if (vec) attn_kmean_kernel<DT><<<(unsigned) (hd / kKmeanFeat), 256, 0, c->stream>>>(k, S, kv_stride, km);
+        else attn_kmean_rows_kernel<DT><<<(unsigned) ((hd + 255) / 256), 256, 0, c->stream>>>(k, S, hd, kv_stride, km);
+        qk(q, qs_stride, qblocks, nullptr, aq, qs);
+        qk(k, kv_stride, kvblocks, km, ak, ks);
     } else {
-        qk(q, qs_stride, qblocks, nullptr, aq, nullptr, c->stream);
-        qk(k, kv_stride, kvblocks, nullptr, ak, nullptr, c->stream);
+        qk(q, qs_stride, qblocks, nullptr, aq, nullptr);
+        qk(k, kv_stride, kvblocks, nullptr, ak, nullptr);
     }
     if (!vec) attn_v_prep_kernel<DT><<<kvblocks, 256, 0, c->stream>>>(v, S, Sp, D, kv_stride, av);
     else if (D == 128) attn_v_prep_vec_kernel<DT, 128><<<kvblocks, 256, 0, c->stream>>>(v, S, Sp, kv_stride, av);
     else attn_v_prep_vec_kernel<DT, 64><<<kvblocks, 256, 0, c->stream>>>(v, S, Sp, kv_stride, av);
-    side_join(c, side);
 }
 
 // one sequence: S query rows of Hq heads (row stride qs_stride) over S key/value rows of Hkv heads (kv_stride);

@@ -27,10 +27,6 @@ struct Ctx {
     hipStream_t stream = nullptr;          // kernels run here, in call order
     bool own_stream = false;
     hipStream_t copy_stream = nullptr;     // h3s_upload, made on first use
-    // h3s_attention's second stream (k's mean and k's preparation beside q's and v's) and its fork / join events,
-    // made on first use; default priority
-    hipStream_t side_stream = nullptr;
-    hipEvent_t side_fork = nullptr, side_join = nullptr;
     std::mutex copy_mu;
     std::string name;
     int cus = 256;                         // compute units of the device (persistent grids are sized by them)

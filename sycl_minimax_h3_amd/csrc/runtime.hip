@@ -261,9 +261,6 @@ H3S_EXPORT void h3s_destroy(void* ctx) {
     (void) hipSetDevice(c->device);
     (void) hipStreamSynchronize(c->stream);
     if (c->copy_stream) { (void) hipStreamSynchronize(c->copy_stream); (void) hipStreamDestroy(c->copy_stream); }
-    if (c->side_stream) { (void) hipStreamSynchronize(c->side_stream); (void) hipStreamDestroy(c->side_stream); }
-    if (c->side_fork) (void) hipEventDestroy(c->side_fork);
-    if (c->side_join) (void) hipEventDestroy(c->side_join);
     if (c->xq) (void) hipFree(c->xq);
     if (c->rs) (void) hipFree(c->rs);
     for (void* p : {(void*) c->aq, (void*) c->ak, (void*) c->av, (void*) c->af, (void*) c->lin})
