@@ -44,7 +44,7 @@ def bytes_cfg():
         "cfg5a_rmsnorm_mod_quant_47104": M4 * C * 2 + M4 * C + M4 * 4,
         "cfg5b_int8_gemm_silu_47104x16384": M4 * C + 16384 * C + M4 * 4 + 16384 * 4 + M4 * 16384 * 2,
         "mlp_swiglu_quant_g256_47104x8192": M4 * 16384 * 2 + M4 * 8192 + M4 * 4,
-        # the other token count of the north star's pair (16.8k and 47k tokens x 4096) for configs 2-5a
+        # the other token count of the measured pair (16.8k and 47k tokens x 4096) for configs 2-5a
         "cfg2_ln_mod_gelu_gate_47104": 3 * M4 * C * 2,
         "cfg3_qk_rmsnorm_rope3d_47104": 4 * M4 * 32 * 128 * 2 + M4 * 64 * 2 * 4,
         "cfg4_rmsnorm_wht128_quant_16896": M2 * C * 2 + M2 * C + M2 * 4,
@@ -98,8 +98,8 @@ def main() -> int:
                          "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the per-token kernels shard "
-              "by token rows with no exchange; see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py: one GPU only; --gpus {args.gpus} is not supported (the per-token kernels would shard by "
+              "contiguous token rows with no exchange step, so one GPU's share is the measured workload)", file=sys.stderr)
         return 2
 
     import numpy as np

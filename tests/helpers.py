@@ -1,4 +1,5 @@
-"""Helpers shared by the tests: uploads, bit comparisons of 16-bit floats, the tolerance of BASELINE's parity bar."""
+"""Helpers shared by the tests: uploads, bit comparisons of 16-bit floats, and the parity tolerance for results
+through transcendental functions (relative error 1e-3, one unit in the last place on few elements)."""
 import numpy as np
 
 from oracle import oracle as o
@@ -43,7 +44,7 @@ def assert_bits_equal(got, want, what=""):
 
 
 def assert_close_16(got, want, dt, what="", max_ulp=1, max_frac=1e-3, rel_l2=1e-3, abs_floor=1e-6):
-    """BASELINE's bar for outputs through a transcendental function: at most max_ulp units in the last place apart
+    """The parity bar for outputs through a transcendental function: at most max_ulp units in the last place apart
     (or within abs_floor, for results that cancel to near zero), on at most max_frac of the elements, and the
     relative L2 error of reference::compare below rel_l2."""
     got, want = np.asarray(got).ravel(), np.asarray(want).ravel()

@@ -1,6 +1,6 @@
 """GPU parity of h3s_attention / h3s_attention_batch (kernels/h3sycl.cpp:1433-1917) against the oracle's restatement:
 the int8 (SageAttention) form and the 16-bit form, through the C ABI. The reference's kernels are third-party (Intel's
-ARK, oneDNN) and their rounding inside the softmax is not restated, so the bar is BASELINE's tolerance on the result:
+ARK, oneDNN) and their rounding inside the softmax is not restated, so the bar is the parity tolerance on the result:
 relative L2 below 1e-3 against the oracle's float64 softmax of the same quantized operands."""
 import os
 

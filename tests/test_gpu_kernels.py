@@ -1,6 +1,6 @@
 """GPU parity: every kernel of libh3hip.so, called through the C ABI (the Python mirror of engine/h3-core/src/ops.rs),
 against the CPU oracle on the same seeded inputs. Bit-exact where the arithmetic is +, -, *, /, sqrt and fma;
-BASELINE's tolerance (1 bf16 ulp on few elements, relative L2 < 1e-3) where it goes through exp or tanh."""
+the parity tolerance (1 bf16 ulp on few elements, relative L2 < 1e-3) where it goes through exp or tanh."""
 import numpy as np
 import pytest
 
@@ -301,7 +301,7 @@ def test_swiglu_quant(dev, rot, group, x_dt, h_dt, M, C):
     want_q, want_s = o.quantize_act(act.to_numpy().ravel(), h_dt, M, C, rot, group)
     assert_bits_equal(gs, want_s, "scales")
     codes_close(gq, want_q, "codes")
-    # against the oracle's whole chain (its expf and division): BASELINE's tolerance
+    # against the oracle's whole chain (its expf and division): the parity tolerance
     oq, os_ = o.swiglu_quant(x, x_dt, M, C, h_dt, rot, group)
     rel, _ = o.compare(gs, os_)
     assert rel < 1e-3 and np.all(np.abs(gs / os_ - 1) <= 2.0 ** -7), "scales"

@@ -1,6 +1,6 @@
 """GPU parity of the plain linear layers (kernels/h3sycl.cpp:656-739) through the C ABI against the oracle's float64
 products: h3s_linear, h3s_linear_acc (row chunks included) and h3s_scale_rows. The reference's products are oneDNN's,
-whose accumulation order is not restated: BASELINE's tolerance (relative L2 < 1e-3, one ulp of the output type)."""
+whose accumulation order is not restated: the parity tolerance (relative L2 < 1e-3, one ulp of the output type)."""
 import numpy as np
 import pytest
 
