@@ -284,19 +284,21 @@ int h3o_layer_norm(const void* x, int x_dt, int64_t M, int64_t C, const float* w
 }
 
 /* ---- rms_rope: kernels/h3sycl.cpp:1276-1376 ----
- * Canonical per-head order: a head's D features are chunks of V; "slots" are the rotated pairs of chunks
- * (p, p + half / V) for p < half / V, then the passed-through chunks from rot_dim on, one per slot. Slot p
- * accumulates its chunk(s) in that order; the P slot partials (padded with zeros to a power of two) are combined by
- * the xor butterfly. */
+ * Canonical per-head order. With V the elements of a 16-byte vector and half = rot_dim / 2, a head's features are
+ * dealt to "slots": rotated slot p takes the pairs j in [pV, min(pV + V, half)) - its first features j, then their
+ * partners half + j - and pass-through slot q the features [rot + qV, min(rot + qV + V, D)). So there are
+ * ceil(half / V) rotated slots and ceil((D - rot) / V) pass-through ones; when half and D - rot are whole vectors,
+ * a slot is one 16-byte chunk (a rotated slot the pair of chunks p, p + half / V). Slot s accumulates its squares
+ * in that order; the P slot partials, padded with zeros to a power of two, are combined by the xor butterfly. */
 static int pow2ceil(int n) { int p = 1; while (p < n) p *= 2; return p; }
 typedef struct {
     void* x; int x_dt; int64_t H, D, stride; const float* w; float eps; const float* cs; int rot;
 } rope_ctx;
 static void rope_rows(void* p, int64_t r0, int64_t r1) {
     const rope_ctx* c = (const rope_ctx*) p;
-    const int64_t D = c->D, half = c->rot / 2;
+    const int64_t D = c->D, half = c->rot / 2, npf = D - c->rot;
     const int V = vec_of(c->x_dt);
-    const int nrot = (int) (half / V), npass = (int) ((D - c->rot) / V), P = nrot + npass, P2 = pow2ceil(P);
+    const int nrot = (int) ((half + V - 1) / V), npass = (int) ((npf + V - 1) / V), P = nrot + npass, P2 = pow2ceil(P);
     float* v = (float*) malloc((size_t) D * sizeof(float));
     for (int64_t m = r0; m < r1; ++m)
         for (int64_t h = 0; h < c->H; ++h) {
@@ -304,16 +306,14 @@ static void rope_rows(void* p, int64_t r0, int64_t r1) {
             for (int64_t i = 0; i < D; ++i) v[i] = h3o_load(c->x, c->x_dt, base + i);
             float part[64];
             for (int s = 0; s < P2; ++s) part[s] = 0.0f;
-            for (int s = 0; s < P; ++s) {
-                int64_t chunks[2];
-                int nc = 0;
-                if (s < nrot) { chunks[nc++] = s; chunks[nc++] = s + nrot; }
-                else chunks[nc++] = 2 * nrot + (s - nrot);
-                for (int k = 0; k < nc; ++k)
-                    for (int e = 0; e < V; ++e) {
-                        const float a = v[chunks[k] * V + e];
-                        part[s] = fmaf(a, a, part[s]);
-                    }
+            for (int s = 0; s < nrot; ++s) {
+                const int64_t j0 = (int64_t) s * V, j1 = j0 + V < half ? j0 + V : half;
+                for (int64_t j = j0; j < j1; ++j) part[s] = fmaf(v[j], v[j], part[s]);
+                for (int64_t j = j0; j < j1; ++j) part[s] = fmaf(v[half + j], v[half + j], part[s]);
+            }
+            for (int q = 0; q < npass; ++q) {
+                const int64_t i0 = c->rot + (int64_t) q * V, i1 = i0 + V < D ? i0 + V : D;
+                for (int64_t i = i0; i < i1; ++i) part[nrot + q] = fmaf(v[i], v[i], part[nrot + q]);
             }
             const float inv = inv_root(butterfly(part, P2), D, c->eps);
             for (int64_t j = 0; j < half; ++j) {
@@ -335,8 +335,8 @@ int h3o_rms_rope(void* x, int x_dt, int64_t M, int64_t H, int64_t D, int64_t str
     if (stride < H * D) return fail("rms_rope: the row stride is shorter than a row");
     if (!dt_ok(x_dt)) return fail("rms_rope: unknown element type");
     const int V = vec_of(x_dt);
-    if ((rot_dim / 2) % V != 0 || (D - rot_dim) % V != 0 || pow2ceil((int) ((rot_dim / 2) / V + (D - rot_dim) / V)) > 64)
-        return fail("rms_rope: rot_dim / 2 and D - rot_dim must be multiples of the 16-byte vector, at most 64 slots");
+    if (pow2ceil((int) ((rot_dim / 2 + V - 1) / V + (D - rot_dim + V - 1) / V)) > 64)
+        return fail("rms_rope: a head of more than 64 slots");
     rope_ctx c = {x, x_dt, H, D, stride, weight, eps, cs, rot_dim};
     parallel_rows(M, rope_rows, &c);
     return 0;
@@ -350,6 +350,9 @@ float h3o_act(float v, int act) {
         return 0.5f * v * (1.0f + tanhf(k * (v + 0.044715f * v * v * v)));
     }
     return v;
+}
+void h3o_act_n(const float* v, int64_t n, int act, float* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = h3o_act(v[i], act);
 }
 
 /* ---- swiglu: kernels/h3sycl.cpp:1378-1419 ---- */
@@ -378,16 +381,20 @@ int h3o_gate_add(void* x, int x_dt, int64_t M, int64_t C, const void* other, int
 }
 
 /* ---- rotations ---- */
-/* regular: one base-4 digit at a time, low digit first; for the four values x0..x3 that differ only in that digit,
- * t = (x0 + x1) + (x2 + x3) and y_a = t - 2 x_(3-a) (kernels/h3sycl.cpp:408-412, 433-459; the pairwise sum is the
- * association of the reference's cross-lane digits, h3sycl.cpp:444-453); then * 1/sqrt(g), a power of two. Sylvester: h = 1, 2, ..., g/2, (a, b) -> (a + b, a - b); then * fl(1/sqrt(g)). */
+/* regular: one base-4 digit at a time, low digit first (kernels/h3sycl.cpp:433-456). For the four values x0..x3
+ * that differ only in that digit, y_a = t - 2 x_(3-a), with t formed as the reference's group-of-256 kernel forms
+ * it: its work-item holds 16 consecutive features, so the digits of stride 1 and 4 are summed in registers left to
+ * right, t = ((x0 + x1) + x2) + x3 (h3sycl.cpp:440), and the digits of stride 16 and 64 across the lanes, pairwise,
+ * t = (x0 + x1) + (x2 + x3) (h3sycl.cpp:452-453). Then * 1/sqrt(g), a power of two (h3sycl.cpp:456). The smaller
+ * groups (4, 16, 64) take the same rule by stride.
+ * Sylvester: h = 1, 2, ..., g/2, (a, b) -> (a + b, a - b); then * fl(1/sqrt(g)). */
 void h3o_rotate_group(float* y, int g, int kind) {
     if (kind == H3O_ROT_REGULAR) {
         for (int d = 1; d < g; d *= 4)
             for (int i = 0; i < g; ++i) {
                 if ((i / d) % 4 != 0) continue;
                 const float x0 = y[i], x1 = y[i + d], x2 = y[i + 2 * d], x3 = y[i + 3 * d];
-                const float t = (x0 + x1) + (x2 + x3);
+                const float t = d < 16 ? ((x0 + x1) + x2) + x3 : (x0 + x1) + (x2 + x3);
                 y[i] = t - 2.0f * x3;
                 y[i + d] = t - 2.0f * x2;
                 y[i + 2 * d] = t - 2.0f * x1;

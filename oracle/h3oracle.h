@@ -123,6 +123,7 @@ int h3o_norm_mod_act_gate(const void* x, int x_dt, int64_t M, int64_t C, int nor
                           const void* gate, int tab_dt, int act, const void* res, int res_dt, void* out, int out_dt);
 /* the pointwise activations, float32 */
 float h3o_act(float v, int act);
+void h3o_act_n(const float* v, int64_t n, int act, float* out);   /* h3o_act on each of n values */
 
 /* ---- attention (kernels/h3sycl.h:185-192; kernels/h3sycl.cpp:1433-1917) ----
  * out = softmax(q . k^T / sqrt(D)) . v per head; q, k, v: S rows of H heads x D features at row stride `stride`

@@ -72,6 +72,7 @@ _SIGS = {
     "h3o_scale_rows": (None, [vp, i32, i64, i64, vp]),
     "h3o_rotations": (None, [vp, i64, vp, i64, vp]),
     "h3o_act": (f32, [f32, i32]),
+    "h3o_act_n": (None, [vp, i64, i32, vp]),
     "h3o_compare": (None, [vp, vp, i64, vp, vp]),
     "h3o_last_error": (C.c_char_p, []),
 }
@@ -366,6 +367,14 @@ def norm_mod_act_gate(x, x_dt, M, C_, norm, weight, bias, eps, rows=None, scale=
 
 def act(v: float, kind: int) -> float:
     return float(lib().h3o_act(v, kind))
+
+
+def act_n(v: np.ndarray, kind: int) -> np.ndarray:
+    """h3o_act on every value of a float32 array"""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.empty_like(v)
+    lib().h3o_act_n(_p(v), v.size, kind, _p(out))
+    return out
 
 
 def compare(a: np.ndarray, b: np.ndarray):

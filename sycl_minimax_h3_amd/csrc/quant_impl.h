@@ -141,31 +141,44 @@ template <int V, bool SW = false> __device__ __forceinline__ void sylvester(floa
     if (G > 32 * V) syl_x<V, 32, SW>(v, pos);
 }
 
-// ---- regular: one base-4 digit at a time, low digit first (kernels/h3sycl.cpp:433-459); for the four values
-// x0..x3 that differ in that digit, t = (x0 + x1) + (x2 + x3) and y_a = t - 2 x_(3-a) ----
-// the digit of stride D inside the lane (4 D <= V)
-template <int V, int D> __device__ __forceinline__ void reg_in(float (&v)[V]) {
+// ---- regular: one base-4 digit at a time, low digit first (kernels/h3sycl.cpp:433-456); for the four values
+// x0..x3 that differ in that digit, y_a = t - 2 x_(3-a). t is formed as the reference's group-of-256 kernel forms
+// it: the digits of stride 1 and 4 (inside its work-item's registers) left to right, ((x0 + x1) + x2) + x3
+// (h3sycl.cpp:440); the digits of stride 16 and 64 (across its lanes) pairwise, (x0 + x1) + (x2 + x3)
+// (h3sycl.cpp:452-453). Float addition commutes bit for bit, so every lane forms the same t from its own view. ----
+// the value of lane 4 (lane / 4) + p[lane % 4] of each quad, for the DPP quad_perm control CTRL
+template <int CTRL> __device__ __forceinline__ float quad(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+// the digit of stride 1, inside a chunk
+template <int V> __device__ __forceinline__ void reg_in(float (&v)[V]) {
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
-        if ((e / D) % 4 != 0) continue;
-        const float x0 = v[e], x1 = v[e + D], x2 = v[e + 2 * D], x3 = v[e + 3 * D];
-        const float t = (x0 + x1) + (x2 + x3);
-        v[e] = t - 2.0f * x3; v[e + D] = t - 2.0f * x2; v[e + 2 * D] = t - 2.0f * x1; v[e + 3 * D] = t - 2.0f * x0;
+    for (int e = 0; e < V; e += 4) {
+        const float x0 = v[e], x1 = v[e + 1], x2 = v[e + 2], x3 = v[e + 3];
+        const float t = ((x0 + x1) + x2) + x3;
+        v[e] = t - 2.0f * x3; v[e + 1] = t - 2.0f * x2; v[e + 2] = t - 2.0f * x1; v[e + 3] = t - 2.0f * x0;
     }
 }
 // the digit of stride 4 with V = 8: x0, x1 at e and e + 4 of an even lane, x2, x3 at e and e + 4 of the odd lane
-// beside it. Each lane forms its own pair sum and its partner's from the partner's values (the same additions, so
-// the same bits), t = own + other (equal to (x0 + x1) + (x2 + x3) in both lanes), and the mirror value x_(3-a)
-// is the partner's value at the other half of the chunk.
-__device__ __forceinline__ void reg_mixed(float (&v)[8]) {
-    float p[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) p[e] = lane_xor<1>(v[e]);
+// beside it. The even lane's pair sum x0 + x1 goes to both lanes (quad_perm [0,0,2,2]), then the odd lane's x2 and
+// x3 are added in turn ([1,1,3,3]); the mirror x_(3-a) is the partner's value at the other half of the chunk
+// ([1,0,3,2]).
+__device__ __forceinline__ void reg_pair(float (&v)[8]) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const float t = (v[r] + v[r + 4]) + (p[r] + p[r + 4]);
-        v[r] = t - 2.0f * p[r + 4];
-        v[r + 4] = t - 2.0f * p[r];
+        const float lo = v[r], hi = v[r + 4];
+        const float t = (quad<0xA0>(lo + hi) + quad<0xF5>(lo)) + quad<0xF5>(hi);
+        v[r] = t - 2.0f * quad<0xB1>(hi);
+        v[r + 4] = t - 2.0f * quad<0xB1>(lo);
+    }
+}
+// the digit of stride 4 with V = 4: x0..x3 in the four lanes of a quad, taken in order (quad_perm [a,a,a,a]); the
+// mirror from the reversed quad ([3,2,1,0])
+__device__ __forceinline__ void reg_quad(float (&v)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float t = ((quad<0x00>(v[e]) + quad<0x55>(v[e])) + quad<0xAA>(v[e])) + quad<0xFF>(v[e]);
+        v[e] = t - 2.0f * quad<0x1B>(v[e]);
     }
 }
 // the digit whose four values sit in lanes S apart (a = (lane / S) % 4): the own pair x_a + x_(a^1), the other pair
@@ -179,13 +192,13 @@ template <int V, int S> __device__ __forceinline__ void reg_x(float (&v)[V]) {
     }
 }
 template <int V> __device__ __forceinline__ void regular(float (&v)[V], int G) {
-    if (G > 1) reg_in<V, 1>(v);
+    if (G > 1) reg_in<V>(v);
     if constexpr (V == 8) {
-        if (G > 4) reg_mixed(v);
+        if (G > 4) reg_pair(v);
         if (G > 16) reg_x<8, 2>(v);
         if (G > 64) reg_x<8, 8>(v);
     } else {
-        if (G > 4) reg_x<4, 1>(v);
+        if (G > 4) reg_quad(v);
         if (G > 16) reg_x<4, 4>(v);
         if (G > 64) reg_x<4, 16>(v);
     }

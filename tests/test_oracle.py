@@ -469,3 +469,186 @@ def test_attention_causal_oracle():
         p = np.exp(s - s.max(1, keepdims=True))
         p /= p.sum(1, keepdims=True)
         assert np.allclose(out[:, h], p @ v[:, gkv * D:(gkv + 1) * D], rtol=1e-5, atol=1e-5)
+
+
+# ---- the regular butterfly's association: kernels/h3sycl.cpp:433-456 ----
+# A planted digit: a column of four values [a, e a, e a, e a] with e = 2^-24. Summed left to right (the two digits a
+# work-item of the reference holds in registers, h3sycl.cpp:440), a + e a rounds back to a at each step, so
+# t = a and the outputs are [a (1 - 2^-23)] * 3 + [-a]; summed pairwise (the digits across lanes, h3sycl.cpp:452-453),
+# t = a (1 + 2^-23) exactly and the outputs are [a] * 3 + [a (-1 + 2^-23)]. Every other digit of the planted input
+# sees a column [v, 0, 0, 0], whose outputs [v, v, v, -v] are exact, so the whole result is known in closed form.
+def _planted_digit(g, k):
+    x = np.zeros(g, dtype=np.float32)
+    d = 4 ** k
+    x[0] = 1.0
+    x[d] = x[2 * d] = x[3 * d] = np.float32(2.0 ** -24)
+    return x
+
+
+def _planted_expected(g, k, left_to_right):
+    nd = int(round(math.log(g, 4)))
+    mid = [1 - 2.0 ** -23] * 3 + [-1.0] if left_to_right else [1.0] * 3 + [-1 + 2.0 ** -23]
+    sign = [1.0, 1.0, 1.0, -1.0]
+    y = np.empty(g, dtype=np.float64)
+    for p in range(g):
+        v = 1.0
+        for j in range(nd):
+            digit = (p // 4 ** j) % 4
+            v *= mid[digit] if j == k else sign[digit]
+        y[p] = v / math.sqrt(g)
+    return y.astype(np.float32)
+
+
+@pytest.mark.parametrize("g", [4, 16, 64, 256])
+def test_regular_butterfly_association(oracle, g):
+    """digits of stride 1 and 4 left to right, of stride 16 and 64 pairwise"""
+    for k in range(int(round(math.log(g, 4)))):
+        got = oracle.rotate_group(_planted_digit(g, k), oracle.ROT_REGULAR)
+        want = _planted_expected(g, k, left_to_right=4 ** k < 16)
+        other = _planted_expected(g, k, left_to_right=4 ** k >= 16)
+        assert not np.array_equal(want, other)
+        assert np.array_equal(got, want), f"g {g}, digit {k}"
+
+
+def test_regular_butterfly_digit_order(oracle):
+    """The low digit first (h3sycl.cpp:433-456). x[0] = 1, x[1..3] = e and x[4] = x[8] = x[12] = e, e = 2^-24: the
+    first digit turns the column (0..3) into [1 - 2e] * 3 + [-1], the second then sums each column
+    [1 - 2e, e, e, e] left to right to exactly 1 (and [-1, -e, -e, -e] to -1), so position r + 4 q holds
+    [1 - 2e, 1 - 2e, 1 - 2e, -1 + 4e][q] for r < 3 and [-1 + 2e, -1 + 2e, -1 + 2e, 1][q] for r = 3. Taken the other
+    way round, position 3 would hold -1 + 4e instead of -1 + 2e."""
+    e = 2.0 ** -24
+    x = np.zeros(16, dtype=np.float32)
+    x[0] = 1.0
+    x[[1, 2, 3, 4, 8, 12]] = np.float32(e)
+    col = [1 - 2 * e, 1 - 2 * e, 1 - 2 * e, -1 + 4 * e]
+    last = [-1 + 2 * e, -1 + 2 * e, -1 + 2 * e, 1.0]
+    want = np.array([(col if r < 3 else last)[q] / 4 for q in range(4) for r in range(4)], dtype=np.float32)
+    assert np.array_equal(oracle.rotate_group(x, oracle.ROT_REGULAR), want)
+
+
+def test_convrot_codes_against_the_reference_cpu_arithmetic(oracle):
+    """The g = 256 quantizer of h3s_int8_linear against engine/h3-core/src/reference.rs:52-70: each rotated value as
+    the reference's CPU path forms it (a float32 sum over the dense normalized matrix in input order), its row scale
+    and round_ties_even. The two orders of summation may round differently, so a code may differ by 1 - only where
+    the exact value y / s lies within the two computations' error bound of a rounding boundary. The bound per
+    element: the dense sum errs by at most 255 u A and the butterfly (four digits, at most four roundings each) by
+    16 u A, A = sum |x_i| / 16 over the group, u = 2^-24; the scale carries the error of its row's maximum. No code
+    may differ by 2 or more."""
+    u = 2.0 ** -24
+    M, K, g = 256, 4096, 256
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((M, K)).astype(np.float32) * np.where(rng.random(K) < 0.01, 20.0, 1.0).astype(np.float32)
+    xb = oracle.to_bf16(x)
+    X = oracle.from_bf16(xb).reshape(M, K // g, g)
+    q_o, s_o = oracle.quantize_act(xb.ravel(), oracle.BF16, M, K, oracle.ROT_REGULAR, g)
+    q_o = q_o.reshape(M, K).astype(np.int32)
+    H = oracle.hadamard(g, oracle.ROT_REGULAR)
+    acc = np.zeros_like(X)
+    for i in range(g):                                          # reference.rs:57-60, in float32 without fma
+        acc = (acc + X[:, :, i:i + 1] * H[i][None, None, :]).astype(np.float32)
+    xr = acc.reshape(M, K)
+    s_r = np.maximum(np.abs(xr).max(1) / np.float32(127), np.float32(1e-30)).astype(np.float32)   # reference.rs:67
+    q_r = np.clip(np.rint(xr / s_r[:, None]), -128, 127).astype(np.int32)                          # reference.rs:68-70
+    ye = (X.astype(np.float64) @ H.astype(np.float64)).reshape(M, K)
+    me = np.abs(ye).max(1)
+    z = ye / (me / 127)[:, None]
+    A = np.abs(X.astype(np.float64)).sum(-1) / 16
+    err = (255 + 16) * u * 1.01
+    delta = err * np.repeat(A, g, axis=1) / (me / 127)[:, None] + np.abs(z) * (err * A.max(1) / me + 3 * u)[:, None]
+    d = q_o - q_r
+    assert np.abs(d).max() <= 1
+    bad = d != 0
+    boundary = np.minimum(q_o, q_r) + 0.5
+    assert np.all(np.abs(z - boundary)[bad] <= delta[bad]), "a code differs away from a rounding boundary"
+    assert np.all(np.abs(s_o / s_r - 1) <= 4 * u)
+    # the comparison has teeth: the butterfly with the wrong mirror (y_a = t - 2 x_a, the matrix ones - 2 I per digit)
+    # moves codes by 2 or more
+    hm = np.ones((4, 4)) - 2 * np.eye(4)
+    Hm = np.kron(np.kron(hm, hm), np.kron(hm, hm)) / 16
+    qm, _ = oracle.quantize_rows(np.ascontiguousarray((X.astype(np.float64) @ Hm).astype(np.float32).reshape(M, K)), M, K)
+    assert np.abs(qm.reshape(M, K).astype(np.int32) - q_r).max() >= 2
+
+
+# ---- closed forms for the pointwise oracle functions ----
+def test_swiglu_closed_form(oracle):
+    """kernels/h3sycl.cpp:1394-1396: out = silu(x[:, :C]) * x[:, C:], the gate half first"""
+    M, C = 9, 520
+    x = (3 * np.random.default_rng(50).standard_normal((M, 2 * C))).astype(np.float32)
+    g, up_ = x[:, :C].astype(np.float64), x[:, C:].astype(np.float64)
+    want = g / (1 + np.exp(-g)) * up_
+    got = oracle.swiglu(x.ravel(), oracle.F32, M, C, oracle.F32).reshape(M, C)
+    assert np.all(np.abs(got - want) <= 4e-7 * np.abs(want) + 1e-30)
+    # 16-bit in and out: within one unit in the last place of the float64 value
+    xb = oracle.to_bf16(x)
+    xf = oracle.from_bf16(xb).astype(np.float64).reshape(M, 2 * C)
+    want16 = xf[:, :C] / (1 + np.exp(-xf[:, :C])) * xf[:, C:]
+    got16 = oracle.from_bf16(oracle.swiglu(xb.ravel(), oracle.BF16, M, C, oracle.BF16)).reshape(M, C)
+    assert np.all(np.abs(got16 - want16) <= 2.0 ** -8 * np.abs(want16) + 1e-30)
+
+
+def test_gate_add_closed_form(oracle):
+    """kernels/h3sycl.cpp:1421-1431: x[r] += other[r] * gate[rows[r]], in float32, rounded once to x's type; rows
+    that are not the identity"""
+    M, C, R = 7, 264, 4
+    rng = np.random.default_rng(51)
+    x = oracle.to_bf16(rng.standard_normal((M, C)).astype(np.float32))
+    other = rng.standard_normal((M, C)).astype(np.float32)
+    rows = np.array([3, 0, 2, 2, 1, 3, 0], dtype=np.int32)
+    gate = rng.standard_normal((R, C)).astype(np.float32)
+    want = oracle.to_bf16(oracle.from_bf16(x).reshape(M, C) + other * gate[rows])
+    got = oracle.gate_add(x.ravel(), oracle.BF16, M, C, other.ravel(), oracle.F32, rows, gate.ravel())
+    assert np.array_equal(got, want.ravel())
+    # no gate: a plain add (ops.rs add)
+    want = oracle.to_bf16(oracle.from_bf16(x).reshape(M, C) + other)
+    assert np.array_equal(oracle.gate_add(x.ravel(), oracle.BF16, M, C, other.ravel(), oracle.F32), want.ravel())
+
+
+@pytest.mark.parametrize("affine", [False, True])
+def test_layer_norm_chain_is_a_composition(oracle, affine):
+    """Config 2's chain (h3o_norm_mod_act_gate with the layer norm) equals h3o_layer_norm into float32, then
+    x (1 + scale) + shift, GELU-tanh, * gate and + res in float32, rounded once to bfloat16, with [1, C] bfloat16
+    tables (every row reads table row 0)."""
+    M, C = 24, 4096
+    rng = np.random.default_rng(52)
+    x = oracle.to_bf16(rng.standard_normal((M, C)).astype(np.float32))
+    res = oracle.to_bf16(rng.standard_normal((M, C)).astype(np.float32))
+    sc, sh, gt = (oracle.to_bf16((0.5 * rng.standard_normal(C)).astype(np.float32)) for _ in range(3))
+    w = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32) if affine else None
+    b = (0.1 * rng.standard_normal(C)).astype(np.float32) if affine else None
+    got = oracle.norm_mod_act_gate(x.ravel(), oracle.BF16, M, C, oracle.NORM_LAYER, w, b, 1e-5, None, sc, sh, gt,
+                                   oracle.BF16, oracle.ACT_GELU_TANH, res.ravel(), oracle.BF16, oracle.BF16)
+    ln = oracle.layer_norm(x.ravel(), oracle.BF16, M, C, w, b, 1e-5, oracle.F32).reshape(M, C)
+    f = oracle.from_bf16
+    v = (ln * (np.float32(1) + f(sc))[None]).astype(np.float32) + f(sh)[None]
+    v = oracle.act_n(v, oracle.ACT_GELU_TANH).reshape(M, C)
+    want = oracle.to_bf16(f(res).reshape(M, C) + (v * f(gt)[None]).astype(np.float32))
+    assert np.array_equal(got, want.ravel())
+    # a mis-indexed table (the shift read as the scale) is caught
+    bad = oracle.norm_mod_act_gate(x.ravel(), oracle.BF16, M, C, oracle.NORM_LAYER, w, b, 1e-5, None, sh, sc, gt,
+                                   oracle.BF16, oracle.ACT_GELU_TANH, res.ravel(), oracle.BF16, oracle.BF16)
+    assert not np.array_equal(bad, want.ravel())
+
+
+# ---- rotary with partial slots: rot_dim / 2 or D - rot_dim not a whole 16-byte vector ----
+@pytest.mark.parametrize("dt", [o.F32, o.BF16])
+@pytest.mark.parametrize("D,rot", [(128, 126), (128, 120), (128, 60), (128, 2), (64, 48), (128, 128)])
+def test_rms_rope_partial_slots(oracle, dt, D, rot):
+    """Every even rot_dim with an even remainder (kernels/h3sycl.cpp:1280-1282): the pairs (j, rot/2 + j) rotate by
+    the table's angle, features from rot_dim on are only normalized, and the norm is the head's RMS."""
+    rng = np.random.default_rng(53)
+    M, H = 4, 3
+    stride = 3 * H * D
+    x = oracle.to_dt(rng.standard_normal(M * stride).astype(np.float32), dt)
+    w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    h = rot // 2
+    ang = rng.uniform(-10, 10, (M, h))
+    cs = np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32).ravel()
+    y = oracle.from_dt(oracle.rms_rope(x, dt, M, H, D, stride, w, 1e-5, cs, rot), dt).reshape(M, stride)
+    X = oracle.from_dt(x, dt).reshape(M, stride).astype(np.float64)
+    assert np.array_equal(y[:, H * D:], X[:, H * D:].astype(np.float32))            # the rest of the row is untouched
+    Xh, Y = X[:, :H * D].reshape(M, H, D), y[:, :H * D].reshape(M, H, D).astype(np.float64)
+    N = Xh / np.sqrt((Xh ** 2).mean(-1, keepdims=True) + 1e-5) * w
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    tol = 1e-5 if dt == o.F32 else 2.0 ** -7
+    want = np.concatenate([N[..., :h] * c - N[..., h:rot] * s, N[..., h:rot] * c + N[..., :h] * s, N[..., rot:]], -1)
+    assert np.all(np.abs(Y - want) <= tol * (1 + np.abs(want)))
