@@ -67,7 +67,13 @@ def test_arguments_are_checked_before_the_device(api):
     assert "rot_dim" in api.error()
     assert api.rms_rope(None, p, 2, 4, 32, 128, 4000, p, 1e-5, p, 128) == -1
     assert "stride" in api.error()
+    # any even rot_dim with an even remainder passes the checks (kernels/h3sycl.cpp:1280-1282): 12 and 126 reach the
+    # context check; a head that is not whole 16-byte vectors does not
     assert api.rms_rope(None, p, 2, 4, 32, 128, 4096, p, 1e-5, p, 12) == -1
+    assert "no context" in api.error()
+    assert api.rms_rope(None, p, 2, 4, 56, 128, 3 * 7168, p, 1e-5, p, 126) == -1
+    assert "no context" in api.error()
+    assert api.rms_rope(None, p, 2, 4, 32, 100, 3200, p, 1e-5, p, 96) == -1
     assert "16-byte" in api.error()
     assert api.rms_norm_mod(None, p, 2, 4, 4100, p, 1e-6, None, None, None, p, 2) == -1
     assert "multiple of 8" in api.error()

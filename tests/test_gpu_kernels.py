@@ -157,7 +157,9 @@ def cs_table(seed, M, rot):
 
 
 @pytest.mark.parametrize("x_dt", [o.BF16, o.F16, o.F32])
-@pytest.mark.parametrize("H,D,rot,pad", [(32, 128, 128, 0), (4, 64, 48, 0), (3, 128, 0, 64), (5, 128, 96, 8), (2, 64, 64, 0)])
+@pytest.mark.parametrize("H,D,rot,pad", [(32, 128, 128, 0), (4, 64, 48, 0), (3, 128, 0, 64), (5, 128, 96, 8), (2, 64, 64, 0),
+                                         (7, 128, 126, 0), (5, 128, 120, 8), (3, 128, 60, 0), (4, 64, 2, 0), (2, 64, 62, 16),
+                                         (9, 64, 36, 0)])
 def test_rms_rope(dev, x_dt, H, D, rot, pad):
     M = 13
     stride = H * D + pad
@@ -189,6 +191,29 @@ def test_qk_rms_rope_in_a_qkv_buffer(dev):
     g3 = got.reshape(M, 3, w_)
     assert_bits_equal(g3[:, 0], q_only.reshape(M, 3, w_)[:, 0], "q")
     assert_bits_equal(g3[:, 2], qkv.reshape(M, 3, w_)[:, 2], "v")
+
+
+@pytest.mark.parametrize("rot", [126, 120, 60, 96, 128])
+def test_qk_rms_rope_dit_call(dev, rot):
+    """The DiT's call (engine/h3-core/src/dit.rs:345-348): 56 heads of 128 in the qkv buffer of stride 3 x 7168, with
+    rot_dim = 6 x the checkpoint's frequencies (dit.rs:71): 21, 20 and 10 frequencies split a 16-byte chunk."""
+    M, H, D = 41, 56, 128
+    w_ = H * D
+    qkv = inputs(60, M * 3 * w_, o.BF16)
+    wq, wk = weight(61, D), weight(62, D)
+    cs = cs_table(63, M, rot)
+    want = o.rms_rope(qkv, o.BF16, M, H, D, 3 * w_, wq, 1e-5, cs, rot)
+    want = o.rms_rope(want[w_:], o.BF16, M, H, D, 3 * w_, wk, 1e-5, cs, rot)
+    t = up(dev, qkv, "BF16", [M, 3 * w_])
+    ops.qk_rms_rope(ops.Rows(t, 0, 3 * w_, M, H, D), ops.Rows(t, w_, 3 * w_, M, H, D), up(dev, wq, "F32", [D]),
+                    up(dev, wk, "F32", [D]), 1e-5, up(dev, cs, "F32", [cs.size]), rot)
+    got = t.to_numpy().ravel()
+    assert_bits_equal(got[w_:], want, "qk_rms_rope")
+    # and q alone through h3s_rms_rope, as the reference's graph calls it
+    t2 = up(dev, qkv, "BF16", [M, 3 * w_])
+    ops.rms_rope(ops.Rows(t2, 0, 3 * w_, M, H, D), up(dev, wq, "F32", [D]), 1e-5, up(dev, cs, "F32", [cs.size]), rot)
+    q_only = o.rms_rope(qkv, o.BF16, M, H, D, 3 * w_, wq, 1e-5, cs, rot)
+    assert_bits_equal(t2.to_numpy().ravel(), q_only, "rms_rope q")
 
 
 # ---- h3s_norm_quant: rms_norm_mod -> bf16 h -> quantizer (configs 1, 4, 5a) ----
@@ -279,6 +304,86 @@ def test_norm_quant_long_segments(dev, pattern):
                    h_dtype=DType.BF16)
     assert_bits_equal(s.to_numpy(), want_s, "scales")
     codes_close(q.to_numpy(), want_q, "codes")
+
+
+def test_norm_quant_fixture_rows(dev):
+    """The reference fixture's 2,159-token layout: the table rows of its first step (text, audio and video segments,
+    tests/golden/layout_384x288_2s.json), float32 tables of the AdaLN's shape [rows, C]."""
+    import json
+    import os
+
+    gold = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "layout_384x288_2s.json")))
+    rows = np.concatenate([np.full(n, r, np.int32) for r, n in gold["mod_rows_rle"]])
+    M, C = rows.size, 4096
+    R = int(rows.max()) + 1
+    x = inputs(64, M * C, o.BF16)
+    w = weight(65, C)
+    sc = (0.5 * np.random.default_rng(66).standard_normal(R * C)).astype(np.float32)
+    sh = (0.5 * np.random.default_rng(67).standard_normal(R * C)).astype(np.float32)
+    want_q, want_s = o.norm_quant(x, o.BF16, M, C, w, 1e-6, rows, sc, sh, o.F32, o.BF16)
+    q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+    tb = ops.Tables(scale=up(dev, sc, "F32", [R, C]), shift=up(dev, sh, "F32", [R, C]), rows=up(dev, rows, "I32", [M]))
+    ops.norm_quant(up(dev, x, "BF16", [M, C]), up(dev, w, "F32", [C]), 1e-6, tb, q, s, h_dtype=DType.BF16)
+    assert_bits_equal(s.to_numpy(), want_s, "scales")
+    codes_close(q.to_numpy(), want_q, "codes")
+
+
+@pytest.mark.parametrize("rot,group", [(o.ROT_NONE, 0), (o.ROT_REGULAR, 256)])
+def test_norm_quant_units_of_many_rows(dev, rot, group):
+    """The real model's width (5376) at 16896 tokens with three table segments: every unit of the persistent
+    quantizer takes many rows, prefetching the next row and reloading the table row at the segment boundaries."""
+    M, C = 16896, 5376
+    rows = np.where(np.arange(M) < 137, 1, np.where(np.arange(M) < 323, 2, 0)).astype(np.int32)
+    x = inputs(68, M * C, o.BF16)
+    w = weight(69, C)
+    sc = o.to_dt(0.5 * np.random.default_rng(70).standard_normal(3 * C).astype(np.float32), o.BF16)
+    sh = o.to_dt(0.5 * np.random.default_rng(71).standard_normal(3 * C).astype(np.float32), o.BF16)
+    want_q, want_s = o.norm_quant(x, o.BF16, M, C, w, 1e-6, rows, sc, sh, o.BF16, o.BF16, rot=rot, group=group)
+    q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+    tb = ops.Tables(scale=up(dev, sc, "BF16", [3, C]), shift=up(dev, sh, "BF16", [3, C]), rows=up(dev, rows, "I32", [M]))
+    ops.norm_quant(up(dev, x, "BF16", [M, C]), up(dev, w, "F32", [C]), 1e-6, tb, q, s, rot=rot, group=group,
+                   h_dtype=DType.BF16)
+    assert_bits_equal(s.to_numpy(), want_s, "scales")
+    codes_close(q.to_numpy(), want_q, "codes")
+
+
+def sample_rows(M, band=256):
+    """one row from every band of rows (at an offset that moves from band to band), and the last row"""
+    r = [b * band + (b * 37) % band for b in range((M + band - 1) // band)]
+    return np.unique(np.minimum(np.array(r + [M - 1]), M - 1))
+
+
+def read_rows(t, rows, width, esize):
+    """rows of a [M, width] device tensor, read one at a time"""
+    return np.stack([t._owner.read(width * esize, (t.ptr() - t._owner.ptr()) + int(r) * width * esize) for r in rows])
+
+
+@pytest.mark.parametrize("config", ["4", "5a"])
+def test_norm_quant_full_size(dev, config):
+    """Configs 4 and 5a at their full size (47104 x 4096, the one-wavefront-a-row layout): every row's largest code is
+    127 in magnitude, and sampled rows (one from every 256-row band, and the last) equal the oracle's bit for bit."""
+    M, C = 47104, 4096
+    rng = np.random.default_rng(72)
+    heavy = np.where(rng.random(C) < 0.01, 20.0, 1.0).astype(np.float32) if config == "4" else np.ones(C, np.float32)
+    x = o.to_bf16(rng.standard_normal((M, C), dtype=np.float32) * heavy)
+    w = weight(73, C)
+    if config == "4":
+        tb, sc, sh, rot, group = None, None, None, o.ROT_SYLVESTER, 128
+    else:
+        sc = o.to_bf16((0.5 * rng.standard_normal(C)).astype(np.float32))
+        sh = o.to_bf16((0.5 * rng.standard_normal(C)).astype(np.float32))
+        tb, rot, group = ops.Tables(scale=up(dev, sc, "BF16", [1, C]), shift=up(dev, sh, "BF16", [1, C])), o.ROT_NONE, 0
+    q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+    ops.norm_quant(up(dev, x, "BF16", [M, C]), up(dev, w, "F32", [C]), 1e-6, tb, q, s, rot=rot, group=group,
+                   h_dtype=DType.BF16)
+    gq = q.to_numpy().reshape(M, C)
+    assert np.all(np.abs(gq.astype(np.int32)).max(1) == 127)
+    rows = sample_rows(M)
+    xs = np.ascontiguousarray(x.reshape(M, C)[rows])
+    want_q, want_s = o.norm_quant(xs.ravel(), o.BF16, rows.size, C, w, 1e-6, None, sc, sh, o.BF16, o.BF16, rot=rot,
+                                  group=group)
+    assert_bits_equal(s.to_numpy()[rows], want_s, "scales")
+    codes_close(gq[rows], want_q, "codes")
 
 
 # ---- h3s_swiglu_quant: swiglu -> the MLP's act scratch -> fc2's quantizer, in one pass ----
@@ -390,6 +495,45 @@ def test_int8_gemm_dequant(dev, act, K):
         assert_bits_equal(out.to_numpy(), want, "gemm")
     else:
         assert_close_16(out.to_numpy(), want, o.BF16, "gemm silu", max_frac=5e-3)
+
+
+@pytest.mark.parametrize("act", [o.ACT_NONE, o.ACT_SILU])
+def test_int8_gemm_tile_order(dev, act):
+    """A grid of 10 x 4 tiles (a multiple of 8, more than 8 tile rows): the blocks are renumbered across the XCDs in
+    groups of 8 tile rows, as at config 5b's size."""
+    M, N, K = 2560, 1024, 4096
+    rng = np.random.default_rng(74)
+    q = rng.integers(-128, 128, M * K, dtype=np.int8)
+    s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    w = rng.integers(-127, 128, N * K, dtype=np.int8)
+    ws = rng.uniform(0.005, 0.02, N).astype(np.float32)
+    want = o.gemm_dequant(q, s, M, K, w, N, ws, None, act, o.BF16)
+    layer = ops.Int8Linear(up(dev, w, "I8", [N, K]), up(dev, ws, "F32", [N]))
+    out = new(dev, "BF16", [M, N])
+    ops.int8_gemm_dequant(up(dev, q, "I8", [M, K]), up(dev, s, "F32", [M]), layer, act, out)
+    if act == o.ACT_NONE:
+        assert_bits_equal(out.to_numpy(), want, "gemm")
+    else:
+        assert_close_16(out.to_numpy(), want, o.BF16, "gemm silu", max_frac=5e-3)
+
+
+def test_int8_gemm_full_size(dev):
+    """Config 5b at its full size, 47104 x 16384 x 4096 with the SiLU epilogue: one row from every 256-row tile band
+    (and the last row), all 16384 columns, against the oracle."""
+    M, N, K = 47104, 16384, 4096
+    rng = np.random.default_rng(75)
+    q = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    w = rng.integers(-127, 128, N * K, dtype=np.int8)
+    ws = rng.uniform(0.005, 0.02, N).astype(np.float32)
+    layer = ops.Int8Linear(up(dev, w, "I8", [N, K]), up(dev, ws, "F32", [N]))
+    out = new(dev, "BF16", [M, N])
+    ops.int8_gemm_dequant(up(dev, q, "I8", [M, K]), up(dev, s, "F32", [M]), layer, o.ACT_SILU, out)
+    rows = sample_rows(M)
+    got = read_rows(out, rows, N, 2).view(np.uint16)
+    want = o.gemm_dequant(np.ascontiguousarray(q[rows]).ravel(), np.ascontiguousarray(s[rows]), rows.size, K, w, N, ws,
+                          None, o.ACT_SILU, o.BF16)
+    assert_close_16(got, want, o.BF16, "gemm silu full size", max_frac=5e-3)
 
 
 # ---- errors through the ABI on the device ----
