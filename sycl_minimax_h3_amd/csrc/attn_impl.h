@@ -52,104 +52,79 @@ __device__ __forceinline__ uint16_t half_bits(float x) {
 
 // k's mean over the sequence per (head, feature): a float32 sum in token order, / S (h3sycl.cpp:1732-1737). Each
 // feature's sum is one serial chain of S additions, so the kernel is built to run that chain at the adder's latency:
-// a block takes 32 features (128 blocks at 4096 features); all its wavefronts fill a ring of four 16 KiB row chunks
-// with direct loads (global_load_lds_dwordx4, three chunks in flight), and the first wavefront runs the 32 sums, one
-// feature a lane, reading 16 rows ahead of the additions. Needs the rows 16-byte aligned (k and the stride);
-// attn_kmean_rows_kernel is the general form.
-constexpr int kKmeanFeat = 32, kKmeanStages = 4, kKmeanChunk = 16384;
+// a block takes 32 features (128 blocks at 4096 features). Wavefronts 1-3 fill a ring of four 12 KiB row chunks with
+// direct loads (global_load_lds_dwordx4, three chunks in flight); wavefront 0 runs the 32 sums, one feature a lane,
+// with ordinary LDS reads 16 rows ahead of the additions. Wavefront 0 issues no global loads, so the waits the
+// compiler places before its LDS reads are exact and never wait on the ring's loads. Needs the rows 16-byte aligned
+// (k and the stride); attn_kmean_rows_kernel is the general form.
+constexpr int kKmeanFeat = 32, kKmeanStages = 4, kKmeanChunk = 12288, kKmeanLoaders = 192;
 template <int DT>
 __global__ __launch_bounds__(256) void attn_kmean_kernel(const void* __restrict__ k, int64_t S, int64_t stride,
                                                          float* __restrict__ mean) {
     constexpr int ESZ = DT == H3S_F32 ? 4 : 2, RB = kKmeanFeat * ESZ;          // bytes of a row's 32 features
-    constexpr int SEG = RB / 16, ROWS = kKmeanChunk / RB, LPT = kKmeanChunk / (256 * 16);
+    constexpr int SEG = RB / 16, ROWS = kKmeanChunk / RB, LPT = kKmeanChunk / (kKmeanLoaders * 16);
+    static_assert(kKmeanChunk % RB == 0 && kKmeanChunk % (kKmeanLoaders * 16) == 0, "attn_kmean_kernel: chunk shape");
     __shared__ __attribute__((aligned(16))) uint8_t ring[kKmeanStages * kKmeanChunk];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t c0 = (int64_t) blockIdx.x * kKmeanFeat, nch = (S + ROWS - 1) / ROWS;
     const char* base = reinterpret_cast<const char*>(k) + c0 * ESZ;
-    // load i of this thread: unit u = tid + 256 i of the chunk (row u / SEG, 16-byte segment u % SEG), landing at
-    // byte 16 u of the stage: the chunk is row-major, RB bytes a row
+    // loader thread p = tid - 64, load i: unit u = p + 192 i of the chunk (row u / SEG, 16-byte segment u % SEG),
+    // landing at byte 16 u of the stage: the chunk is row-major, RB bytes a row
     auto issue = [&](int64_t ch) {
         uint8_t* st = ring + (ch % kKmeanStages) * kKmeanChunk;
 #pragma unroll
         for (int i = 0; i < LPT; ++i) {
-            const int u = tid + 256 * i;
+            const int u = (tid - 64) + kKmeanLoaders * i;
             int64_t row = ch * ROWS + u / SEG;
             row = row < S ? row : S - 1;
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) (base + row * stride * ESZ + 16 * (u % SEG)),
-                                             (__attribute__((address_space(3))) void*) (st + (4 * i + wave) * 1024), 16, 0, 0);
+                                             (__attribute__((address_space(3))) void*) (st + (3 * i + wave - 1) * 1024), 16, 0, 0);
         }
     };
+    // the value of row r of a stage for this lane's feature, as float32
+    auto at = [&](const uint8_t* st, int r) -> float {
+        const uint8_t* e = st + r * RB + lane * ESZ;
+        if constexpr (DT == H3S_F32) return *reinterpret_cast<const float*>(e);
+        else if constexpr (DT == H3S_BF16) return bf16_lo(*reinterpret_cast<const uint16_t*>(e));
+        else return f16_lo(*reinterpret_cast<const uint16_t*>(e));
+    };
     float sum = 0.0f;
-    for (int64_t ch = 0; ch < kKmeanStages - 1 && ch < nch; ++ch) issue(ch);
+    if (wave > 0)
+        for (int64_t ch = 0; ch < kKmeanStages - 1 && ch < nch; ++ch) issue(ch);
     for (int64_t ch = 0; ch < nch; ++ch) {
-        // this chunk has landed once the loads of the (at most two) chunks issued after it are all that is left
-        const int64_t after = (nch - 1 - ch) < kKmeanStages - 2 ? nch - 1 - ch : kKmeanStages - 2;
-        if (after >= 2) wait_vm<2 * LPT>();
-        else if (after == 1) wait_vm<LPT>();
-        else wait_vm<0>();
-        lds_barrier();                       // every wavefront's loads of chunk ch are in; chunk ch - 1 is summed
-        if (ch + kKmeanStages - 1 < nch) issue(ch + kKmeanStages - 1);   // into chunk ch - 1's stage
+        if (wave > 0) {
+            // this chunk has landed once the loads of the (at most two) chunks issued after it are all that is left
+            const int64_t after = (nch - 1 - ch) < kKmeanStages - 2 ? nch - 1 - ch : kKmeanStages - 2;
+            if (after >= 2) wait_vm<2 * LPT>();
+            else if (after == 1) wait_vm<LPT>();
+            else wait_vm<0>();
+        }
+        lds_barrier();                       // chunk ch is in; wavefront 0's reads of chunk ch - 1 are complete
+        if (wave > 0 && ch + kKmeanStages - 1 < nch) issue(ch + kKmeanStages - 1);   // into chunk ch - 1's stage
         if (wave == 0 && lane < kKmeanFeat) {
-            const uint32_t at = (uint32_t) (uintptr_t) (ring + (ch % kKmeanStages) * kKmeanChunk) + lane * ESZ;
+            const uint8_t* st = ring + (ch % kKmeanStages) * kKmeanChunk;
             const int rows = S - ch * ROWS < ROWS ? (int) (S - ch * ROWS) : ROWS;
-            // rows read in asm, 16 at a time and 16 rows ahead of the additions, with a wait tied to the values (the
-            // compiler would otherwise wait for every direct load in flight before a read of the ring). A bfloat16
-            // value is read into the high half of a register whose low half stays 0: the register is then the
-            // float32 value, and each row costs one read and one addition.
-            auto read16 = [&](uint32_t (&v)[16], uint32_t a) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    if constexpr (DT == H3S_BF16) asm volatile("ds_read_u16_d16_hi %0, %1 offset:%2" : "+v"(v[i]) : "v"(a), "i"(i * RB) : "memory");
-                    else if constexpr (ESZ == 2) asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v[i]) : "v"(a), "i"(i * RB) : "memory");
-                    else asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v[i]) : "v"(a), "i"(i * RB) : "memory");
-                }
-            };
-            auto wait16 = [&](uint32_t (&v)[16]) {
-                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
-                             "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]),
-                             "+v"(v[14]), "+v"(v[15]));
-            };
-            auto add16 = [&](const uint32_t (&v)[16]) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    float x;
-                    if constexpr (DT == H3S_F32 || DT == H3S_BF16) x = __uint_as_float(v[i]);
-                    else x = f16_lo(v[i]);
-                    sum = sum + x;
-                }
-            };
             const int full = rows / 16 * 16;
-            uint32_t va[16], vb[16];
+            float va[16], vb[16];
+            if (full > 0)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) va[i] = vb[i] = 0u;        // the low halves the bfloat16 reads keep
-            if (full > 0) {
-                read16(va, at);
-                wait16(va);
-            }
-            int r = 0;
-            for (; r < full; r += 32) {
+                for (int i = 0; i < 16; ++i) va[i] = at(st, i);
+            for (int r = 0; r < full; r += 32) {
                 const bool b1 = r + 16 < full, b2 = r + 32 < full;
-                if (b1) read16(vb, at + (r + 16) * RB);
-                add16(va);
+                if (b1)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) vb[i] = at(st, r + 16 + i);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sum = sum + va[i];
                 if (b1) {
-                    wait16(vb);
-                    if (b2) read16(va, at + (r + 32) * RB);
-                    add16(vb);
-                    if (b2) wait16(va);
+                    if (b2)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) va[i] = at(st, r + 32 + i);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) sum = sum + vb[i];
                 }
             }
-            r = full;
-            for (; r < rows; ++r) {
-                const uint8_t* e = ring + (ch % kKmeanStages) * kKmeanChunk + r * RB + lane * ESZ;
-                uint32_t v;
-                if constexpr (ESZ == 2) asm volatile("ds_read_u16 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"((uint32_t) (uintptr_t) e) : "memory");
-                else asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"((uint32_t) (uintptr_t) e) : "memory");
-                float x;
-                if constexpr (DT == H3S_F32) x = __uint_as_float(v);
-                else if constexpr (DT == H3S_BF16) x = bf16_lo(v);
-                else x = f16_lo(v);
-                sum = sum + x;
-            }
+            for (int r = full; r < rows; ++r) sum = sum + at(st, r);
         }
     }
     if (wave == 0 && lane < kKmeanFeat) mean[c0 + lane] = sum / (float) S;
