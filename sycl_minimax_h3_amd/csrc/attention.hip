@@ -54,10 +54,10 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
     const int64_t Sp = (S + kAttnQBlock - 1) / kAttnQBlock * kAttnQBlock, nbp = Sp / kAttnRows;
     const int64_t esz = sage ? 1 : 2;
     if (Hq * (Sp / kAttnQBlock) > 0x7fffffff) return fail(std::string(fn) + ": too many query blocks");
-    int8_t* aq = c->grow(c->aq, c->aq_cap, (size_t) (Sp * Hq * D * esz));
-    int8_t* ak = c->grow(c->ak, c->ak_cap, (size_t) (Sp * Hkv * D * esz));
-    uint16_t* av = c->grow(c->av, c->av_cap, (size_t) (Sp * Hkv * D));
-    float* af = c->grow(c->af, c->af_cap, (size_t) ((Hq + Hkv) * nbp + Hkv * D));
+    int8_t* aq = c->scratch<int8_t>(Ctx::ATT_Q, (size_t) (Sp * Hq * D * esz));
+    int8_t* ak = c->scratch<int8_t>(Ctx::ATT_K, (size_t) (Sp * Hkv * D * esz));
+    uint16_t* av = c->scratch<uint16_t>(Ctx::ATT_V, (size_t) (Sp * Hkv * D));
+    float* af = c->scratch<float>(Ctx::ATT_AUX, (size_t) ((Hq + Hkv) * nbp + Hkv * D));
     if (!aq || !ak || !av || !af) return -1;
     float *qs = af, *ks = af + Hq * nbp, *km = af + (Hq + Hkv) * nbp;
     switch (dt) {

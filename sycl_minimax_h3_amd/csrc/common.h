@@ -9,6 +9,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/h3hip.h"
 
@@ -22,6 +23,28 @@ namespace h3 {
 void set_error(const std::string& msg);
 int fail(const std::string& msg);          // sets the message, returns -1
 
+// The device memory one context answers for. A single budget - H3S_MEM_FRACTION of the card, 0.94 unless set (the
+// reference's cap, kernels/h3sycl.cpp:221-224) - covers the caller's buffers (h3s_alloc) and the library's scratch
+// regions together. A request that would pass it is refused with the numbers before the driver is asked. Thread-safe.
+class Budget {
+  public:
+    void set_limit(size_t bytes) { std::lock_guard<std::mutex> l(mu_); limit_ = bytes; }
+    size_t limit() const { std::lock_guard<std::mutex> l(mu_); return limit_; }
+    size_t in_use() const { std::lock_guard<std::mutex> l(mu_); return in_use_; }
+    // counts `bytes` more for `what` when they fit; else false, with the refusal as this thread's error
+    bool take(size_t bytes, const std::string& what);
+    void give_back(size_t bytes) { std::lock_guard<std::mutex> l(mu_); in_use_ -= bytes < in_use_ ? bytes : in_use_; }
+    // the caller's buffers: remembered with their size, forgotten (and their bytes given back) when freed
+    void remember(void* p, size_t bytes) { std::lock_guard<std::mutex> l(mu_); buffers_[p] = bytes; }
+    bool forget(void* p);                               // false when p is not one of the caller's buffers
+    std::vector<void*> buffers() const;
+
+  private:
+    mutable std::mutex mu_;
+    size_t limit_ = 0, in_use_ = 0;
+    std::unordered_map<void*, size_t> buffers_;
+};
+
 struct Ctx {
     int device = 0;
     hipStream_t stream = nullptr;          // kernels run here, in call order
@@ -31,27 +54,28 @@ struct Ctx {
     std::string name;
     int cus = 256;                         // compute units of the device (persistent grids are sized by them)
     bool poison = false;                   // H3S_POISON: fresh buffers filled with 0xff bytes
-    // the allocation book (kernels/h3sycl.cpp:149-151): allocations and scratch counted against one cap
-    std::mutex mem_mu;
-    std::unordered_map<void*, size_t> mem;
-    size_t mem_used = 0, mem_cap = 0;
-    // scratch of h3s_int8_linear: the int8 activations and the row scales of one row chunk
-    int8_t* xq = nullptr; size_t xq_cap = 0;
-    float* rs = nullptr; size_t rs_cap = 0;
-    // scratch of h3s_attention: q and k prepared [H, Sp, D] (int8 or half), v as half [H, D, Sp], the scales and k's mean
-    int8_t* aq = nullptr; size_t aq_cap = 0;
-    int8_t* ak = nullptr; size_t ak_cap = 0;
-    uint16_t* av = nullptr; size_t av_cap = 0;
-    float* af = nullptr; size_t af_cap = 0;
-    // h3s_linear / h3s_linear_acc: the rocBLAS handle (on this context's stream) and the float32 product of a row chunk
-    void* blas = nullptr;
-    float* lin = nullptr; size_t lin_cap = 0;
+    Budget budget;
+    // The library's scratch: one region per use, kept across calls and grown when a call needs more.
+    enum Region {
+        LIN_CODES,   // h3s_int8_linear: the int8 rows of a row chunk
+        LIN_SCALES,  //   and their row scales
+        ATT_Q,       // h3s_attention: q prepared [H, Sp, D] (int8 or half)
+        ATT_K,       //   k prepared
+        ATT_V,       //   v as half, transposed [H, D, Sp]
+        ATT_AUX,     //   the block scales and k's mean
+        LIN_F32,     // h3s_linear / h3s_linear_acc: the float32 product of a row chunk
+        N_REGIONS
+    };
+    struct Area { void* p = nullptr; size_t bytes = 0; };
+    Area areas[N_REGIONS];
+    void* blas = nullptr;                  // h3s_linear: the rocBLAS handle, on this context's stream
     bool sage_want = true;                 // H3S_ATTN=onednn: false
     int64_t sage_min_s = 8192;             // H3S_SAGE_MIN_S
     int64_t quant_wave_min = 8192;         // H3S_QUANT_WAVE_MIN_ROWS: fewest rows for the one-wavefront-a-row quantizer
 
-    // A scratch buffer of at least n elements, counted against the cap; NULL with the reason on failure.
-    template <typename T> T* grow(T*& p, size_t& cap, size_t n);
+    // region r with room for at least `bytes`; NULL, with the reason as this thread's error, when it cannot grow
+    void* scratch_bytes(Region r, size_t bytes);
+    template <typename T> T* scratch(Region r, size_t n) { return static_cast<T*>(scratch_bytes(r, n * sizeof(T))); }
 };
 
 // the context of an entry point: NULL with an error when ctx is NULL; makes its device current
@@ -69,30 +93,6 @@ inline bool aligned16(const void* p) { return ((uintptr_t) p & 15) == 0; }
 inline int elem_size(int dt) { return dt == H3S_F32 ? 4 : 2; }
 inline bool dt_ok(int dt) { return dt == H3S_F32 || dt == H3S_F16 || dt == H3S_BF16; }
 inline int vec_of(int dt) { return 16 / elem_size(dt); }   // elements in one 16-byte vector
-
-template <typename T> T* Ctx::grow(T*& p, size_t& cap, size_t n) {
-    if (n <= cap) return p;
-    const size_t want = n + (n >> 3);
-    std::lock_guard<std::mutex> l(mem_mu);
-    if (mem_used - cap * sizeof(T) + want * sizeof(T) > mem_cap) {
-        set_error("a scratch buffer of " + std::to_string((want * sizeof(T)) >> 20) + " MiB would pass the device memory cap (" +
-                  std::to_string(mem_used >> 20) + " of " + std::to_string(mem_cap >> 20) + " MiB in use)");
-        return nullptr;
-    }
-    if (p) { (void) hipStreamSynchronize(stream); (void) hipFree(p); }
-    mem_used -= cap * sizeof(T);
-    cap = 0;
-    void* q = nullptr;
-    if (hipMalloc(&q, want * sizeof(T)) != hipSuccess) {
-        p = nullptr;
-        set_error("the device refused a scratch buffer of " + std::to_string((want * sizeof(T)) >> 20) + " MiB");
-        return nullptr;
-    }
-    p = (T*) q;
-    cap = want;
-    mem_used += cap * sizeof(T);
-    return p;
-}
 
 // ---- device side -----------------------------------------------------------------------------------------------
 

@@ -1,6 +1,6 @@
 // int8_gemm.hip - the entry points of the int8 GEMM (kernel: gemm_impl.h): h3s_int8_gemm_dequant (quantized rows in,
-// dequant + bias + activation epilogue) and h3s_int8_linear (kernels/h3sycl.cpp:633-652: the quantizer, then the
-// GEMM, a chunk of rows at a time).
+// dequant + bias + activation epilogue) and h3s_int8_linear (kernels/h3sycl.cpp:633-652: the quantizer, then the GEMM,
+// a chunk of rows at a time, the quantized rows in the context's scratch).
 #include "gemm_impl.h"
 
 namespace h3 {
@@ -50,29 +50,50 @@ H3S_EXPORT int h3s_int8_gemm_dequant(void* ctx, const int8_t* q, const float* s,
     return launch_gemm(c, "h3s_int8_gemm_dequant", q, s, M, K, w, N, wscale, n_wscale, bias, act, out, out_dt);
 } catch (const std::exception& e) { return fail(e.what()); }
 
-H3S_EXPORT int h3s_int8_linear(void* ctx, const void* x, int x_dt, int64_t M, int64_t K, const int8_t* w, int64_t N,
-                               const float* wscale, int64_t n_wscale, const float* bias, void* out, int out_dt, int group) try {
-    if (M <= 0 || K <= 0 || N <= 0) return 0;
+namespace h3 {
+
+// the checks both int8 linear entry points share; 0 or -1 with the reason
+static int linear_checks(const char* fn, const void* x, int x_dt, int64_t K, int64_t N, const int8_t* w, int64_t n_wscale,
+                         void* out, int out_dt, int group) {
     // kernels/h3sycl.h:83: the group is 0 or a power of 4, at most 256, dividing K
     if (group < 0 || (group > 0 && (group > 256 || K % group != 0 || (group & (group - 1)) != 0 || (__builtin_ctz((unsigned) group) & 1))))
-        return fail("h3s_int8_linear: unsupported ConvRot group size (0, or a power of 4 at most 256 dividing K)");
-    if (!dt_ok(x_dt)) return fail("h3s_int8_linear: unknown element type");
-    if (gemm_checks("h3s_int8_linear", K, N, n_wscale, out_dt, x, w, out)) return -1;
-    Ctx* c = ctx_of(ctx, "h3s_int8_linear");
-    if (!c) return -1;
-    // the quantized rows and their scales, a chunk of rows at a time (kernels/h3sycl.cpp:640-651)
-    constexpr int64_t kRows = 65536;
-    const int64_t rows = M < kRows ? M : kRows;
-    int8_t* xq = c->grow(c->xq, c->xq_cap, (size_t) (rows * K));
-    float* rs = c->grow(c->rs, c->rs_cap, (size_t) rows);
-    if (!xq || !rs) return -1;
+        return fail(std::string(fn) + ": unsupported ConvRot group size (0, or a power of 4 at most 256 dividing K)");
+    if (!dt_ok(x_dt)) return fail(std::string(fn) + ": unknown element type");
+    return gemm_checks(fn, K, N, n_wscale, out_dt, x, w, out);
+}
+
+// the quantizer, then the GEMM, rows at a time into xq [rows, K] and rs [rows]
+static int linear_chunks(Ctx* c, const char* fn, const void* x, int x_dt, int64_t M, int64_t K, const int8_t* w, int64_t N,
+                         const float* wscale, int64_t n_wscale, const float* bias, void* out, int out_dt, int group, int8_t* xq,
+                         float* rs, int64_t rows) {
     const size_t xe = (size_t) elem_size(x_dt), oe = (size_t) elem_size(out_dt);
-    for (int64_t r0 = 0; r0 < M; r0 += kRows) {
-        const int64_t n = M - r0 < kRows ? M - r0 : kRows;
+    for (int64_t r0 = 0; r0 < M; r0 += rows) {
+        const int64_t n = M - r0 < rows ? M - r0 : rows;
         if (launch_quantize(c, (const char*) x + (size_t) (r0 * K) * xe, x_dt, n, K, group, xq, rs)) return -1;
-        if (launch_gemm(c, "h3s_int8_linear", xq, rs, n, K, w, N, wscale, n_wscale, bias, H3S_ACT_NONE,
-                        (char*) out + (size_t) (r0 * N) * oe, out_dt))
+        if (launch_gemm(c, fn, xq, rs, n, K, w, N, wscale, n_wscale, bias, H3S_ACT_NONE, (char*) out + (size_t) (r0 * N) * oe,
+                        out_dt))
             return -1;
     }
     return 0;
+}
+
+}  // namespace h3
+
+using namespace h3;
+
+H3S_EXPORT int h3s_int8_linear(void* ctx, const void* x, int x_dt, int64_t M, int64_t K, const int8_t* w, int64_t N,
+                               const float* wscale, int64_t n_wscale, const float* bias, void* out, int out_dt, int group) try {
+    const char* fn = "h3s_int8_linear";
+    if (M <= 0 || K <= 0 || N <= 0) return 0;
+    if (linear_checks(fn, x, x_dt, K, N, w, n_wscale, out, out_dt, group)) return -1;
+    Ctx* c = ctx_of(ctx, fn);
+    if (!c) return -1;
+    // the quantized rows and their scales in the context's scratch, a chunk of rows at a time
+    // (kernels/h3sycl.cpp:640-651)
+    constexpr int64_t kRows = 65536;
+    const int64_t rows = M < kRows ? M : kRows;
+    int8_t* xq = c->scratch<int8_t>(Ctx::LIN_CODES, (size_t) (rows * K));
+    float* rs = c->scratch<float>(Ctx::LIN_SCALES, (size_t) rows);
+    if (!xq || !rs) return -1;
+    return linear_chunks(c, fn, x, x_dt, M, K, w, N, wscale, n_wscale, bias, out, out_dt, group, xq, rs, rows);
 } catch (const std::exception& e) { return fail(e.what()); }

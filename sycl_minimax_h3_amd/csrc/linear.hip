@@ -89,7 +89,7 @@ static int linear(Ctx* c, const char* fn, const void* x, int dt, int64_t M, int6
     int64_t rows = (int64_t) (256 << 20) / (N * 4);
     rows = rows < 1 ? 1 : rows > 8192 ? 8192 : rows;
     rows = rows < M ? rows : M;
-    float* tmp = c->grow(c->lin, c->lin_cap, (size_t) (rows * N));
+    float* tmp = c->scratch<float>(Ctx::LIN_F32, (size_t) (rows * N));
     if (!tmp) return -1;
     const size_t xe = (size_t) elem_size(dt), oe = (size_t) elem_size(out_dt);
     const float one = 1.0f, zero = 0.0f;

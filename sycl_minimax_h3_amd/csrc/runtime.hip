@@ -44,6 +44,76 @@ int launched(const char* fn) {
     return 0;
 }
 
+static std::string mib(size_t bytes) { return std::to_string((bytes + (1 << 20) - 1) >> 20) + " MiB"; }
+
+bool Budget::take(size_t bytes, const std::string& what) {
+    std::lock_guard<std::mutex> l(mu_);
+    if (in_use_ <= limit_ && bytes <= limit_ - in_use_) {
+        in_use_ += bytes;
+        return true;
+    }
+    set_error(what + ": " + mib(bytes) + " more would exceed this context's device memory budget (" + mib(in_use_) +
+              " of " + mib(limit_) + " taken; H3S_MEM_FRACTION sets the budget)");
+    return false;
+}
+
+bool Budget::forget(void* p) {
+    std::lock_guard<std::mutex> l(mu_);
+    const auto it = buffers_.find(p);
+    if (it == buffers_.end()) return false;
+    in_use_ -= it->second < in_use_ ? it->second : in_use_;
+    buffers_.erase(it);
+    return true;
+}
+
+std::vector<void*> Budget::buffers() const {
+    std::lock_guard<std::mutex> l(mu_);
+    std::vector<void*> out;
+    for (const auto& kv : buffers_) out.push_back(kv.first);
+    return out;
+}
+
+static const char* region_name(Ctx::Region r) {
+    switch (r) {
+        case Ctx::LIN_CODES: return "int8 linear scratch (quantized rows)";
+        case Ctx::LIN_SCALES: return "int8 linear scratch (row scales)";
+        case Ctx::ATT_Q: return "attention scratch (q)";
+        case Ctx::ATT_K: return "attention scratch (k)";
+        case Ctx::ATT_V: return "attention scratch (v)";
+        case Ctx::ATT_AUX: return "attention scratch (scales and k's mean)";
+        case Ctx::LIN_F32: return "linear scratch (float32 product)";
+        default: return "scratch";
+    }
+}
+
+// Regions grow to whole 2 MiB granules (the device's allocation granule for large buffers), so a region that needs a
+// few more rows than last time is not reallocated at every call. The old region goes first, once the queued kernels
+// that may use it are done, so the budget never holds both.
+void* Ctx::scratch_bytes(Region r, size_t bytes) {
+    constexpr size_t kGranule = (size_t) 2 << 20;
+    Area& a = areas[r];
+    if (bytes <= a.bytes) return a.p;
+    const size_t want = (bytes + kGranule - 1) / kGranule * kGranule;
+    if (a.p) {
+        (void) hipStreamSynchronize(stream);
+        (void) hipFree(a.p);
+        budget.give_back(a.bytes);
+        a = Area{};
+    }
+    if (!budget.take(want, region_name(r))) return nullptr;
+    void* p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess || !p) {
+        (void) hipGetLastError();
+        budget.give_back(want);
+        set_error(std::string(region_name(r)) + ": hipMalloc of " + mib(want) + " failed");
+        return nullptr;
+    }
+    if (poison) (void) hipMemsetAsync(p, 0xff, want, stream);
+    a.p = p;
+    a.bytes = want;
+    return p;
+}
+
 // what every way of making a context shares: the device's name and the memory cap (kernels/h3sycl.cpp:216-235)
 static void init(Ctx& c) {
     hipDeviceProp_t p;
@@ -56,7 +126,7 @@ static void init(Ctx& c) {
     (void) hipMemGetInfo(&free_b, &total);
     double frac = 0.94;
     if (const char* e = std::getenv("H3S_MEM_FRACTION")) frac = std::min(0.97, std::max(0.05, std::atof(e)));
-    c.mem_cap = (size_t) ((double) total * frac);
+    c.budget.set_limit((size_t) ((double) total * frac));
     c.poison = std::getenv("H3S_POISON") != nullptr;
     // the attention form (kernels/h3sycl.cpp:231-232): H3S_ATTN=onednn keeps every call on the 16-bit form;
     // H3S_SAGE_MIN_S sets the shortest sequence that takes the int8 (SageAttention) form
@@ -125,14 +195,9 @@ H3S_EXPORT void* h3s_stream(void* ctx) { return ctx ? static_cast<Ctx*>(ctx)->st
 
 H3S_EXPORT const char* h3s_device_name(void* ctx) { return ctx ? static_cast<Ctx*>(ctx)->name.c_str() : ""; }
 
-H3S_EXPORT uint64_t h3s_mem_cap(void* ctx) { return ctx ? static_cast<Ctx*>(ctx)->mem_cap : 0; }
+H3S_EXPORT uint64_t h3s_mem_cap(void* ctx) { return ctx ? static_cast<Ctx*>(ctx)->budget.limit() : 0; }
 
-H3S_EXPORT uint64_t h3s_mem_used(void* ctx) {
-    if (!ctx) return 0;
-    auto& c = *static_cast<Ctx*>(ctx);
-    std::lock_guard<std::mutex> l(c.mem_mu);
-    return c.mem_used;
-}
+H3S_EXPORT uint64_t h3s_mem_used(void* ctx) { return ctx ? static_cast<Ctx*>(ctx)->budget.in_use() : 0; }
 
 H3S_EXPORT uint64_t h3s_mem_free(void* ctx) {
     if (!ctx_of(ctx, "h3s_mem_free")) return 0;
@@ -140,41 +205,37 @@ H3S_EXPORT uint64_t h3s_mem_free(void* ctx) {
     return hipMemGetInfo(&free_b, &total) == hipSuccess ? free_b : 0;
 }
 
+// Device memory for the caller, counted against the context's budget. A zero-byte request still returns a distinct
+// buffer (one 256-byte allocation granule), so the pointer can be freed like any other.
 H3S_EXPORT void* h3s_alloc(void* ctx, uint64_t bytes) try {
     Ctx* c = ctx_of(ctx, "h3s_alloc");
     if (!c) return nullptr;
-    std::lock_guard<std::mutex> l(c->mem_mu);
-    if (c->mem_used + bytes > c->mem_cap) {
-        set_error("h3s_alloc: " + std::to_string(bytes >> 20) + " MiB would pass the device memory cap (" +
-                  std::to_string(c->mem_used >> 20) + " of " + std::to_string(c->mem_cap >> 20) + " MiB in use)");
-        return nullptr;
-    }
+    if (!c->budget.take(bytes, "h3s_alloc")) return nullptr;
     void* p = nullptr;
-    if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) {
-        set_error("h3s_alloc: the device refused " + std::to_string(bytes >> 20) + " MiB");
+    if (hipMalloc(&p, bytes ? bytes : 256) != hipSuccess || !p) {
+        (void) hipGetLastError();
+        c->budget.give_back(bytes);
+        set_error("h3s_alloc: hipMalloc of " + mib(bytes) + " failed");
         return nullptr;
     }
-    if (c->poison && hipMemset(p, 0xff, bytes ? bytes : 1) != hipSuccess) {
+    if (c->poison && hipMemset(p, 0xff, bytes ? bytes : 256) != hipSuccess) {
         (void) hipFree(p);
-        set_error("h3s_alloc: poisoning the buffer failed");
+        c->budget.give_back(bytes);
+        set_error("h3s_alloc: filling the new buffer with 0xff (H3S_POISON) failed");
         return nullptr;
     }
-    c->mem.emplace(p, bytes);
-    c->mem_used += bytes;
+    c->budget.remember(p, bytes);
     return p;
 } catch (const std::exception& e) { set_error(e.what()); return nullptr; }
 
+// Frees a buffer of h3s_alloc once the work queued on the context (kernels and uploads) is done with it; any other
+// pointer is left alone.
 H3S_EXPORT void h3s_free(void* ctx, void* p) {
     Ctx* c = ctx_of(ctx, "h3s_free");
     if (!c || !p) return;
-    (void) hipStreamSynchronize(c->stream);          // nothing queued may still read or write it
+    (void) hipStreamSynchronize(c->stream);
     if (c->copy_stream) (void) hipStreamSynchronize(c->copy_stream);
-    std::lock_guard<std::mutex> l(c->mem_mu);
-    auto it = c->mem.find(p);
-    if (it == c->mem.end()) return;
-    c->mem_used -= it->second;
-    c->mem.erase(it);
-    (void) hipFree(p);
+    if (c->budget.forget(p)) (void) hipFree(p);
 }
 
 H3S_EXPORT int h3s_write(void* ctx, void* dst, const void* src_host, uint64_t bytes) {
@@ -261,12 +322,10 @@ H3S_EXPORT void h3s_destroy(void* ctx) {
     (void) hipSetDevice(c->device);
     (void) hipStreamSynchronize(c->stream);
     if (c->copy_stream) { (void) hipStreamSynchronize(c->copy_stream); (void) hipStreamDestroy(c->copy_stream); }
-    if (c->xq) (void) hipFree(c->xq);
-    if (c->rs) (void) hipFree(c->rs);
-    for (void* p : {(void*) c->aq, (void*) c->ak, (void*) c->av, (void*) c->af, (void*) c->lin})
-        if (p) (void) hipFree(p);
+    for (auto& a : c->areas)
+        if (a.p) (void) hipFree(a.p);
     release_blas(c);
-    for (auto& kv : c->mem) (void) hipFree(kv.first);
+    for (void* p : c->budget.buffers()) (void) hipFree(p);
     if (c->own_stream) (void) hipStreamDestroy(c->stream);
     delete c;
 }

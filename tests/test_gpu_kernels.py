@@ -50,7 +50,8 @@ def test_context_and_memory(dev):
     dev.api.free_host(dev.ctx, p)
     # the cap refuses, with a message, instead of asking the driver
     assert not dev.api.alloc(dev.ctx, dev.mem_cap() + 1)
-    assert "cap" in dev.api.error()
+    assert "budget" in dev.api.error()
+    assert dev.mem_used() == used + 3 * a.size                      # the refused request took nothing
     assert dev.api.gpu_count() >= 1
     name = dev.name()
     assert name
