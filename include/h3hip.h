@@ -205,6 +205,15 @@ int h3s_qk_rms_rope(void* ctx, void* q, void* k, int x_dt, int64_t M, int64_t H,
 int h3s_int8_gemm_dequant(void* ctx, const int8_t* q, const float* s, int64_t M, int64_t K, const int8_t* w, int64_t N,
                           const float* wscale, int64_t n_wscale, const float* bias, int act, void* out, int out_dt);
 
+/* h3s_int8_linear without any allocation: no counterpart in the reference. For callers that cannot allocate device
+ * memory - code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. Same arguments and
+ * results as h3s_int8_linear; the quantized rows go into a fixed device array of the library (64 MiB of codes and
+ * 65536 row scales, held on each GPU the library runs on until the process ends) instead of the context's scratch.
+ * Any M (rows go through in chunks that fit the array); K at most 65536, else -1 with the reason. Calls on one GPU
+ * share its array: calls that overlap on one GPU (two streams or two contexts at once) race. */
+int h3s_int8_linear_noalloc(void* ctx, const void* x, int x_dt, int64_t M, int64_t K, const int8_t* w, int64_t N,
+                            const float* wscale, int64_t n_wscale, const float* bias, void* out, int out_dt, int group);
+
 #ifdef __cplusplus
 }
 #endif

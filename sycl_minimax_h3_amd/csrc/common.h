@@ -85,6 +85,9 @@ int launched(const char* fn);
 
 // frees the context's rocBLAS handle, if it has one (linear.hip)
 void release_blas(Ctx* c);
+// looks up, once per device, the device address of h3s_int8_linear_noalloc's fixed scratch (int8_gemm.hip); the
+// device must be current. 0, or -1 when the lookup failed (the entry point then reports why).
+int noalloc_setup(int device);
 
 // the quantizer of h3s_int8_linear (rownorm.hip): x [M, K] -> regular rotation per group (0: none) -> q, s
 int launch_quantize(Ctx* c, const void* x, int x_dt, int64_t M, int64_t K, int group, int8_t* q, float* s);

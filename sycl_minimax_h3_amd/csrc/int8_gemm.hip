@@ -1,9 +1,49 @@
 // int8_gemm.hip - the entry points of the int8 GEMM (kernel: gemm_impl.h): h3s_int8_gemm_dequant (quantized rows in,
-// dequant + bias + activation epilogue) and h3s_int8_linear (kernels/h3sycl.cpp:633-652: the quantizer, then the GEMM,
-// a chunk of rows at a time, the quantized rows in the context's scratch).
+// dequant + bias + activation epilogue), h3s_int8_linear (kernels/h3sycl.cpp:633-652: the quantizer, then the GEMM, a
+// chunk of rows at a time, the quantized rows in the context's scratch) and h3s_int8_linear_noalloc (the same, the
+// quantized rows in a fixed device array, for callers that cannot allocate).
+#include <map>
+
 #include "gemm_impl.h"
 
 namespace h3 {
+
+// ---- the fixed scratch of h3s_int8_linear_noalloc ----
+// int8 codes of one row chunk (64 MiB), then the chunk's float32 row scales. Each device the library runs on holds
+// its own copy until the process ends. Host code never hands the array's name to a kernel: in host code it stands for
+// no device address. Its address on each device is looked up once (noalloc_setup, at context creation).
+constexpr size_t kScratchCodes = (size_t) 64 << 20;
+constexpr int64_t kScratchRows = 65536;
+constexpr int64_t kScratchMaxK = 65536;             // features a row: every chunk then holds at least 1024 rows
+static __device__ __align__(256) int8_t scratch[kScratchCodes + kScratchRows * sizeof(float)];
+
+static std::mutex g_scratch_mu;
+static std::map<int, void*> g_scratch_at;           // device -> the array's address there
+static std::map<int, std::string> g_scratch_err;    // device -> why the lookup failed
+
+int noalloc_setup(int device) {
+    std::lock_guard<std::mutex> l(g_scratch_mu);
+    if (g_scratch_at.count(device) || g_scratch_err.count(device)) return g_scratch_at.count(device) ? 0 : -1;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        (void) hipGetLastError();
+        g_scratch_err[device] = std::string("the address of the fixed scratch on GPU ") + std::to_string(device) +
+                                " could not be found: " + hipGetErrorString(e);
+        return -1;
+    }
+    g_scratch_at[device] = p;
+    return 0;
+}
+
+static void* scratch_on(int device, std::string& why) {
+    std::lock_guard<std::mutex> l(g_scratch_mu);
+    const auto it = g_scratch_at.find(device);
+    if (it != g_scratch_at.end()) return it->second;
+    const auto er = g_scratch_err.find(device);
+    why = er != g_scratch_err.end() ? er->second : "the fixed scratch was not set up on GPU " + std::to_string(device);
+    return nullptr;
+}
 
 int launch_gemm(Ctx* c, const char* fn, const int8_t* q, const float* s, int64_t M, int64_t K, const int8_t* w, int64_t N,
                 const float* wscale, int64_t n_wscale, const float* bias, int act_, void* out, int out_dt) {
@@ -96,4 +136,27 @@ H3S_EXPORT int h3s_int8_linear(void* ctx, const void* x, int x_dt, int64_t M, in
     float* rs = c->scratch<float>(Ctx::LIN_SCALES, (size_t) rows);
     if (!xq || !rs) return -1;
     return linear_chunks(c, fn, x, x_dt, M, K, w, N, wscale, n_wscale, bias, out, out_dt, group, xq, rs, rows);
+} catch (const std::exception& e) { return fail(e.what()); }
+
+// h3s_int8_linear with the quantized rows in the fixed device array: no allocation, any M (in chunks of at most
+// 65536 rows and 64 MiB of codes), K at most 65536. Calls on one GPU share its array: calls that overlap on one GPU
+// (two streams, two contexts) race.
+H3S_EXPORT int h3s_int8_linear_noalloc(void* ctx, const void* x, int x_dt, int64_t M, int64_t K, const int8_t* w, int64_t N,
+                                       const float* wscale, int64_t n_wscale, const float* bias, void* out, int out_dt,
+                                       int group) try {
+    const char* fn = "h3s_int8_linear_noalloc";
+    if (M <= 0 || K <= 0 || N <= 0) return 0;
+    if (K > kScratchMaxK)
+        return fail(std::string(fn) + ": rows of " + std::to_string(K) + " features pass the fixed scratch's limit of " +
+                    std::to_string(kScratchMaxK));
+    if (linear_checks(fn, x, x_dt, K, N, w, n_wscale, out, out_dt, group)) return -1;
+    Ctx* c = ctx_of(ctx, fn);
+    if (!c) return -1;
+    std::string why;
+    char* base = static_cast<char*>(scratch_on(c->device, why));
+    if (!base) return fail(std::string(fn) + ": " + why);
+    const int64_t by_codes = (int64_t) (kScratchCodes / (size_t) K);
+    const int64_t rows = by_codes < kScratchRows ? by_codes : kScratchRows;
+    return linear_chunks(c, fn, x, x_dt, M, K, w, N, wscale, n_wscale, bias, out, out_dt, group, reinterpret_cast<int8_t*>(base),
+                         reinterpret_cast<float*>(base + kScratchCodes), rows);
 } catch (const std::exception& e) { return fail(e.what()); }

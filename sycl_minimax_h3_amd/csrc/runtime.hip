@@ -128,6 +128,9 @@ static void init(Ctx& c) {
     if (const char* e = std::getenv("H3S_MEM_FRACTION")) frac = std::min(0.97, std::max(0.05, std::atof(e)));
     c.budget.set_limit((size_t) ((double) total * frac));
     c.poison = std::getenv("H3S_POISON") != nullptr;
+    // h3s_int8_linear_noalloc's fixed scratch: its address on this device, looked up once (a failure is reported by
+    // that entry point, not here)
+    (void) noalloc_setup(c.device);
     // the attention form (kernels/h3sycl.cpp:231-232): H3S_ATTN=onednn keeps every call on the 16-bit form;
     // H3S_SAGE_MIN_S sets the shortest sequence that takes the int8 (SageAttention) form
     if (const char* e = std::getenv("H3S_ATTN")) c.sage_want = std::strcmp(e, "onednn") != 0;

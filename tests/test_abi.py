@@ -31,7 +31,7 @@ def declared():
 
 def test_header_and_library_agree(api):
     names = declared()
-    assert len(names) == 57          # the 49 of kernels/h3sycl.h and the 8 additions
+    assert len(names) == 58          # the 49 of kernels/h3sycl.h, the 8 fused additions, the allocation-free int8 linear
     out = subprocess.run(["nm", "-D", "--defined-only", api.path], capture_output=True, text=True, check=True).stdout
     exported = sorted(set(l.split()[-1] for l in out.splitlines() if l.split()[-1].startswith("h3s_")))
     assert exported == names, f"missing {set(names) - set(exported)}, extra {set(exported) - set(names)}"
@@ -63,6 +63,11 @@ def test_arguments_are_checked_before_the_device(api):
     assert "multiple of 64" in api.error()
     assert api.int8_linear(None, p, 2, 8, 256, p, 8, p, 3, None, p, 2, 0) == -1
     assert "weight scales" in api.error()
+    # the allocation-free int8 linear refuses rows longer than its fixed scratch takes, before the device
+    assert api.int8_linear_noalloc(None, p, 2, 8, 131072, p, 8, p, 1, None, p, 2, 0) == -1
+    assert "65536" in api.error()
+    assert api.int8_linear_noalloc(None, p, 2, 8, 256, p, 8, p, 1, None, p, 2, 128) == -1
+    assert "group" in api.error()
     assert api.rms_rope(None, p, 2, 4, 32, 128, 4096, p, 1e-5, p, 127) == -1
     assert "rot_dim" in api.error()
     assert api.rms_rope(None, p, 2, 4, 32, 128, 4000, p, 1e-5, p, 128) == -1
