@@ -1,24 +1,43 @@
 """Benchmark of the fused per-token layer kernels on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only k1,k2] [--mark] [--copy-probe]
+    python bench.py --summarize-trace TRACE.csv --bench-json BENCH.json           (a profiles/ table, see below)
+    python bench.py --summarize-pmc COUNTERS.csv [COUNTERS2.csv] --bench-json BENCH.json
 
-A step is one launch of the headline kernel over the whole batch: the AdaLN chain (LayerNorm without affine, then x
-* (1 + scale) + shift, GELU-tanh, out = res + gate * y) on X, res [16896 x 4096] bf16, token grid T16 x H24 x W44.
+A step is one launch of the headline kernel over the whole batch: the AdaLN chain (LayerNorm without affine, then
+x * (1 + scale) + shift, GELU-tanh, out = res + gate * y) on X, res [16896 x 4096] bf16, token grid T16 x H24 x W44.
 ``value`` is its achieved HBM bandwidth: algorithmic bytes (X and res read once, out written once) divided by the
-mean kernel time. Each kernel first runs untimed for 0.15 s (``--settle``; the clocks ramp up over the first
-milliseconds of load), then W warm-up launches, then the K timed launches. The library context wraps PyTorch's
-current stream (h3s_create), so the kernels run on that stream and the HIP events recorded on it (torch.cuda.Event)
-bracket exactly the timed launches; inputs are already in HBM. The other fused kernels are timed the same way and
-reported under ``kernels``; the int8 GEMM also as int8 TOPS. ``roofline.traffic`` is the headline kernel's HBM bytes
-per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarized in profiles/hbm_traffic_pmc.md (each counter
-scaled by what it reads for a 1 GiB device copy). ``cpu_baseline`` times the CPU oracle (the C restatement of the
-reference arithmetic) on the same workload on this host. Prints one JSON line.
+mean launch time.
+
+Cache-cold timing: MI355X's 256 MB Infinity Cache would hold part of a 415 MB working set launched back to back on
+the same buffers. Every workload of less than 1 GiB per launch is therefore timed over a ring of independent buffer
+sets whose footprint is at least 1 GiB (3 sets for the headline), one set per launch in turn: a launch never finds
+its inputs in the cache. The headline's back-to-back figure on one set is reported beside it.
+
+Each kernel first runs untimed for 0.15 s (``--settle``; the clocks ramp up over the first milliseconds of load), then
+W warm-up launches, then the K timed launches, bracketed by HIP events on the stream the kernels run on (the library
+context wraps PyTorch's current stream, h3s_create). Inputs are already in HBM. The other fused kernels are timed the
+same way and reported under ``kernels``; the int8 GEMM also as int8 TOPS and attention against the mixed
+int8 / fp16 matrix peak. ``roofline.traffic`` is the headline kernel's HBM bytes per launch from the rocprofv3
+FETCH_SIZE / WRITE_SIZE runs summarized in profiles/hbm_traffic_pmc.md (each counter scaled by what it reads for a
+1 GiB device copy). ``cpu_baseline`` times the CPU oracle (the C restatement of the reference arithmetic) on the same
+workload on this host.
+
+``--mark`` launches a one-cycle spin kernel right before and right after each timed region (outside its HIP
+events), so a rocprofv3 trace of the run can be cut into exactly the timed dispatches of each workload; the bench
+line then lists the marked workloads in order. ``--summarize-trace`` and ``--summarize-pmc`` turn such a trace
+(kernel trace or counter collection, rocprofv3 ``-f csv``) and the bench line of the same run into the tables
+committed under profiles/. Prints one JSON line.
 """
 from __future__ import annotations
 
 import argparse
+import collections
+import csv
 import json
+import math
 import os
+import re
 import sys
 import time
 
@@ -28,17 +47,21 @@ sys.path.insert(0, ROOT)
 PEAK_GBS = 8000.0          # MI355X HBM3E
 PEAK_I8_TOPS = 5000.0      # MI355X dense int8 matrix peak
 PEAK_F16_TFLOPS = 2500.0   # MI355X dense fp16 / bf16 matrix peak
+RING_BYTES = 1 << 30       # the least footprint of a ring of buffer sets (4x the Infinity Cache)
+MARKER = "spin_kernel"     # the kernel torch.cuda._sleep launches: the --mark boundaries
 
 M2 = 16 * 24 * 44          # 16896 tokens (T16 x H24 x W44)
 M4 = 47104
 C = 4096
+HEADLINE = "cfg2_ln_mod_gelu_gate_16896"
 
 
 def bytes_cfg():
     """Algorithmic bytes per launch (minimum HBM traffic: every input read once, every output written once)."""
     return {
+        HEADLINE: 3 * M2 * C * 2,
+        HEADLINE + "_same_buffers": 3 * M2 * C * 2,
         "cfg1_rmsnorm_quant_2159": 2159 * C * 2 + 2159 * C + 2159 * 4,
-        "cfg2_ln_mod_gelu_gate_16896": 3 * M2 * C * 2,
         "cfg3_qk_rmsnorm_rope3d_16896": 4 * M2 * 32 * 128 * 2 + M2 * 64 * 2 * 4,
         "cfg4_rmsnorm_wht128_quant_47104": M4 * C * 2 + M4 * C + M4 * 4,
         "cfg5a_rmsnorm_mod_quant_47104": M4 * C * 2 + M4 * C + M4 * 4,
@@ -51,20 +74,24 @@ def bytes_cfg():
         "cfg5a_rmsnorm_mod_quant_16896": M2 * C * 2 + M2 * C + M2 * 4,
         "attn_sage_16896x32x128": 4 * M2 * 4096 * 2,     # q, k, v read, out written (the products are the bound)
         "attn_sage_47104x32x128": 4 * M4 * 4096 * 2,
+        "copy_probe_1GiB": 2 << 30,
     }
 
 
+def ring_size(nbytes: int) -> int:
+    """Buffer sets of a ring whose footprint is at least RING_BYTES (one set when a launch moves that much)."""
+    return max(1, min(64, -(-RING_BYTES // nbytes)))
+
+
 def measured_traffic(key):
-    """HBM bytes per launch of kernel `key` from the committed counter summary, scaled by the copy calibration."""
+    """HBM bytes per launch of workload `key` from the committed counter summary, scaled by the copy calibration."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
     try:
         with open(path) as f:
             for line in f:
                 if line.startswith("traffic:") and line.split()[1] == key:
                     kv = dict(t.split("=") for t in line.split()[2:])
-                    cal_f = float(kv["copy_kib"]) / float(kv["copy_fetch_kib"])
-                    cal_w = float(kv["copy_kib"]) / float(kv["copy_write_kib"])
-                    return int(round((float(kv["fetch_kib"]) * cal_f + float(kv["write_kib"]) * cal_w) * 1024))
+                    return int(kv["bytes"])
     except (OSError, KeyError, ValueError):
         return None
     return None
@@ -85,6 +112,29 @@ def rope_table(T, Hh, Ww, dims=(32, 48, 48), theta=10000.0):
     return np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
 
 
+def cpu_share() -> dict:
+    """This host's CPUs as the process sees them: nproc, the affinity mask and the cgroup CPU quota (if any)."""
+    out = {"nproc": os.cpu_count() or 1}
+    try:
+        out["affinity"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        out["affinity"] = out["nproc"]
+    quota = None
+    try:
+        q, p = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = int(q) / int(p)
+    except (OSError, ValueError):
+        pass
+    out["cgroup_quota"] = quota
+    try:
+        with open("/proc/cpuinfo") as f:
+            out["model"] = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except Exception:
+        out["model"] = "unknown"
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -92,20 +142,30 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--settle", type=float, default=0.15, help="seconds each kernel runs untimed before its warm-up")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of kernel keys to time (default all)")
+    ap.add_argument("--only", default="", help="comma list of workload keys to time (default all)")
+    ap.add_argument("--mark", action="store_true", help="bracket each timed region with a spin-kernel marker")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also time a plain device copy of 1 GiB (the attainable HBM rate; the known-size kernel that "
                          "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--summarize-trace", default="", help="a rocprofv3 kernel trace csv of a --mark run: print a table")
+    ap.add_argument("--summarize-pmc", nargs="+", default=[], help="rocprofv3 counter csv(s) of --mark runs")
+    ap.add_argument("--bench-json", default="", help="the bench line of the profiled run (for --summarize-*)")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace, args.bench_json))
+        return 0
+    if args.summarize_pmc:
+        print(summarize_pmc(args.summarize_pmc, args.bench_json))
+        return 0
     if args.gpus != 1:
         print(f"bench.py: one GPU only; --gpus {args.gpus} is not supported (the per-token kernels would shard by "
               "contiguous token rows with no exchange step, so one GPU's share is the measured workload)", file=sys.stderr)
         return 2
 
-    import numpy as np
+    import numpy as np  # noqa: F401
     import torch
 
-    from sycl_minimax_h3_amd import Device, DType, Tensor, ops
+    from sycl_minimax_h3_amd import Device, Tensor, ops
     import sycl_minimax_h3_amd.api as A
 
     torch.manual_seed(0)
@@ -114,11 +174,12 @@ def main() -> int:
     T = lambda t, dt=None: Tensor.from_torch(t, dt, dev)   # noqa: E731
     B = bytes_cfg()
     only = set(filter(None, args.only.split(",")))
+    marked, steps_of = [], {}
 
     def bf16(*shape, scale=1.0):
         return (torch.randn(*shape, device=dev_t) * scale).to(torch.bfloat16)
 
-    def timed(fn, steps, warmup, settle_s=args.settle):
+    def timed(key, fn, steps, warmup, settle_s=args.settle):
         # The device's clocks ramp up over the first ~10 ms of sustained load: before the W warm-up launches, keep
         # launching (untimed) until settle_s seconds of this kernel have run, so the timed launches see the sustained
         # state a busy serving loop runs in.
@@ -130,114 +191,174 @@ def main() -> int:
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
+        steps_of[key] = steps
+        if args.mark:
+            torch.cuda._sleep(1)
+            marked.append(key)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(steps):
             fn()
         e1.record()
+        if args.mark:
+            torch.cuda._sleep(1)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps   # ms per launch
 
-    kernels = {}
+    def cycle(fns):
+        """one launch of the next buffer set of a ring"""
+        state = [0]
 
-    # ---- config 2 (headline): LN (no affine) -> * (1 + scale) + shift -> GELU-tanh -> res + gate * y ----
-    x2, r2, o2 = bf16(M2, C), bf16(M2, C), torch.empty(M2, C, dtype=torch.bfloat16, device=dev_t)
-    tab = [bf16(1, C, scale=0.5) for _ in range(3)]
-    tb2 = ops.Tables(scale=T(tab[0]), shift=T(tab[1]), gate=T(tab[2]))
-    X2, R2, O2 = T(x2), T(r2), T(o2)
-    f2 = lambda: ops.norm_mod_act_gate(X2, A.NORM_LAYER, None, None, 1e-5, tb2, A.ACT_GELU_TANH, R2, O2)  # noqa: E731
-    ms2 = timed(f2, args.steps, args.warmup)
-    kernels["cfg2_ln_mod_gelu_gate_16896"] = ms2
+        def f():
+            fns[state[0] % len(fns)]()
+            state[0] += 1
+        return f
 
-    def run(key, fn, steps=20):
+    kernels, rings = {}, {}
+
+    def run(key, make, steps=20, warmup=3):
+        """times workload `key`: make() builds one buffer set and returns its launch; a ring of them when small"""
         if only and key not in only:
             return
-        kernels[key] = timed(fn, steps, 3)
+        n = ring_size(B[key])
+        fns = [make() for _ in range(n)]
+        kernels[key] = timed(key, cycle(fns), steps, warmup)
+        rings[key] = n
+        del fns
+        torch.cuda.empty_cache()
+
+    # ---- config 2 (headline): LN (no affine) -> * (1 + scale) + shift -> GELU-tanh -> res + gate * y ----
+    tab = [bf16(1, C, scale=0.5) for _ in range(3)]
+    tb2 = ops.Tables(scale=T(tab[0]), shift=T(tab[1]), gate=T(tab[2]))
+    first = {}
+
+    def make2():
+        x, r, o = bf16(M2, C), bf16(M2, C), torch.empty(M2, C, dtype=torch.bfloat16, device=dev_t)
+        first.setdefault("x2", x)
+        first.setdefault("r2", r)
+        X, R, O = T(x), T(r), T(o)
+        return lambda: ops.norm_mod_act_gate(X, A.NORM_LAYER, None, None, 1e-5, tb2, A.ACT_GELU_TANH, R, O)
+
+    n2 = ring_size(B[HEADLINE])
+    ring2 = [make2() for _ in range(n2)]
+    ms2 = timed(HEADLINE, cycle(ring2), args.steps, args.warmup)
+    kernels[HEADLINE], rings[HEADLINE] = ms2, n2
+    # the same launches back to back on one buffer set: part of the 415 MB stays in the Infinity Cache
+    if not only or HEADLINE + "_same_buffers" in only:
+        kernels[HEADLINE + "_same_buffers"] = timed(HEADLINE + "_same_buffers", ring2[0], args.steps, args.warmup)
+        rings[HEADLINE + "_same_buffers"] = 1
+    del ring2
+    x2, r2 = first["x2"], first["r2"]
 
     # ---- config 1: RMSNorm (eps 1e-6) + per-token int8 quant, [2159 x 4096] ----
-    x1 = bf16(2159, C)
     g1 = (1 + 0.1 * torch.randn(C, device=dev_t)).float()
-    q1, s1 = torch.empty(2159, C, dtype=torch.int8, device=dev_t), torch.empty(2159, device=dev_t)
-    X1, G1, Q1, S1 = T(x1), T(g1), T(q1), T(s1)
-    run("cfg1_rmsnorm_quant_2159", lambda: ops.norm_quant(X1, G1, 1e-6, None, Q1, S1), 200)
+    G1 = T(g1)
+
+    def make1():
+        x = bf16(2159, C)
+        first.setdefault("x1", x)
+        X, Q, S = T(x), T(torch.empty(2159, C, dtype=torch.int8, device=dev_t)), T(torch.empty(2159, device=dev_t))
+        return lambda: ops.norm_quant(X, G1, 1e-6, None, Q, S)
+    run("cfg1_rmsnorm_quant_2159", make1, 200)
+    if "x1" not in first:
+        first["x1"] = bf16(2159, C)
 
     # ---- config 3: qk-RMSNorm + 3D RoPE in place, q, k [16896 x 32 x 128], split 32/48/48 ----
-    q3, k3 = bf16(M2, 32 * 128), bf16(M2, 32 * 128)
     wq, wk = (1 + 0.1 * torch.randn(128, device=dev_t)).float(), (1 + 0.1 * torch.randn(128, device=dev_t)).float()
+    WQ, WK = T(wq), T(wk)
     cs = torch.from_numpy(rope_table(16, 24, 44)).to(dev_t)
-    Q3, K3, WQ, WK, CS = T(q3), T(k3), T(wq), T(wk), T(cs)
-    run("cfg3_qk_rmsnorm_rope3d_16896", lambda: ops.qk_rms_rope(ops.Rows(Q3, 0, 4096, M2, 32, 128), ops.Rows(K3, 0, 4096, M2, 32, 128),
-                                                                 WQ, WK, 1e-5, CS, 128))
+    CS = T(cs)
 
-    # ---- config 4: RMSNorm -> Sylvester WHT-128 -> int8 quant, [47104 x 4096], 1% of channels x20 ----
+    def make3(M, csT):
+        def make():
+            q, k = bf16(M, 32 * 128), bf16(M, 32 * 128)
+            first.setdefault(f"q3_{M}", q)
+            first.setdefault(f"k3_{M}", k)
+            Qr, Kr = ops.Rows(T(q), 0, 4096, M, 32, 128), ops.Rows(T(k), 0, 4096, M, 32, 128)
+            return lambda: ops.qk_rms_rope(Qr, Kr, WQ, WK, 1e-5, csT, 128)
+        return make
+    run("cfg3_qk_rmsnorm_rope3d_16896", make3(M2, CS))
+
+    # ---- config 4: RMSNorm -> Sylvester WHT-128 -> int8 quant, 1% of channels x20 ----
     ch = torch.randperm(C, generator=torch.Generator().manual_seed(4))[:41].to(dev_t)
-    x4 = torch.randn(M4, C, device=dev_t)
-    x4[:, ch] *= 20
-    x4 = x4.to(torch.bfloat16)
-    q4, s4 = torch.empty(M4, C, dtype=torch.int8, device=dev_t), torch.empty(M4, device=dev_t)
-    X4, Q4, S4 = T(x4), T(q4), T(s4)
-    run("cfg4_rmsnorm_wht128_quant_47104", lambda: ops.norm_quant(X4, G1, 1e-6, None, Q4, S4, rot=A.ROT_SYLVESTER, group=128))
 
-    # ---- config 5a: RMSNorm + modulate + int8 quant, [47104 x 4096]; 5b: int8 GEMM + dequant + SiLU ----
-    x5 = bf16(M4, C)
+    def make4(M):
+        def make():
+            x = torch.randn(M, C, device=dev_t)
+            x[:, ch] *= 20
+            x = x.to(torch.bfloat16)
+            first.setdefault(f"x4_{M}", x)
+            X, Q, S = T(x), T(torch.empty(M, C, dtype=torch.int8, device=dev_t)), T(torch.empty(M, device=dev_t))
+            return lambda: ops.norm_quant(X, G1, 1e-6, None, Q, S, rot=A.ROT_SYLVESTER, group=128)
+        return make
+    run("cfg4_rmsnorm_wht128_quant_47104", make4(M4))
+
+    # ---- config 5a: RMSNorm + modulate + int8 quant; 5b: int8 GEMM + dequant + SiLU ----
     sc5, sh5 = bf16(1, C, scale=0.5), bf16(1, C, scale=0.5)
     tb5 = ops.Tables(scale=T(sc5), shift=T(sh5))
-    X5 = T(x5)
-    run("cfg5a_rmsnorm_mod_quant_47104", lambda: ops.norm_quant(X5, G1, 1e-6, tb5, Q4, S4))
+
+    def make5a(M):
+        def make():
+            x = bf16(M, C)
+            first.setdefault(f"x5_{M}", x)
+            X, Q, S = T(x), T(torch.empty(M, C, dtype=torch.int8, device=dev_t)), T(torch.empty(M, device=dev_t))
+            return lambda: ops.norm_quant(X, G1, 1e-6, tb5, Q, S)
+        return make
+    run("cfg5a_rmsnorm_mod_quant_47104", make5a(M4))
+    # the GEMM's inputs: config 5a's codes and scales of the first set
+    x5 = first.get(f"x5_{M4}", None)
+    if x5 is None:
+        x5 = bf16(M4, C)
+    q5, s5 = torch.empty(M4, C, dtype=torch.int8, device=dev_t), torch.empty(M4, device=dev_t)
+    Q5, S5 = T(q5), T(s5)
+    ops.norm_quant(T(x5), G1, 1e-6, tb5, Q5, S5)
     w5 = torch.randint(-127, 128, (16384, C), dtype=torch.int8, device=dev_t)
     ws5 = (0.005 + 0.015 * torch.rand(16384, device=dev_t)).float()
-    out5 = bf16(M4, 16384)
     layer = ops.Int8Linear(T(w5), T(ws5))
+    out5 = torch.empty(M4, 16384, dtype=torch.bfloat16, device=dev_t)
     O5 = T(out5)
-    run("cfg5b_int8_gemm_silu_47104x16384", lambda: ops.int8_gemm_dequant(Q4, S4, layer, A.ACT_SILU, O5), 5)
+    run("cfg5b_int8_gemm_silu_47104x16384", lambda: (lambda: ops.int8_gemm_dequant(Q5, S5, layer, A.ACT_SILU, O5)), 5)
 
     # ---- the MLP's middle: swiglu of fc1's [gate | up] output [47104 x 2*8192] -> fc2's quantizer (regular g 256) ----
-    q6, s6 = torch.empty(M4, 8192, dtype=torch.int8, device=dev_t), torch.empty(M4, device=dev_t)
-    X6, Q6, S6 = O5, T(q6), T(s6)    # the GEMM's output rows are [gate | up] halves of 8192
-    run("mlp_swiglu_quant_g256_47104x8192", lambda: ops.swiglu_quant(X6, Q6, S6, rot=A.ROT_REGULAR, group=256))
+    def make6():
+        q6, s6 = torch.empty(M4, 8192, dtype=torch.int8, device=dev_t), torch.empty(M4, device=dev_t)
+        X6, Q6, S6 = O5, T(q6), T(s6)    # the GEMM's output rows are [gate | up] halves of 8192
+        return lambda: ops.swiglu_quant(X6, Q6, S6, rot=A.ROT_REGULAR, group=256)
+    run("mlp_swiglu_quant_g256_47104x8192", make6)
 
     # ---- configs 2-5a at the other token count: 47104 tokens (grid T46 x H32 x W32) for 2 and 3, 16896 for 4 and 5a ----
-    x2b, r2b, o2b = bf16(M4, C), bf16(M4, C), torch.empty(M4, C, dtype=torch.bfloat16, device=dev_t)
-    X2b, R2b, O2b = T(x2b), T(r2b), T(o2b)
-    run("cfg2_ln_mod_gelu_gate_47104", lambda: ops.norm_mod_act_gate(X2b, A.NORM_LAYER, None, None, 1e-5, tb2, A.ACT_GELU_TANH, R2b, O2b))
-    del x2b, r2b, o2b, X2b, R2b, O2b
-    q3b, k3b = bf16(M4, 32 * 128), bf16(M4, 32 * 128)
-    cs3b = torch.from_numpy(rope_table(46, 32, 32)).to(dev_t)
-    Q3b, K3b, CS3b = T(q3b), T(k3b), T(cs3b)
-    run("cfg3_qk_rmsnorm_rope3d_47104", lambda: ops.qk_rms_rope(ops.Rows(Q3b, 0, 4096, M4, 32, 128), ops.Rows(K3b, 0, 4096, M4, 32, 128),
-                                                                 WQ, WK, 1e-5, CS3b, 128))
-    del q3b, k3b, cs3b, Q3b, K3b, CS3b
-    X4s, Q4s, S4s, X5s = T(x4[:M2]), T(q4[:M2]), T(s4[:M2]), T(x5[:M2])
-    run("cfg4_rmsnorm_wht128_quant_16896", lambda: ops.norm_quant(X4s, G1, 1e-6, None, Q4s, S4s, rot=A.ROT_SYLVESTER, group=128))
-    run("cfg5a_rmsnorm_mod_quant_16896", lambda: ops.norm_quant(X5s, G1, 1e-6, tb5, Q4s, S4s))
+    def make2b():
+        x, r, o = bf16(M4, C), bf16(M4, C), torch.empty(M4, C, dtype=torch.bfloat16, device=dev_t)
+        X, R, O = T(x), T(r), T(o)
+        return lambda: ops.norm_mod_act_gate(X, A.NORM_LAYER, None, None, 1e-5, tb2, A.ACT_GELU_TANH, R, O)
+    run("cfg2_ln_mod_gelu_gate_47104", make2b)
+    run("cfg3_qk_rmsnorm_rope3d_47104", make3(M4, T(torch.from_numpy(rope_table(46, 32, 32)).to(dev_t))))
+    run("cfg4_rmsnorm_wht128_quant_16896", make4(M2))
+    run("cfg5a_rmsnorm_mod_quant_16896", make5a(M2))
 
-    # ---- attention of the 16896-token grid, 32 heads of 128 (the int8 form: S >= 8192) ----
-    qkv7 = bf16(M2, 3 * 4096)
-    o7 = torch.empty(M2, 4096, dtype=torch.bfloat16, device=dev_t)
-    QKV7, O7 = T(qkv7), T(o7)
-    rows7 = [ops.Rows(QKV7, i * 4096, 3 * 4096, M2, 32, 128) for i in range(3)]
-    run("attn_sage_16896x32x128", lambda: ops.attention(*rows7, O7), 10)
-    del qkv7, o7, QKV7, O7, rows7
-    # the same at 47104 tokens (the 47k configurations' sequence)
-    qkv8 = bf16(M4, 3 * 4096)
-    o8 = torch.empty(M4, 4096, dtype=torch.bfloat16, device=dev_t)
-    QKV8, O8 = T(qkv8), T(o8)
-    rows8 = [ops.Rows(QKV8, i * 4096, 3 * 4096, M4, 32, 128) for i in range(3)]
-    run("attn_sage_47104x32x128", lambda: ops.attention(*rows8, O8), 3)
-    del qkv8, o8, QKV8, O8, rows8
+    # ---- attention of the 16896-token grid, 32 heads of 128 (the int8 form: S >= 8192), and at 47104 tokens ----
+    def make_attn(M):
+        def make():
+            qkv, o = bf16(M, 3 * 4096), torch.empty(M, 4096, dtype=torch.bfloat16, device=dev_t)
+            QKV, O = T(qkv), T(o)
+            rows = [ops.Rows(QKV, i * 4096, 3 * 4096, M, 32, 128) for i in range(3)]
+            return lambda: ops.attention(*rows, O)
+        return make
+    run("attn_sage_16896x32x128", make_attn(M2), 10)
+    run("attn_sage_47104x32x128", make_attn(M4), 3)
 
-    copy = None
     if args.copy_probe:
-        src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev_t).fill_(1.0)
-        dst = torch.empty_like(src)
-        ms_c = timed(lambda: dst.copy_(src), 20, 3)
-        copy = {"bytes": 2 * src.numel() * 2, "ms": round(ms_c, 4), "GB/s": round(2 * src.numel() * 2 / (ms_c * 1e-3) / 1e9, 1)}
-        del src, dst
+        def make_copy():
+            src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev_t).fill_(1.0)
+            dst = torch.empty_like(src)
+            return lambda: dst.copy_(src)
+        run("copy_probe_1GiB", make_copy, 20)
 
     per = {}
     for k, ms in kernels.items():
         gbs = B[k] / (ms * 1e-3) / 1e9
-        e = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_GBS, 4), "bytes": B[k]}
+        e = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_GBS, 4), "bytes": B[k],
+             "ring": rings[k], "steps": steps_of[k]}
         if k.startswith("cfg5b"):
             tops = 2 * M4 * C * 16384 / (ms * 1e-3) / 1e12
             e.update({"TOPS_i8": round(tops, 1), "frac_i8_peak": round(tops / PEAK_I8_TOPS, 4)})
@@ -249,7 +370,7 @@ def main() -> int:
             e.update({"TOPS": round(2 * half_ops / (ms * 1e-3) / 1e12, 1), "frac_mfma_peak": round(t_peak / (ms * 1e-3), 4)})
         per[k] = e
 
-    value = B["cfg2_ln_mod_gelu_gate_16896"] / (ms2 * 1e-3) / 1e9
+    value = B[HEADLINE] / (ms2 * 1e-3) / 1e9
     line = {
         "metric": "achieved HBM GB/s (% of 8 TB/s) per fused kernel at 16.8k/47k tokens x 4096",
         "value": round(value, 1),
@@ -264,38 +385,44 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (torch.randn on the device; shift/scale/gate ~N(0,0.5))",
         "config": {"workload": "AdaLN chain: LayerNorm(no affine) -> x*(1+scale)+shift -> GELU-tanh -> res + gate*y, "
-                               "X,res [16896 x 4096] bf16 (grid T16xH24xW44)", "tokens": M2, "hidden": C},
+                               "X,res [16896 x 4096] bf16 (grid T16xH24xW44), cache-cold: a ring of "
+                               f"{n2} buffer sets ({n2 * B[HEADLINE] / 1e9:.2f} GB)", "tokens": M2, "hidden": C},
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / PEAK_GBS, 4), "traffic": measured_traffic("cfg2_ln_mod_gelu_gate_16896")},
+                     "frac": round(value / PEAK_GBS, 4), "traffic": measured_traffic(HEADLINE)},
         "kernels": per,
         "device": dev.name(),
+        "cus": torch.cuda.get_device_properties(0).multi_processor_count,
     }
-    if copy:
-        line["copy_probe"] = copy
+    if args.mark:
+        line["marked"] = marked
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(x2, r2, tab, {"x1": x1, "g1": g1, "q3": q3, "k3": k3, "wq": wq, "wk": wk,
-                                                          "cs": cs, "x4": x4, "x5": x5, "sc5": sc5, "sh5": sh5,
-                                                          "q4": q4, "s4": s4, "w5": w5, "ws5": ws5})
+        line["cpu_baseline"] = cpu_baseline(x2, r2, tab, {"x1": first["x1"], "g1": g1, "wq": wq, "wk": wk, "cs": cs,
+                                                          "q3": first.get(f"q3_{M2}"), "k3": first.get(f"k3_{M2}"),
+                                                          "x4": first.get(f"x4_{M4}"), "x5": x5, "sc5": sc5, "sh5": sh5,
+                                                          "q5": q5, "s5": s5, "w5": w5, "ws5": ws5})
     print(json.dumps(line), flush=True)
     return 0
 
 
 def cpu_baseline(x2, r2, tab, t):
-    """The CPU oracle (oracle/h3oracle.c, C restatement of the reference arithmetic, row-parallel with contiguous row
-    chunks as engine/h3-core/src/reference.rs:43-80) on this host: the headline workload, and under `kernels` the other
-    configurations on their full inputs (the GEMM on its first 1024 rows, scaled linearly), each the median of a few
-    runs (about 10 s in all for the headline, a few runs for the others)."""
+    """The CPU oracle (oracle/h3oracle.c, the C restatement of the reference arithmetic, row-parallel with contiguous
+    row chunks as engine/h3-core/src/reference.rs:43-80) on this host, one thread per CPU of the process's share (the
+    cgroup quota or affinity mask, at most 16: the host's share for one GPU): the headline workload in full, the median
+    of the runs that fit about 10 s; under `kernels` the other configurations on the tensors the GPU ran (the GEMM on
+    its first 1024 rows, scaled linearly), each the median of at least 5 runs."""
     import numpy as np
     import torch
 
     from oracle import oracle as o
 
-    threads = min(16, os.cpu_count() or 1)
+    share = cpu_share()
+    avail = min(share["affinity"], int(share["cgroup_quota"]) if share["cgroup_quota"] else share["affinity"])
+    threads = max(1, min(16, avail))
     o.set_threads(threads)
     u16 = lambda a: a.view(torch.int16).cpu().numpy().view(np.uint16).ravel()   # noqa: E731
     f32 = lambda a: a.float().cpu().numpy().ravel()                              # noqa: E731
 
-    def median_time(fn, budget, least=3, most=50):
+    def median_time(fn, budget, least=5, most=50):
         fn()
         times = []
         t_end = time.perf_counter() + budget
@@ -310,37 +437,32 @@ def cpu_baseline(x2, r2, tab, t):
     med, n = median_time(lambda: o.norm_mod_act_gate(x, o.BF16, M2, C, o.NORM_LAYER, None, None, 1e-5, None, tb[0], tb[1],
                                                      tb[2], o.BF16, o.ACT_GELU_TANH, r, o.BF16, o.BF16), 10.0)
     B = bytes_cfg()
-    gbs = B["cfg2_ln_mod_gelu_gate_16896"] / med / 1e9
-    cpu = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
-    except Exception:
-        pass
+    gbs = B[HEADLINE] / med / 1e9
     out = {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-           "sample": f"the full 16896 x 4096 workload, median of {n} runs ({med * 1e3:.1f} ms each) on {cpu}"}
+           "sample": f"the full 16896 x 4096 workload, median of {n} runs ({med * 1e3:.1f} ms each), {threads} threads "
+                     f"on {share['model']} (nproc {share['nproc']}, affinity {share['affinity']}, cgroup quota "
+                     f"{share['cgroup_quota']})",
+           "host": share}
 
-    # the other configurations, on the same tensors the GPU ran
     per = {}
     x1, g1 = u16(t["x1"]), f32(t["g1"])
-    m, _ = median_time(lambda: o.norm_quant(x1, o.BF16, 2159, C, g1, 1e-6), 2.0)
-    per["cfg1_rmsnorm_quant_2159"] = m
-    q3, k3, wq, wk, cs = u16(t["q3"]), u16(t["k3"]), f32(t["wq"]), f32(t["wk"]), f32(t["cs"])
-    m, _ = median_time(lambda: (o.rms_rope(q3, o.BF16, M2, 32, 128, 4096, wq, 1e-5, cs, 128),
-                                o.rms_rope(k3, o.BF16, M2, 32, 128, 4096, wk, 1e-5, cs, 128)), 2.0)
-    per["cfg3_qk_rmsnorm_rope3d_16896"] = m
-    x4 = u16(t["x4"])
-    m, _ = median_time(lambda: o.norm_quant(x4, o.BF16, M4, C, g1, 1e-6, rot=o.ROT_SYLVESTER, group=128), 2.0)
-    per["cfg4_rmsnorm_wht128_quant_47104"] = m
+    per["cfg1_rmsnorm_quant_2159"] = median_time(lambda: o.norm_quant(x1, o.BF16, 2159, C, g1, 1e-6), 2.0)[0]
+    if t["q3"] is not None:
+        q3, k3, wq, wk, cs = u16(t["q3"]), u16(t["k3"]), f32(t["wq"]), f32(t["wk"]), f32(t["cs"])
+        per["cfg3_qk_rmsnorm_rope3d_16896"] = median_time(lambda: (o.rms_rope(q3, o.BF16, M2, 32, 128, 4096, wq, 1e-5, cs, 128),
+                                                                   o.rms_rope(k3, o.BF16, M2, 32, 128, 4096, wk, 1e-5, cs, 128)), 2.0)[0]
+    if t["x4"] is not None:
+        x4 = u16(t["x4"])
+        per["cfg4_rmsnorm_wht128_quant_47104"] = median_time(
+            lambda: o.norm_quant(x4, o.BF16, M4, C, g1, 1e-6, rot=o.ROT_SYLVESTER, group=128), 2.0)[0]
     x5, sc5, sh5 = u16(t["x5"]), u16(t["sc5"]), u16(t["sh5"])
-    m, _ = median_time(lambda: o.norm_quant(x5, o.BF16, M4, C, g1, 1e-6, None, sc5, sh5, o.BF16), 2.0)
-    per["cfg5a_rmsnorm_mod_quant_47104"] = m
+    per["cfg5a_rmsnorm_mod_quant_47104"] = median_time(lambda: o.norm_quant(x5, o.BF16, M4, C, g1, 1e-6, None, sc5, sh5, o.BF16), 2.0)[0]
     rows = 1024
-    q4 = t["q4"][:rows].cpu().numpy().ravel()
-    s4 = t["s4"][:rows].cpu().numpy().ravel()
+    q5 = t["q5"][:rows].cpu().numpy().ravel()
+    s5 = t["s5"][:rows].cpu().numpy().ravel()
     w5, ws5 = t["w5"].cpu().numpy().ravel(), f32(t["ws5"])
-    m, _ = median_time(lambda: o.gemm_dequant(q4, s4, rows, C, w5, 16384, ws5, act=o.ACT_SILU), 2.0, least=2)
-    per["cfg5b_int8_gemm_silu_47104x16384"] = m * M4 / rows
+    per["cfg5b_int8_gemm_silu_47104x16384"] = median_time(
+        lambda: o.gemm_dequant(q5, s5, rows, C, w5, 16384, ws5, act=o.ACT_SILU), 2.0, least=5)[0] * M4 / rows
     kernels = {}
     for k, sec in per.items():
         e = {"ms": round(sec * 1e3, 3), "GB/s": round(B[k] / sec / 1e9, 2)}
@@ -349,6 +471,136 @@ def cpu_baseline(x2, r2, tab, t):
             e["sample"] = f"the first {rows} of {M4} rows, time scaled by {M4 / rows:.1f}"
         kernels[k] = e
     out["kernels"] = kernels
+    return out
+
+
+# ---- the profiles/ tables: a rocprofv3 csv of a --mark run, cut into the timed dispatches of each workload ----
+def _short(name: str) -> str:
+    return re.sub(r"\(.*", "", name).replace("void ", "").strip()
+
+
+def _dispatches(path: str):
+    """(dispatch id, kernel name, row) in launch order; counter csvs hold one row per counter and dispatch"""
+    rows = list(csv.DictReader(open(path)))
+    key = "Dispatch_Id" if rows and "Dispatch_Id" in rows[0] else "Correlation_Id"
+    rows.sort(key=lambda r: int(r[key]))
+    return key, rows
+
+
+def _regions(rows, key, marked):
+    """the dispatches between each pair of markers, keyed by the marked workloads in order"""
+    out, cur, inside, i, seen = {}, [], False, 0, set()
+    for r in rows:
+        d = r[key]
+        if MARKER in r["Kernel_Name"]:
+            if d in seen:
+                continue
+            seen.add(d)
+            if inside:
+                if i < len(marked):
+                    out[marked[i]] = cur
+                i += 1
+            cur, inside = [], not inside
+            continue
+        if inside:
+            cur.append(r)
+    return out
+
+
+def _bench(path):
+    if not path:
+        return {}
+    txt = open(path).read().strip().splitlines()
+    return json.loads([l for l in txt if l.startswith("{")][-1])
+
+
+def summarize_trace(path: str, bench_json: str) -> str:
+    """Markdown: per workload, its kernels' mean and median rocprofv3 durations over exactly the timed launches,
+    against bench.py's HIP-event time per launch of the same run."""
+    b = _bench(bench_json)
+    key, rows = _dispatches(path)
+    regions = _regions(rows, key, b.get("marked", []))
+    lines = ["| workload | kernel | dispatches | mean µs | median µs | µs per launch (all its kernels) | bench µs per launch (HIP events) | ratio |",
+             "|---|---|---:|---:|---:|---:|---:|---:|"]
+    for w, rs in regions.items():
+        steps = b.get("kernels", {}).get(w, {}).get("steps")
+        per_kernel = collections.OrderedDict()
+        for r in rs:
+            per_kernel.setdefault(_short(r["Kernel_Name"]), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        bench_us = b["kernels"][w]["ms"] * 1e3 if w in b.get("kernels", {}) else float("nan")
+        first_k = next(iter(per_kernel.values()), [])
+        launches = steps or len(first_k) or 1
+        total = sum(sum(v) for v in per_kernel.values()) / launches
+        for j, (kn, v) in enumerate(per_kernel.items()):
+            v_sorted = sorted(v)
+            med = v_sorted[len(v) // 2]
+            tail = (f"{total:.2f} | {bench_us:.2f} | {total / bench_us:.3f}" if j == 0 else " | | ")
+            lines.append(f"| {w if j == 0 else ''} | `{kn}` | {len(v)} | {sum(v) / len(v):.2f} | {med:.2f} | {tail} |")
+    return "\n".join(lines)
+
+
+def summarize_pmc(paths, bench_json: str) -> str:
+    """Markdown: per workload, each counter summed over a launch's dispatches and averaged over the timed launches.
+    With FETCH_SIZE and WRITE_SIZE and the --copy-probe region: the HBM traffic per launch, each counter scaled by what
+    it reads for the 1 GiB copy, against the algorithmic bytes, and one machine-readable `traffic:` line per workload
+    (read by bench.py's roofline.traffic). With SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE: the matrix cores' busy
+    fraction, busy / (GRBM_GUI_ACTIVE x CUs x 4 SIMDs)."""
+    b = _bench(bench_json)
+    cus = int(b.get("cus", 256))
+    vals = collections.defaultdict(lambda: collections.defaultdict(float))   # workload -> counter -> sum
+    names = collections.defaultdict(set)
+    span = collections.defaultdict(dict)                                     # workload -> dispatch -> duration ns
+    for path in paths:
+        key, rows = _dispatches(path)
+        for w, rs in _regions(rows, key, b.get("marked", [])).items():
+            for r in rs:
+                vals[w][r["Counter_Name"]] += float(r["Counter_Value"])
+                names[w].add(_short(r["Kernel_Name"]))
+                if "Start_Timestamp" in r:
+                    span[w][r[key]] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    B = bytes_cfg()
+    counters = sorted({c for w in vals for c in vals[w]})
+    lines = ["| workload | kernels | " + " | ".join(f"{c} per launch" for c in counters) + " |",
+             "|---|---|" + "---:|" * len(counters)]
+    per_launch, dur = {}, {}
+    for w in vals:
+        n = b["kernels"][w]["steps"]
+        if span[w]:
+            dur[w] = sum(span[w].values()) / n
+        per_launch[w] = {c: vals[w][c] / n for c in vals[w]}
+        lines.append(f"| {w} | {', '.join('`' + k + '`' for k in sorted(names[w]))} | " +
+                     " | ".join(f"{per_launch[w].get(c, float('nan')):.1f}" for c in counters) + " |")
+    out = "\n".join(lines)
+    cal = per_launch.get("copy_probe_1GiB", {})
+    if "FETCH_SIZE" in counters and "WRITE_SIZE" in counters and cal.get("FETCH_SIZE") and cal.get("WRITE_SIZE"):
+        kib = (1 << 30) / 1024.0
+        sf, sw = kib / cal["FETCH_SIZE"], kib / cal["WRITE_SIZE"]
+        t = [f"\nCalibration (the 1 GiB device copy: {kib:.0f} KiB read and written): FETCH_SIZE reads "
+             f"{cal['FETCH_SIZE']:.1f} KiB, scale {sf:.3f}; WRITE_SIZE reads {cal['WRITE_SIZE']:.1f} KiB, scale {sw:.3f}.\n",
+             "| workload | scaled fetch + write bytes per launch | algorithmic bytes | ratio |", "|---|---:|---:|---:|"]
+        mr = []
+        for w in vals:
+            if w == "copy_probe_1GiB" or w not in B:
+                continue
+            tb = int(round((per_launch[w].get("FETCH_SIZE", 0) * sf + per_launch[w].get("WRITE_SIZE", 0) * sw) * 1024))
+            t.append(f"| {w} | {tb:,} | {B[w]:,} | {tb / B[w]:.4f} |")
+            mr.append(f"traffic: {w} bytes={tb} algorithmic={B[w]}")
+        out += "\n" + "\n".join(t) + "\n\n" + "\n".join(mr)
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in counters and "GRBM_GUI_ACTIVE" in counters:
+        # GRBM_GUI_ACTIVE counts the busy cycles of each XCD's graphics block, summed over the XCDs: divided by them it
+        # is the kernel's length in cycles (its quotient by the dispatch's duration is the clock, shown as a check).
+        # SQ_VALU_MFMA_BUSY_CYCLES is summed over every SIMD: divided by the SIMDs and the kernel's cycles it is the
+        # fraction of time a SIMD's matrix core is busy.
+        xcds = int(b.get("xcds", 8))
+        t = [f"\n| workload | kernel cycles (GRBM_GUI_ACTIVE / {xcds} XCDs) | clock GHz | MFMA busy per SIMD "
+             f"(SQ_VALU_MFMA_BUSY_CYCLES / ({cus} CUs x 4 SIMDs x kernel cycles)) |", "|---|---:|---:|---:|"]
+        for w in vals:
+            g = per_launch[w].get("GRBM_GUI_ACTIVE", 0) / xcds
+            if g:
+                ns = dur.get(w)
+                ghz = f"{g / ns:.2f}" if ns else "n/a"
+                t.append(f"| {w} | {g:,.0f} | {ghz} | {per_launch[w]['SQ_VALU_MFMA_BUSY_CYCLES'] / (g * cus * 4):.4f} |")
+        out += "\n" + "\n".join(t)
     return out
 
 
