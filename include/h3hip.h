@@ -205,6 +205,31 @@ int h3s_qk_rms_rope(void* ctx, void* q, void* k, int x_dt, int64_t M, int64_t H,
 int h3s_int8_gemm_dequant(void* ctx, const int8_t* q, const float* s, int64_t M, int64_t K, const int8_t* w, int64_t N,
                           const float* wscale, int64_t n_wscale, const float* bias, int act, void* out, int out_dt);
 
+/* The token layout of one denoiser call (engine/h3-core/src/layout.rs:107-176, Layout::new), owned by the library.
+ * The sequence is [text | keyframe conditioning | reference audio | audio | video]; a token's kind is one of: */
+enum { H3S_TOK_TEXT = 0, H3S_TOK_COND = 1, H3S_TOK_COND_AUDIO = 2, H3S_TOK_REF_AUDIO = 3, H3S_TOK_AUDIO = 4, H3S_TOK_VIDEO = 5 };
+/* A keyframe to condition on (layout.rs:45-52): its place on the target timeline in pixel frames, and the latent
+ * frames of video and of audio it brings (-1: none). */
+typedef struct {
+    double frame_index;
+    int64_t video_latent_t;
+    int64_t audio_latent_t;
+} h3s_keyframe;
+/* h3s_layout_plan (host only, no device): the segments of the sequence in row order - seg_start, seg_stop (rows) and
+ *   seg_kind, at most seg_cap of each written, any of them NULL - for a text of text_len tokens, a video latent
+ *   [latent_t, latent_h, latent_w] (even height and width; a token is 2 x 2 latent pixels), audio_t audio latent
+ *   frames (two rows each, one per stereo channel), n_keyframes keyframes and n_refs reference voices of ref_audio[i]
+ *   audio latent frames. Returns the number of segments (the last one's stop is the token count), or -1.
+ * h3s_layout: for the same request, each token's position (time, height, width) into positions float64 [tokens, 3],
+ *   with the reference's float64 arithmetic, and with rows not NULL its AdaLN table row rows[t] = row_of_kind[kind]
+ *   (row_of_kind: 6 host int32, the row each kind reads at the step). tokens must be the layout's token count. */
+int64_t h3s_layout_plan(int64_t text_len, int64_t latent_t, int64_t latent_h, int64_t latent_w, int64_t audio_t,
+                        const h3s_keyframe* keyframes, int64_t n_keyframes, const int64_t* ref_audio, int64_t n_refs,
+                        int64_t* seg_start, int64_t* seg_stop, int32_t* seg_kind, int64_t seg_cap);
+int h3s_layout(void* ctx, int64_t text_len, int64_t latent_t, int64_t latent_h, int64_t latent_w, int64_t audio_t,
+               const h3s_keyframe* keyframes, int64_t n_keyframes, const int64_t* ref_audio, int64_t n_refs,
+               const int32_t* row_of_kind, double* positions, int32_t* rows, int64_t tokens);
+
 /* h3s_int8_linear without any allocation: no counterpart in the reference. For callers that cannot allocate device
  * memory - code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. Same arguments and
  * results as h3s_int8_linear; the quantized rows go into a fixed device array of the library (64 MiB of codes and

@@ -848,6 +848,59 @@ void h3o_rotations(const double* positions, int64_t S, const float* inv_freq, in
             }
 }
 
+/* ---- token layout: engine/h3-core/src/layout.rs:88-176 (Layout::new), appended row by row in its order ---- */
+typedef struct { double* pos; int32_t* kind; int64_t n, cap; } lay_out;
+static void lay_put(lay_out* o, double t, double h, double w, int32_t kind) {
+    if (o->n < o->cap) {
+        if (o->pos) { o->pos[3 * o->n] = t; o->pos[3 * o->n + 1] = h; o->pos[3 * o->n + 2] = w; }
+        if (o->kind) o->kind[o->n] = kind;
+    }
+    ++o->n;
+}
+static double lay_axis(int64_t dim, double sqrt_area, int64_t i) {                             /* layout.rs:89-93 */
+    const double ratio = (double) dim / sqrt_area;
+    const int64_t n = dim / 2;
+    return ((double) i * (ratio / (double) n) + (1.0 - ratio) / 2.0) * 32.0;
+}
+static void lay_video(lay_out* o, int64_t vt, double origin, int64_t H, int64_t W, double sa, int32_t kind) {
+    static const double per[5] = {1.0, 4.0, 4.0, 4.0, 4.0};                                    /* layout.rs:15-16 */
+    double t = origin;
+    for (int64_t k = 0; k < vt; ++k) {                                                          /* layout.rs:96-105 */
+        for (int64_t a = 0; a < H / 2; ++a)
+            for (int64_t b = 0; b < W / 2; ++b) lay_put(o, t, lay_axis(H, sa, a), lay_axis(W, sa, b), kind);
+        t += 5.0 / 3.0 * per[k % 5];
+    }
+}
+static void lay_audio(lay_out* o, int64_t at, double origin, int64_t W, double sa, int32_t kind) {   /* layout.rs:134-140 */
+    const double ends[2] = {lay_axis(W, sa, 0), lay_axis(W, sa, W / 2 - 1)};
+    for (int c = 0; c < 2; ++c)
+        for (int64_t i = 0; i < at; ++i) lay_put(o, origin + (double) i, 0.0, ends[c], kind);
+}
+int64_t h3o_layout(int64_t text_len, int64_t latent_t, int64_t latent_h, int64_t latent_w, int64_t audio_t,
+                   const double* kf_index, const int64_t* kf_video, const int64_t* kf_audio, int64_t n_kf,
+                   const int64_t* ref_audio, int64_t n_refs, double* positions, int32_t* kinds, int64_t cap) {
+    if (latent_h <= 0 || latent_w <= 0 || latent_h % 2 || latent_w % 2) return fail("layout: even latent height and width");
+    const double sa = sqrt((double) (latent_h * latent_w));
+    lay_out o = {positions, kinds, 0, cap};
+    for (int64_t i = 0; i < text_len; ++i) lay_put(&o, (double) i, 0.0, 0.0, H3O_TOK_TEXT);     /* layout.rs:142-145 */
+    double spans = 0.0;
+    for (int64_t r = 0; r < n_refs; ++r) spans += (double) ref_audio[r];
+    const double cursor = (double) text_len + spans;                                            /* layout.rs:147 */
+    for (int64_t k = 0; k < n_kf; ++k) {                                                        /* layout.rs:148-158 */
+        const double at = cursor + 5.0 / 3.0 * kf_index[k];
+        if (kf_video[k] >= 0) lay_video(&o, kf_video[k], at, latent_h, latent_w, sa, H3O_TOK_COND);
+        if (kf_audio[k] >= 0) lay_audio(&o, kf_audio[k], at, latent_w, sa, H3O_TOK_COND_AUDIO);
+    }
+    double rc = (double) text_len;                                                              /* layout.rs:159-170 */
+    for (int64_t r = 0; r < n_refs; ++r) {
+        if (ref_audio[r] > 0) lay_audio(&o, ref_audio[r], rc, latent_w, sa, H3O_TOK_REF_AUDIO);
+        rc += (double) ref_audio[r];
+    }
+    lay_audio(&o, audio_t, cursor, latent_w, sa, H3O_TOK_AUDIO);                               /* layout.rs:171-174 */
+    lay_video(&o, latent_t, cursor, latent_h, latent_w, sa, H3O_TOK_VIDEO);
+    return o.n;
+}
+
 void h3o_compare(const float* a, const float* b, int64_t n, double* rel, double* cos) {
     double d2 = 0, a2 = 0, b2 = 0, ab = 0;
     for (int64_t i = 0; i < n; ++i) {

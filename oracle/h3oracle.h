@@ -167,6 +167,13 @@ void h3o_adaln_tables(const float* w, const float* b, const float* t_emb, int64_
 void h3o_rotations(const double* positions, int64_t S, const float* inv_freq, int64_t n, float* cs);
 
 /* reference::compare (engine/h3-core/src/reference.rs:84-95): relative L2 error and cosine */
+/* token kinds (engine/h3-core/src/layout.rs:21-32) and the layout of one denoiser call (layout.rs:107-176):
+ * positions float64 [tokens, 3] and kinds [tokens] (either may be NULL), at most cap rows written; keyframes as three
+ * arrays (frame index; video and audio latent frames, -1 for none); returns the number of tokens, or -1 */
+enum { H3O_TOK_TEXT = 0, H3O_TOK_COND = 1, H3O_TOK_COND_AUDIO = 2, H3O_TOK_REF_AUDIO = 3, H3O_TOK_AUDIO = 4, H3O_TOK_VIDEO = 5 };
+int64_t h3o_layout(int64_t text_len, int64_t latent_t, int64_t latent_h, int64_t latent_w, int64_t audio_t,
+                   const double* kf_index, const int64_t* kf_video, const int64_t* kf_audio, int64_t n_kf,
+                   const int64_t* ref_audio, int64_t n_refs, double* positions, int32_t* kinds, int64_t cap);
 void h3o_compare(const float* a, const float* b, int64_t n, double* rel, double* cos);
 
 /* the error of the last failing call (argument checks) */

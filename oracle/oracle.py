@@ -74,6 +74,7 @@ _SIGS = {
     "h3o_act": (f32, [f32, i32]),
     "h3o_act_n": (None, [vp, i64, i32, vp]),
     "h3o_compare": (None, [vp, vp, i64, vp, vp]),
+    "h3o_layout": (i64, [i64, i64, i64, i64, i64, vp, vp, vp, i64, vp, i64, vp, vp, i64]),
     "h3o_last_error": (C.c_char_p, []),
 }
 
@@ -375,6 +376,26 @@ def act_n(v: np.ndarray, kind: int) -> np.ndarray:
     out = np.empty_like(v)
     lib().h3o_act_n(_p(v), v.size, kind, _p(out))
     return out
+
+
+TOK_TEXT, TOK_COND, TOK_COND_AUDIO, TOK_REF_AUDIO, TOK_AUDIO, TOK_VIDEO = range(6)
+
+
+def layout(text_len, latent_t, latent_h, latent_w, audio_t, keyframes=(), ref_audio=()):
+    """positions float64 [tokens, 3] and kinds int32 [tokens] of one denoiser call (layout.rs:107-176); keyframes:
+    (frame_index, video latent frames or None, audio latent frames or None)"""
+    kf_i = np.array([k[0] for k in keyframes], np.float64)
+    kf_v = np.array([-1 if k[1] is None else k[1] for k in keyframes], np.int64)
+    kf_a = np.array([-1 if k[2] is None else k[2] for k in keyframes], np.int64)
+    refs = np.array(list(ref_audio), np.int64)
+    args = (text_len, latent_t, latent_h, latent_w, audio_t, _p(kf_i), _p(kf_v), _p(kf_a), len(keyframes), _p(refs),
+            refs.size)
+    n = lib().h3o_layout(*args, None, None, 0)
+    if n < 0:
+        raise RuntimeError(lib().h3o_last_error().decode())
+    pos, kinds = np.empty((n, 3), np.float64), np.empty(n, np.int32)
+    lib().h3o_layout(*args, _p(pos), _p(kinds), n)
+    return pos, kinds
 
 
 def compare(a: np.ndarray, b: np.ndarray):

@@ -11,7 +11,7 @@ import pytest
 from oracle import oracle as o
 from helpers import new, up
 from sycl_minimax_h3_amd import DType, Error, ops
-from sycl_minimax_h3_amd.layout import Layout
+from sycl_minimax_h3_amd.layout import Request, place, plan, step_rows
 
 pytestmark = pytest.mark.gpu
 o.set_threads(8)
@@ -32,18 +32,45 @@ def test_adaln_tables(dev, R, td, m, C):
     assert bad.size == 0, f"{bad.size} differ, first {bad[:5]}: {got[bad[:5]]} vs {want[bad[:5]]}"
 
 
-def test_rotations_on_the_fixture_layout(dev):
+def fixture_request():
     gold = json.load(open(os.path.join(HERE, "golden", "layout_384x288_2s.json")))
     m = {k: int(v) for k, v in gold["metadata"].items() if k != "sigma"}
-    lay = Layout.new(m["text_len"], m["latent_t"], m["latent_h"], m["latent_w"], m["audio_t"])
-    S, n = lay.tokens(), 21                                  # rot_dim 126 = 6 x 21
+    return Request(m["text_len"], m["latent_t"], m["latent_h"], m["latent_w"], m["audio_t"])
+
+
+@pytest.mark.parametrize("req", [
+    fixture_request(),
+    Request(10, 3, 4, 6, 5, keyframes=[(0.0, 1, None), (7.5, 2, 3)], ref_audio=(4, 0, 2)),
+    Request(0, 11, 46, 64, 0),                      # no text, no audio: 11 frames of 23 x 32 patches
+    Request(300, 31, 48, 80, 62, keyframes=[(120.0, 1, 1)]),
+])
+def test_layout_on_the_device(dev, req):
+    """h3s_layout: every position bit for bit as the oracle's restatement of Layout::new (layout.rs:107-176), and
+    every table row the kind's row of the step"""
+    segs = plan(req)
+    st = step_rows([s.kind for s in segs], 0.4, 12.0, 3.0)
+    pos, rows = place(dev, req, st.row_of_kind)
+    want_pos, kinds = o.layout(req.text_len, req.latent_t, req.latent_h, req.latent_w, req.audio_t, req.keyframes,
+                               req.ref_audio)
+    got = pos.to_numpy()
+    assert got.shape == want_pos.shape
+    assert np.array_equal(got.view(np.int64), want_pos.view(np.int64))
+    assert np.array_equal(rows.to_numpy(), st.row_of_kind[kinds])
+
+
+def test_rotations_on_the_fixture_layout(dev):
+    """the fixture's positions, placed on the device by h3s_layout, then h3s_rotations (rot_dim 126 = 6 x 21)"""
+    req = fixture_request()
+    pos, _ = place(dev, req)
+    positions = pos.to_numpy()
+    S, n = positions.shape[0], 21
     inv = (1.0 / np.power(np.float32(10000.0), np.arange(n, dtype=np.float32) / np.float32(n))).astype(np.float32)
-    want = o.rotations(lay.positions, S, inv)
+    want = o.rotations(positions, S, inv)
     cs = new(dev, "F32", [S, 3 * n, 2])
-    ops.rotations(up(dev, lay.positions.ravel(), "F64", [S, 3]), up(dev, inv, "F32", [n]), cs)
+    ops.rotations(pos, up(dev, inv, "F32", [n]), cs)
     got = cs.to_numpy().ravel()
     # the device rounds float64 cos / sin of the float argument once: the correctly rounded float32 values
-    ang = (lay.positions.astype(np.float32)[:, :, None] * inv[None, None, :]).astype(np.float64)
+    ang = (positions.astype(np.float32)[:, :, None] * inv[None, None, :]).astype(np.float64)
     cr = np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32).ravel()
     assert np.array_equal(got.view(np.int32), cr.view(np.int32))
     # the C library's cosf / sinf (the reference's values) are within one ulp of them, equal in all but a few
