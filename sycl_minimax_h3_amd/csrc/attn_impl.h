@@ -204,7 +204,7 @@ __global__ __launch_bounds__(256) void attn_qk_prep_vec_kernel(const void* __res
     for (int k = 0; k < N; ++k) {
         const int u = tid + 256 * k, r = u / CPR, c = u % CPR;
         uint4 raw = make_uint4(0, 0, 0, 0);
-        if (r0 + r < S) raw = *reinterpret_cast<const uint4*>(base + (int64_t) r * stride * (16 / V) + 16 * c);
+        if (r0 + r < S) raw = ld_nt(base + (int64_t) r * stride * (16 / V) + 16 * c);
         Vec<DT>::unpack(raw, v[k]);
     }
     if constexpr (SAGE) {
@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) void attn_v_prep_vec_kernel(const void* __rest
     for (int k = 0; k < N; ++k) {
         const int u = tid + 256 * k, t = u / CPR, c = u % CPR;
         uint4 raw = make_uint4(0, 0, 0, 0);
-        if (t0 + t < S) raw = *reinterpret_cast<const uint4*>(base + (int64_t) t * stride * (16 / V) + 16 * c);
+        if (t0 + t < S) raw = ld_nt(base + (int64_t) t * stride * (16 / V) + 16 * c);
         float f[V];
         Vec<DT>::unpack(raw, f);
 #pragma unroll

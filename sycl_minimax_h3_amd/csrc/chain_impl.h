@@ -73,14 +73,14 @@ __global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift)
     {
         const uint4* xp = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * (16 / V));
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) xr[j] = xp[cc[j]];
+        for (int j = 0; j < CPL; ++j) xr[j] = ld_nt(xp + cc[j]);
     }
     Raw<V, RW> rr[CPL];
     Raw<V, true> wr[CPL], br[CPL];
     Raw<V, TW> sr[CPL], hr[CPL], gr[CPL];
     if (has_res)
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) fetch(rr[j], A.res, res_dt, row * C + cc[j] * V);
+        for (int j = 0; j < CPL; ++j) fetch<V, RW, true>(rr[j], A.res, res_dt, row * C + cc[j] * V);
     if (has_w)
 #pragma unroll
         for (int j = 0; j < CPL; ++j) fetch(wr[j], A.w, H3S_F32, cc[j] * V);

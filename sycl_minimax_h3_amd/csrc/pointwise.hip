@@ -1,6 +1,6 @@
 // pointwise.hip - h3s_swiglu (kernels/h3sycl.cpp:1378-1419) and h3s_gate_add (kernels/h3sycl.cpp:1421-1431): one
 // 16-byte chunk of the row per thread, grid-stride over the whole tensor.
-#include "common.h"
+#include "rowcore.h"
 
 namespace h3 {
 
@@ -34,8 +34,8 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const void* __restrict__ x,
         const int64_t r = k / cpr, i = (k - r * cpr) * V;
         const uint4* xr = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(x) + r * 2 * C * (16 / V));
         float g[V], u[V], o[V];
-        Vec<XDT>::unpack(xr[i / V], g);
-        Vec<XDT>::unpack(xr[(C + i) / V], u);
+        Vec<XDT>::unpack(ld_nt(xr + i / V), g);
+        Vec<XDT>::unpack(ld_nt(xr + (C + i) / V), u);
 #pragma unroll
         for (int e = 0; e < V; ++e) o[e] = act_silu(g[e]) * u[e];
         store_rt2<V>(out, out_dt, r * C + i, o);
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void gate_add_kernel(void* x, int64_t M, int64
         const int64_t r = k / cpr, i = (k - r * cpr) * V, p = r * C + i;
         uint4* xp = reinterpret_cast<uint4*>(reinterpret_cast<char*>(x) + p * (16 / V));
         float a[V], b[V];
-        Vec<XDT>::unpack(*xp, a);
+        Vec<XDT>::unpack(ld_nt(xp), a);
         load_rt<V>(other, other_dt, p, b);
         if (gate) {
             float g[V];

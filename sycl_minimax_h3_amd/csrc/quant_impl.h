@@ -272,10 +272,10 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
     auto load_row = [&](uint4 (&xr)[CPL], uint4 (&ur)[CPL], int64_t row) {
         const uint4* xp = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * (SWI ? 2 : 1) * (16 / V));
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) xr[j] = xp[cc[j]];
+        for (int j = 0; j < CPL; ++j) xr[j] = ld_nt(xp + cc[j]);
         if constexpr (SWI)
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) ur[j] = xp[nch + cc[j]];
+            for (int j = 0; j < CPL; ++j) ur[j] = ld_nt(xp + nch + cc[j]);
     };
     // rounds a chunk to h's type (the reference's 16-bit scratch between its kernels)
     auto round_h = [&](float (&o)[V]) {
@@ -545,7 +545,7 @@ void quant_wave_kernel(QuantArgs A) {
     auto load_row = [&](uint4 (&xr)[CPL], int64_t row) {
         const char* xp = reinterpret_cast<const char*>(A.x) + wave_uniform(row) * C * 2;
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) xr[j] = *reinterpret_cast<const uint4*>(xp + (uint32_t) (cc[j] * 16));
+        for (int j = 0; j < CPL; ++j) xr[j] = ld_nt(xp + (uint32_t) (cc[j] * 16));
     };
     // The table rows of each step's group of NW rows (rows g + [0, NW), g = b0 + k U, one a wavefront), 64 steps
     // at a time, one step a lane, taken out with readlane: the group's first row's (gix), this wavefront's (tix),

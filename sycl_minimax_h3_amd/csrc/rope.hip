@@ -56,8 +56,8 @@ __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M
             const int u = u0 + k < nunits ? u0 + k : nunits - 1, t = u / ngroups, h0 = (u % ngroups) * HPW + hh;
             const int head = active && h0 < H ? h0 : 0;
             const uint16_t* base = (const uint16_t*) (t ? x1 : x0) + (tok * stride + (int64_t) head * D) * (16 / V / 2);
-            ra[k] = *reinterpret_cast<const uint4*>(base + (active ? off0 : 0) * (16 / V / 2));
-            rb[k] = *reinterpret_cast<const uint4*>(base + (rotated ? off1 : 0) * (16 / V / 2));
+            ra[k] = ld_nt(base + (active ? off0 : 0) * (16 / V / 2));
+            rb[k] = ld_nt(base + (rotated ? off1 : 0) * (16 / V / 2));
         }
 #pragma unroll
         for (int k = 0; k < kUnits; ++k) {
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(256) void rope_any_kernel(void* x0, void* x1, int64
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int c = slot + P2 * i;
-            if (hp && c < DC) buf[i] = hp[c];
+            if (hp && c < DC) buf[i] = ld_nt(hp + c);
         }
     };
     fetch(0);

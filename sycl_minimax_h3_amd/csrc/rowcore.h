@@ -120,15 +120,33 @@ template <int V, bool WIDE> struct Raw {
 template <int V> struct Raw<V, false> {
     uint4 a;
 };
-template <int V, bool WIDE> __device__ __forceinline__ void fetch(Raw<V, WIDE>& r, const void* p, int dt, int64_t i) {
+// Loads of data that is read once (the rows a kernel streams) use the nontemporal form: the lines are not kept for
+// reuse. A cold streaming probe (x and a residual read, one output written, 16896 x 4096 bf16 each, over a ring of
+// 1.25 GB) moved 73.8 % of 8 TB/s with ordinary loads and 81.3 % with these. Weights and tables, which every row
+// reads again, keep ordinary loads.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ld_nt(const void* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld_nt2(const void* p) {
+    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    return make_uint2(v.x, v.y);
+}
+// NT: a row streamed once (the nontemporal form); else a side input read again by other rows
+template <int V, bool WIDE, bool NT = false>
+__device__ __forceinline__ void fetch(Raw<V, WIDE>& r, const void* p, int dt, int64_t i) {
     if (WIDE && dt == H3S_F32) {
         const uint4* q = reinterpret_cast<const uint4*>((const float*) p + i);
-        r.a = q[0];
-        if constexpr (WIDE && V == 8) r.b = q[1];
+        r.a = NT ? ld_nt(q) : q[0];
+        if constexpr (WIDE && V == 8) r.b = NT ? ld_nt(q + 1) : q[1];
     } else if constexpr (V == 8) {
-        r.a = *reinterpret_cast<const uint4*>((const uint16_t*) p + i);
+        const uint4* q = reinterpret_cast<const uint4*>((const uint16_t*) p + i);
+        r.a = NT ? ld_nt(q) : *q;
     } else {
-        const uint2 t = *reinterpret_cast<const uint2*>((const uint16_t*) p + i);
+        const uint2* q = reinterpret_cast<const uint2*>((const uint16_t*) p + i);
+        const uint2 t = NT ? ld_nt2(q) : *q;
         r.a = make_uint4(t.x, t.y, 0u, 0u);
     }
 }
@@ -169,8 +187,6 @@ enum : int {
 constexpr int row_act(int f) { return (f / ROW_ACT1) & 3; }
 
 // ---- stores that bypass the caches' retention (the outputs are streamed, never read back by the kernel) ----
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void st_nt(void* p, uint4 v) {
     const u32x4 t = {v.x, v.y, v.z, v.w};
     __builtin_nontemporal_store(t, reinterpret_cast<u32x4*>(p));
