@@ -2,6 +2,7 @@
 // h3s_attention_causal (kernels/h3sycl.h:104-108) on the kernels of attn_impl.h. The form follows the reference's choice: the int8 (SageAttention) form for sequences of
 // at least H3S_SAGE_MIN_S tokens (8192) unless H3S_ATTN=onednn, the 16-bit form otherwise. Head sizes 64 and 128.
 #include <cmath>
+#include <cstdio>
 
 #include "attn_impl.h"
 
@@ -60,6 +61,8 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
     float* af = c->scratch<float>(Ctx::ATT_AUX, (size_t) ((Hq + Hkv) * nbp + Hkv * D));
     if (!aq || !ak || !av || !af) return -1;
     float *qs = af, *ks = af + Hq * nbp, *km = af + (Hq + Hkv) * nbp;
+    PhaseTimer timer(c);
+    timer.mark();
     switch (dt) {
         case H3S_BF16: prep<H3S_BF16>(c, q, k, v, S, Sp, Hq, Hkv, (int) D, qs_stride, kv_stride, sage, aq, ak, av, qs, ks, km); break;
         case H3S_F16: prep<H3S_F16>(c, q, k, v, S, Sp, Hq, Hkv, (int) D, qs_stride, kv_stride, sage, aq, ak, av, qs, ks, km); break;
@@ -75,6 +78,7 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
     P.kvdiv = (int) (Hq / Hkv);
     P.Spk = Sp;
     const unsigned grid = (unsigned) (Hq * P.nqb);
+    timer.mark();
     if (causal) {
         if (D == 128) attn_kernel<false, 128, true><<<grid, 256, 0, c->stream>>>(P);
         else attn_kernel<false, 64, true><<<grid, 256, 0, c->stream>>>(P);
@@ -85,7 +89,14 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
         if (D == 128) attn_kernel<false, 128><<<grid, 256, 0, c->stream>>>(P);
         else attn_kernel<false, 64><<<grid, 256, 0, c->stream>>>(P);
     }
-    return launched(fn);
+    if (launched(fn)) return -1;
+    timer.mark();
+    const std::vector<float> ms = timer.elapsed();
+    if (ms.size() == 2)   // H3S_PROFILE (kernels/h3sycl.cpp:1753-1760)
+        std::fprintf(stderr, "h3hip: attention (%s) S=%lld H=%lld D=%lld: preparation %.2f ms, attention %.2f ms\n",
+                     sage ? "int8" : causal ? "16-bit, causal" : "16-bit", (long long) S, (long long) Hq, (long long) D, ms[0],
+                     ms[1]);
+    return 0;
 }
 
 static int attention_checks(const char* fn, int dt, int64_t H, int64_t D, int64_t stride, int out_dt, const void* q,

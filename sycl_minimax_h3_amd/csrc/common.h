@@ -72,10 +72,32 @@ struct Ctx {
     bool sage_want = true;                 // H3S_ATTN=onednn: false
     int64_t sage_min_s = 8192;             // H3S_SAGE_MIN_S
     int64_t quant_wave_min = 8192;         // H3S_QUANT_WAVE_MIN_ROWS: fewest rows for the one-wavefront-a-row quantizer
+    // H3S_PROFILE (kernels/h3sycl.cpp:117, 228): the int8 linear's time by pass, summed over its row chunks and
+    // reported at h3s_destroy; attention's time by phase, reported per call
+    bool profile = false;
+    double lin_ms[2] = {0.0, 0.0};         // quantize (rotation, row scales and codes in one pass), int8 GEMM
+    int64_t lin_chunks = 0;
 
     // region r with room for at least `bytes`; NULL, with the reason as this thread's error, when it cannot grow
     void* scratch_bytes(Region r, size_t bytes);
     template <typename T> T* scratch(Region r, size_t n) { return static_cast<T*>(scratch_bytes(r, n * sizeof(T))); }
+};
+
+// The phases of one call timed with events on the context's stream (H3S_PROFILE): mark() at each boundary, then
+// elapsed() waits for the last mark and gives the milliseconds between consecutive marks. Inert when profiling is off.
+class PhaseTimer {
+  public:
+    // allowed false: never times (a caller that must create nothing, h3s_int8_linear_noalloc)
+    explicit PhaseTimer(Ctx* c, bool allowed = true);
+    ~PhaseTimer();
+    void mark();
+    std::vector<float> elapsed();
+    bool on() const { return on_; }
+
+  private:
+    Ctx* c_;
+    bool on_;
+    std::vector<hipEvent_t> ev_;
 };
 
 // the context of an entry point: NULL with an error when ctx is NULL; makes its device current

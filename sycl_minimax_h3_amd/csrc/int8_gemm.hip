@@ -105,14 +105,24 @@ static int linear_checks(const char* fn, const void* x, int x_dt, int64_t K, int
 // the quantizer, then the GEMM, rows at a time into xq [rows, K] and rs [rows]
 static int linear_chunks(Ctx* c, const char* fn, const void* x, int x_dt, int64_t M, int64_t K, const int8_t* w, int64_t N,
                          const float* wscale, int64_t n_wscale, const float* bias, void* out, int out_dt, int group, int8_t* xq,
-                         float* rs, int64_t rows) {
+                         float* rs, int64_t rows, bool timed) {
     const size_t xe = (size_t) elem_size(x_dt), oe = (size_t) elem_size(out_dt);
     for (int64_t r0 = 0; r0 < M; r0 += rows) {
         const int64_t n = M - r0 < rows ? M - r0 : rows;
+        PhaseTimer t(c, timed);
+        t.mark();
         if (launch_quantize(c, (const char*) x + (size_t) (r0 * K) * xe, x_dt, n, K, group, xq, rs)) return -1;
+        t.mark();
         if (launch_gemm(c, fn, xq, rs, n, K, w, N, wscale, n_wscale, bias, H3S_ACT_NONE, (char*) out + (size_t) (r0 * N) * oe,
                         out_dt))
             return -1;
+        t.mark();
+        const std::vector<float> ms = t.elapsed();
+        if (ms.size() == 2) {
+            c->lin_ms[0] += ms[0];
+            c->lin_ms[1] += ms[1];
+            ++c->lin_chunks;
+        }
     }
     return 0;
 }
@@ -135,7 +145,7 @@ H3S_EXPORT int h3s_int8_linear(void* ctx, const void* x, int x_dt, int64_t M, in
     int8_t* xq = c->scratch<int8_t>(Ctx::LIN_CODES, (size_t) (rows * K));
     float* rs = c->scratch<float>(Ctx::LIN_SCALES, (size_t) rows);
     if (!xq || !rs) return -1;
-    return linear_chunks(c, fn, x, x_dt, M, K, w, N, wscale, n_wscale, bias, out, out_dt, group, xq, rs, rows);
+    return linear_chunks(c, fn, x, x_dt, M, K, w, N, wscale, n_wscale, bias, out, out_dt, group, xq, rs, rows, true);
 } catch (const std::exception& e) { return fail(e.what()); }
 
 // h3s_int8_linear with the quantized rows in the fixed device array: no allocation, any M (in chunks of at most
@@ -158,5 +168,5 @@ H3S_EXPORT int h3s_int8_linear_noalloc(void* ctx, const void* x, int x_dt, int64
     const int64_t by_codes = (int64_t) (kScratchCodes / (size_t) K);
     const int64_t rows = by_codes < kScratchRows ? by_codes : kScratchRows;
     return linear_chunks(c, fn, x, x_dt, M, K, w, N, wscale, n_wscale, bias, out, out_dt, group, reinterpret_cast<int8_t*>(base),
-                         reinterpret_cast<float*>(base + kScratchCodes), rows);
+                         reinterpret_cast<float*>(base + kScratchCodes), rows, false);
 } catch (const std::exception& e) { return fail(e.what()); }

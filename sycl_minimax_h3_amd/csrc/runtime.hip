@@ -44,6 +44,29 @@ int launched(const char* fn) {
     return 0;
 }
 
+PhaseTimer::PhaseTimer(Ctx* c, bool allowed) : c_(c), on_(allowed && c->profile) {}
+PhaseTimer::~PhaseTimer() {
+    for (hipEvent_t e : ev_) (void) hipEventDestroy(e);
+}
+void PhaseTimer::mark() {
+    if (!on_) return;
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) { on_ = false; (void) hipGetLastError(); return; }
+    ev_.push_back(e);
+    (void) hipEventRecord(e, c_->stream);
+}
+std::vector<float> PhaseTimer::elapsed() {
+    std::vector<float> out;
+    if (!on_ || ev_.size() < 2) return out;
+    (void) hipEventSynchronize(ev_.back());
+    for (size_t i = 1; i < ev_.size(); ++i) {
+        float ms = 0.0f;
+        (void) hipEventElapsedTime(&ms, ev_[i - 1], ev_[i]);
+        out.push_back(ms);
+    }
+    return out;
+}
+
 static std::string mib(size_t bytes) { return std::to_string((bytes + (1 << 20) - 1) >> 20) + " MiB"; }
 
 bool Budget::take(size_t bytes, const std::string& what) {
@@ -128,6 +151,7 @@ static void init(Ctx& c) {
     if (const char* e = std::getenv("H3S_MEM_FRACTION")) frac = std::min(0.97, std::max(0.05, std::atof(e)));
     c.budget.set_limit((size_t) ((double) total * frac));
     c.poison = std::getenv("H3S_POISON") != nullptr;
+    c.profile = std::getenv("H3S_PROFILE") != nullptr;
     // h3s_int8_linear_noalloc's fixed scratch: its address on this device, looked up once (a failure is reported by
     // that entry point, not here)
     (void) noalloc_setup(c.device);
@@ -325,6 +349,9 @@ H3S_EXPORT void h3s_destroy(void* ctx) {
     (void) hipSetDevice(c->device);
     (void) hipStreamSynchronize(c->stream);
     if (c->copy_stream) { (void) hipStreamSynchronize(c->copy_stream); (void) hipStreamDestroy(c->copy_stream); }
+    if (c->profile && c->lin_chunks)
+        std::fprintf(stderr, "h3hip: int8 linear, %lld row chunks: quantize %.1f ms, int8 GEMM %.1f ms\n",
+                     (long long) c->lin_chunks, c->lin_ms[0], c->lin_ms[1]);
     for (auto& a : c->areas)
         if (a.p) (void) hipFree(a.p);
     release_blas(c);
