@@ -35,12 +35,17 @@ struct ChainArgs {
     int out_dt;
 };
 
-template <int XDT, int CPL, int F>
+// R rows a unit: with R > 1 (rows of 256 or 512 lanes, one unit a block) the block takes rows R b .. R b + R - 1.
+// It issues every row's x and residual together, loads the weights and the table rows once and uses them for all
+// its rows, reloading the table rows only for a row whose table row differs. The weights and tables are read from
+// L2 by every block. At 16896 x 4096 with the AdaLN's three tables, two rows a block measured 68.6 us against
+// 71.2 for one (cache-cold), and three or four rows were slower (more registers, fewer wavefronts a SIMD).
+template <int XDT, int CPL, int F, int R = 1>
 __global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift) {
     constexpr int V = Vec<XDT>::V;
     constexpr bool DYN = F & ROW_DYN;
     constexpr bool TW = DYN || (F & ROW_TAB32), RW = DYN || (F & ROW_RES32);   // wide storage of tables, residual
-    __shared__ float red[2][8];
+    __shared__ float red[2 * R][8];
     const bool has_w = DYN ? A.w != nullptr : (F & ROW_W) != 0;
     const bool has_b = DYN ? A.b != nullptr : (F & ROW_B) != 0;
     const bool has_tab = DYN ? A.scale != nullptr : (F & ROW_TAB) != 0;
@@ -52,130 +57,167 @@ __global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift)
     const int out_dt = DYN ? A.out_dt : H3S_BF16;
     const int norm = DYN ? A.norm : (F & ROW_LN) ? H3S_NORM_LAYER : H3S_NORM_RMS;
     const int act_kind = DYN ? A.act : row_act(F);
-    const RowPos P = row_pos(lshift, A.M);
     const int L = 1 << lshift;
-    const int64_t row = P.row, C = A.C, nch = C / V;
+    const int64_t C = A.C, nch = C / V;
+    // this lane's place: lane t of the rows rowk[0 .. R) (clamped into [0, M); live = false past M)
+    int t, W;
+    int64_t rowk[R];
+    bool livek[R];
+    if constexpr (R == 1) {
+        const RowPos P = row_pos(lshift, A.M);
+        t = P.t;
+        W = P.W;
+        rowk[0] = P.row;
+        livek[0] = P.live;
+    } else {
+        t = (int) threadIdx.x;
+        W = L >> 6;
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const int64_t r = (int64_t) blockIdx.x * R + k;
+            livek[k] = r < A.M;
+            rowk[k] = livek[k] ? r : A.M - 1;
+        }
+    }
 
     // chunk j of this lane, clamped into the row (a clamped chunk is loaded and never used)
     int64_t cc[CPL];
     bool ok[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int64_t c = P.t + (int64_t) L * j;
+        const int64_t c = t + (int64_t) L * j;
         ok[j] = c < nch;
         cc[j] = ok[j] ? c : nch - 1;
     }
 
-    // ---- every load of the row, in flight together: the table row index first, then the row and the residual
-    // (HBM), then the weights and table rows (small, cache resident) ----
-    const int64_t tr = (has_tab || has_gate) && A.rows ? (int64_t) A.rows[row] * C : 0;
-    uint4 xr[CPL];
-    {
-        const uint4* xp = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + row * C * (16 / V));
+    // ---- every load, in flight together: the rows' table row indices, then the rows and their residuals (HBM,
+    // streamed once), then the weights and table rows (small, cache resident, shared by the unit's rows) ----
+    const bool tabbed = (has_tab || has_gate) && A.rows;
+    int64_t trk[R];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) xr[j] = ld_nt(xp + cc[j]);
+    for (int k = 0; k < R; ++k) trk[k] = tabbed ? (int64_t) A.rows[rowk[k]] * C : 0;
+    int64_t tr = trk[0];
+    uint4 xr[R][CPL];
+    Raw<V, RW> rr[R][CPL];
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        const uint4* xp = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.x) + rowk[k] * C * (16 / V));
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) xr[k][j] = ld_nt(xp + cc[j]);
+        if (has_res)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) fetch<V, RW, true>(rr[k][j], A.res, res_dt, rowk[k] * C + cc[j] * V);
     }
-    Raw<V, RW> rr[CPL];
     Raw<V, true> wr[CPL], br[CPL];
     Raw<V, TW> sr[CPL], hr[CPL], gr[CPL];
-    if (has_res)
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) fetch<V, RW, true>(rr[j], A.res, res_dt, row * C + cc[j] * V);
     if (has_w)
 #pragma unroll
         for (int j = 0; j < CPL; ++j) fetch(wr[j], A.w, H3S_F32, cc[j] * V);
     if (has_b)
 #pragma unroll
         for (int j = 0; j < CPL; ++j) fetch(br[j], A.b, H3S_F32, cc[j] * V);
-    if (has_tab) {
+    auto load_tables = [&](int64_t at) {
+        if (has_tab) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                fetch(sr[j], A.scale, tab_dt, at + cc[j] * V);
+                fetch(hr[j], A.shift, tab_dt, at + cc[j] * V);
+            }
+        }
+        if (has_gate)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) fetch(gr[j], A.gate, tab_dt, at + cc[j] * V);
+    };
+    load_tables(tr);
+
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        const int64_t row = rowk[k];
+        if (k > 0 && trk[k] != tr) {
+            // a row of another table row (a segment boundary between the unit's rows): its own tables
+            tr = trk[k];
+            load_tables(tr);
+        }
+
+        // ---- row statistics ----
+        float v[CPL][V];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(xr[k][j], v[j]);
+        float mean = 0.0f, inv;
+        if (norm == H3S_NORM_LAYER) {
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+                if (ok[j])
+#pragma unroll
+                    for (int e = 0; e < V; ++e) s = s + v[j][e];
+            mean = row_sum(s, red[2 * k], W) / (float) C;
+            float q = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+                if (ok[j])
+#pragma unroll
+                    for (int e = 0; e < V; ++e) {
+                        const float d = v[j][e] - mean;
+                        q = __builtin_fmaf(d, d, q);
+                    }
+            inv = inv_root(row_sum(q, red[2 * k + 1], W), (float) C, A.eps);
+        } else {
+            float q = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+                if (ok[j])
+#pragma unroll
+                    for (int e = 0; e < V; ++e) q = __builtin_fmaf(v[j][e], v[j][e], q);
+            inv = inv_root(row_sum(q, red[2 * k], W), (float) C, A.eps);
+        }
+
+        // ---- the chain, one chunk at a time ----
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            fetch(sr[j], A.scale, tab_dt, tr + cc[j] * V);
-            fetch(hr[j], A.shift, tab_dt, tr + cc[j] * V);
+            float o[V], f[V], g[V];
+            if (norm == H3S_NORM_LAYER) {
+#pragma unroll
+                for (int e = 0; e < V; ++e) o[e] = (v[j][e] - mean) * inv;
+            } else {
+#pragma unroll
+                for (int e = 0; e < V; ++e) o[e] = v[j][e] * inv;
+            }
+            if (has_w) {
+                decode(wr[j], H3S_F32, f);
+#pragma unroll
+                for (int e = 0; e < V; ++e) o[e] = o[e] * f[e];
+            }
+            if (has_b) {
+                decode(br[j], H3S_F32, f);
+#pragma unroll
+                for (int e = 0; e < V; ++e) o[e] = o[e] + f[e];
+            }
+            if (has_tab) {
+                decode(sr[j], tab_dt, f);
+                decode(hr[j], tab_dt, g);
+#pragma unroll
+                for (int e = 0; e < V; ++e) o[e] = o[e] * (1.0f + f[e]) + g[e];
+            }
+            if (act_kind == H3S_ACT_GELU_TANH) {
+#pragma unroll
+                for (int e = 0; e < V; ++e) o[e] = act_gelu_tanh(o[e]);
+            } else if (act_kind == H3S_ACT_SILU) {
+#pragma unroll
+                for (int e = 0; e < V; ++e) o[e] = act_silu(o[e]);
+            }
+            if (has_gate) {
+                decode(gr[j], tab_dt, f);
+#pragma unroll
+                for (int e = 0; e < V; ++e) o[e] = o[e] * f[e];
+            }
+            if (has_res) {
+                decode(rr[k][j], res_dt, f);
+#pragma unroll
+                for (int e = 0; e < V; ++e) o[e] = f[e] + o[e];
+            }
+            if (livek[k] && ok[j]) store_chunk<V>(A.out, out_dt, row * C + cc[j] * V, o);
         }
-    }
-    if (has_gate)
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) fetch(gr[j], A.gate, tab_dt, tr + cc[j] * V);
-
-    // ---- row statistics ----
-    float v[CPL][V];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(xr[j], v[j]);
-    float mean = 0.0f, inv;
-    if (norm == H3S_NORM_LAYER) {
-        float s = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j)
-            if (ok[j])
-#pragma unroll
-                for (int e = 0; e < V; ++e) s = s + v[j][e];
-        mean = row_sum(s, red[0], P.W) / (float) C;
-        float q = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j)
-            if (ok[j])
-#pragma unroll
-                for (int e = 0; e < V; ++e) {
-                    const float d = v[j][e] - mean;
-                    q = __builtin_fmaf(d, d, q);
-                }
-        inv = inv_root(row_sum(q, red[1], P.W), (float) C, A.eps);
-    } else {
-        float q = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j)
-            if (ok[j])
-#pragma unroll
-                for (int e = 0; e < V; ++e) q = __builtin_fmaf(v[j][e], v[j][e], q);
-        inv = inv_root(row_sum(q, red[0], P.W), (float) C, A.eps);
-    }
-
-    // ---- the chain, one chunk at a time ----
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        float o[V], f[V], g[V];
-        if (norm == H3S_NORM_LAYER) {
-#pragma unroll
-            for (int e = 0; e < V; ++e) o[e] = (v[j][e] - mean) * inv;
-        } else {
-#pragma unroll
-            for (int e = 0; e < V; ++e) o[e] = v[j][e] * inv;
-        }
-        if (has_w) {
-            decode(wr[j], H3S_F32, f);
-#pragma unroll
-            for (int e = 0; e < V; ++e) o[e] = o[e] * f[e];
-        }
-        if (has_b) {
-            decode(br[j], H3S_F32, f);
-#pragma unroll
-            for (int e = 0; e < V; ++e) o[e] = o[e] + f[e];
-        }
-        if (has_tab) {
-            decode(sr[j], tab_dt, f);
-            decode(hr[j], tab_dt, g);
-#pragma unroll
-            for (int e = 0; e < V; ++e) o[e] = o[e] * (1.0f + f[e]) + g[e];
-        }
-        if (act_kind == H3S_ACT_GELU_TANH) {
-#pragma unroll
-            for (int e = 0; e < V; ++e) o[e] = act_gelu_tanh(o[e]);
-        } else if (act_kind == H3S_ACT_SILU) {
-#pragma unroll
-            for (int e = 0; e < V; ++e) o[e] = act_silu(o[e]);
-        }
-        if (has_gate) {
-            decode(gr[j], tab_dt, f);
-#pragma unroll
-            for (int e = 0; e < V; ++e) o[e] = o[e] * f[e];
-        }
-        if (has_res) {
-            decode(rr[j], res_dt, f);
-#pragma unroll
-            for (int e = 0; e < V; ++e) o[e] = f[e] + o[e];
-        }
-        if (P.live && ok[j]) store_chunk<V>(A.out, out_dt, row * C + cc[j] * V, o);
     }
 }
 
@@ -200,7 +242,22 @@ inline int chain_features(const ChainArgs& A, int x_dt) {
 template <int XDT> int chain_launch(Ctx* c, const char* fn, const ChainArgs& A, RowPlan p) {
     const RowLaunch R = row_launch(A.M, p);
     const int f = chain_features(A, XDT);
-#define H3_CHAIN_F(CC, FF) row_chain_kernel<XDT, CC, FF><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift)
+    // two rows a block: rows of 256 or 512 lanes and at most two chunks a lane (more would cost wavefronts a SIMD),
+    // with side inputs the rows share, and rows enough that half as many blocks still fill the device many times
+    const bool pair = XDT == H3S_BF16 && f != ROW_DYN && p.L >= 256 && p.cpl <= 2 &&
+                      (f & (ROW_W | ROW_B | ROW_TAB | ROW_GATE)) && A.M >= (int64_t) c->cus * 16;
+    const unsigned grid2 = (unsigned) ((A.M + 1) / 2);
+#define H3_CHAIN_F(CC, FF)                                                                                            \
+    {                                                                                                                 \
+        if constexpr (CC <= 2) {                                                                                      \
+            if (pair) {                                                                                               \
+                row_chain_kernel<XDT, CC, FF, 2><<<grid2, R.threads, 0, c->stream>>>(A, R.lshift);                   \
+                return launched(fn);                                                                                  \
+            }                                                                                                         \
+        }                                                                                                             \
+        row_chain_kernel<XDT, CC, FF, 1><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift);                          \
+    }
+#define H3_CHAIN_D(CC) row_chain_kernel<XDT, CC, ROW_DYN, 1><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift)
 #define H3_CHAIN_ADA(CC, NORM)                                                                                        \
     if (f == (kChainAda | NORM)) { H3_CHAIN_F(CC, kChainAda | NORM); return launched(fn); }                          \
     if (f == (kChainAda | NORM | H3S_ACT_GELU_TANH * ROW_ACT1)) { H3_CHAIN_F(CC, kChainAda | NORM | H3S_ACT_GELU_TANH * ROW_ACT1); return launched(fn); } \
@@ -215,7 +272,7 @@ template <int XDT> int chain_launch(Ctx* c, const char* fn, const ChainArgs& A, 
             H3_CHAIN_ADA(CC, 0)                                                                  \
             H3_CHAIN_ADA(CC, ROW_LN)                                                             \
         }                                                                                       \
-        H3_CHAIN_F(CC, ROW_DYN);                                                                \
+        H3_CHAIN_D(CC);                                                                         \
         return launched(fn);                                                                    \
     }
     H3_CHAIN_CPL(1)
@@ -224,6 +281,7 @@ template <int XDT> int chain_launch(Ctx* c, const char* fn, const ChainArgs& A, 
     H3_CHAIN_CPL(4)
 #undef H3_CHAIN_CPL
 #undef H3_CHAIN_ADA
+#undef H3_CHAIN_D
 #undef H3_CHAIN_F
     return fail(std::string(fn) + ": no kernel for this row length");
 }

@@ -457,6 +457,56 @@ def test_norm_mod_act_gate_float32_and_affine(dev):
     assert_bits_equal(out.to_numpy(), want, "norm_mod_act_gate f32")
 
 
+def segment_rows(seed, M, R):
+    """table rows in runs of 1 to 9 rows: many runs change between the two rows of a block of two"""
+    lens = np.random.default_rng(seed).integers(1, 10, M)
+    return np.repeat(np.arange(M) % R, lens)[:M].astype(np.int32)
+
+
+@pytest.mark.parametrize("C", [2048, 4096])
+@pytest.mark.parametrize("kind", ["ada_ln_gelu", "ada_rms_silu", "ada_ln", "rms_mod_f32", "layer_norm_affine"])
+def test_chain_two_rows_a_block(dev, kind, C):
+    """Enough rows (an odd count) that rows of 256 lanes go two to a block: the weights and table rows are loaded
+    once for both, and reloaded for the second row where its table row differs; the last block's second row is
+    past the end."""
+    M, R = 5001, 5          # at least 16 rows a compute unit of the 256
+    x = inputs(40, M * C, o.BF16, 2.0)
+    res = inputs(41, M * C, o.BF16)
+    rows = segment_rows(42, M, R)
+    assert np.count_nonzero(rows[1::2] != rows[0:-1:2]) > M // 10
+    out = new(dev, "BF16", [M, C])
+    xt = up(dev, x, "BF16", [M, C])
+    if kind.startswith("ada"):
+        norm = o.NORM_LAYER if "_ln" in kind else o.NORM_RMS
+        act = o.ACT_GELU_TANH if "gelu" in kind else o.ACT_SILU if "silu" in kind else o.ACT_NONE
+        tabs = [o.to_dt(0.5 * np.random.default_rng(43 + i).standard_normal(R * C).astype(np.float32), o.BF16)
+                for i in range(3)]
+        w = weight(46, C) if norm == o.NORM_RMS else None
+        want = o.norm_mod_act_gate(x, o.BF16, M, C, norm, w, None, 1e-5, rows, tabs[0], tabs[1], tabs[2], o.BF16, act,
+                                   res, o.BF16, o.BF16)
+        tb = ops.Tables(scale=up(dev, tabs[0], "BF16", [R, C]), shift=up(dev, tabs[1], "BF16", [R, C]),
+                        gate=up(dev, tabs[2], "BF16", [R, C]), rows=up(dev, rows, "I32", [M]))
+        ops.norm_mod_act_gate(xt, norm, up(dev, w, "F32", [C]) if w is not None else None, None, 1e-5, tb, act,
+                              up(dev, res, "BF16", [M, C]), out)
+        if act == o.ACT_NONE:
+            assert_bits_equal(out.to_numpy(), want, kind)
+        else:
+            assert_close_16(out.to_numpy(), want, o.BF16, kind, max_frac=5e-3)
+    elif kind == "rms_mod_f32":
+        w = weight(47, C)
+        sc = (0.5 * np.random.default_rng(48).standard_normal((R, C))).astype(np.float32)
+        sh = (0.5 * np.random.default_rng(49).standard_normal((R, C))).astype(np.float32)
+        want = o.rms_norm_mod(x, o.BF16, M, C, w, 1e-6, rows, sc, sh, o.BF16)
+        m = ops.Mod(up(dev, rows, "I32", [M]), up(dev, sc, "F32", [R, C]), up(dev, sh, "F32", [R, C]))
+        ops.rms_norm_mod(xt, up(dev, w, "F32", [C]), 1e-6, m, out)
+        assert_bits_equal(out.to_numpy(), want, kind)
+    else:
+        w, b = weight(50, C), (0.1 * np.random.default_rng(51).standard_normal(C)).astype(np.float32)
+        want = o.layer_norm(x, o.BF16, M, C, w, b, 1e-5, o.BF16)
+        ops.layer_norm(xt, C, up(dev, w, "F32", [C]), up(dev, b, "F32", [C]), 1e-5, out)
+        assert_bits_equal(out.to_numpy(), want, kind)
+
+
 # ---- h3s_int8_linear and h3s_int8_gemm_dequant (kernels/h3sycl.cpp:404-652) ----
 @pytest.mark.parametrize("M,K,N", [(1, 64, 5), (300, 256, 300), (257, 4096, 129), (64, 1024, 512), (33, 320, 70)])
 @pytest.mark.parametrize("group", [0, 4, 16, 64, 256])
