@@ -54,6 +54,7 @@ M2 = 16 * 24 * 44          # 16896 tokens (T16 x H24 x W44)
 M4 = 47104
 C = 4096
 HEADLINE = "cfg2_ln_mod_gelu_gate_16896"
+CFG1_COPY_ELEMS = (2159 * C * 2 + 2159 * C + 2159 * 4) // 4      # bf16 elements: read + write = config 1's bytes
 
 
 def bytes_cfg():
@@ -75,6 +76,8 @@ def bytes_cfg():
         "attn_sage_16896x32x128": 4 * M2 * 4096 * 2,     # q, k, v read, out written (the products are the bound)
         "attn_sage_47104x32x128": 4 * M4 * 4096 * 2,
         "copy_probe_1GiB": 2 << 30,
+        # a plain copy moving config 1's bytes (half read, half written): the floor a launch of that size reaches
+        "copy_probe_cfg1_bytes": 2 * CFG1_COPY_ELEMS * 2,
     }
 
 
@@ -317,7 +320,9 @@ def main() -> int:
     layer = ops.Int8Linear(T(w5), T(ws5))
     out5 = torch.empty(M4, 16384, dtype=torch.bfloat16, device=dev_t)
     O5 = T(out5)
-    run("cfg5b_int8_gemm_silu_47104x16384", lambda: (lambda: ops.int8_gemm_dequant(Q5, S5, layer, A.ACT_SILU, O5)), 5)
+    # the GEMM's output, the [gate | up] rows the MLP's middle reads: one untimed call here; the GEMM is timed after
+    # every HBM-bound kernel, since a third of a second of it lowers the clock of the kernels timed right after it
+    ops.int8_gemm_dequant(Q5, S5, layer, A.ACT_SILU, O5)
 
     # ---- the MLP's middle: swiglu of fc1's [gate | up] output [47104 x 2*8192] -> fc2's quantizer (regular g 256) ----
     def make6():
@@ -336,6 +341,9 @@ def main() -> int:
     run("cfg4_rmsnorm_wht128_quant_16896", make4(M2))
     run("cfg5a_rmsnorm_mod_quant_16896", make5a(M2))
 
+    # ---- the compute-bound kernels, last: config 5b's int8 GEMM, then attention ----
+    run("cfg5b_int8_gemm_silu_47104x16384", lambda: (lambda: ops.int8_gemm_dequant(Q5, S5, layer, A.ACT_SILU, O5)), 5)
+
     # ---- attention of the 16896-token grid, 32 heads of 128 (the int8 form: S >= 8192), and at 47104 tokens ----
     def make_attn(M):
         def make():
@@ -353,6 +361,12 @@ def main() -> int:
             dst = torch.empty_like(src)
             return lambda: dst.copy_(src)
         run("copy_probe_1GiB", make_copy, 20)
+
+        def make_copy1():
+            src = torch.empty(CFG1_COPY_ELEMS, dtype=torch.bfloat16, device=dev_t).fill_(1.0)
+            dst = torch.empty_like(src)
+            return lambda: dst.copy_(src)
+        run("copy_probe_cfg1_bytes", make_copy1, 200)
 
     per = {}
     for k, ms in kernels.items():
@@ -600,6 +614,19 @@ def summarize_pmc(paths, bench_json: str) -> str:
                 ns = dur.get(w)
                 ghz = f"{g / ns:.2f}" if ns else "n/a"
                 t.append(f"| {w} | {g:,.0f} | {ghz} | {per_launch[w]['SQ_VALU_MFMA_BUSY_CYCLES'] / (g * cus * 4):.4f} |")
+        out += "\n" + "\n".join(t)
+    if {"SQ_INSTS_VALU", "SQ_ACTIVE_INST_VALU", "SQ_WAVES", "GRBM_GUI_ACTIVE"} <= set(counters):
+        # VALU issue: instructions per wavefront, and the profiler's VALUBusy for gfx950,
+        # SQ_ACTIVE_INST_VALU / (CUs x kernel cycles): near or above 1 the kernel is bound by VALU issue, not by HBM
+        xcds = int(b.get("xcds", 8))
+        t = [f"\n| workload | wavefronts | VALU instructions per wavefront | VALU busy (SQ_ACTIVE_INST_VALU / ({cus} CUs x "
+             f"GRBM_GUI_ACTIVE / {xcds})) |", "|---|---:|---:|---:|"]
+        for w in vals:
+            pl = per_launch[w]
+            g = pl.get("GRBM_GUI_ACTIVE", 0) / xcds
+            if g and pl.get("SQ_WAVES"):
+                t.append(f"| {w} | {pl['SQ_WAVES']:,.0f} | {pl['SQ_INSTS_VALU'] / pl['SQ_WAVES']:,.0f} | "
+                         f"{pl['SQ_ACTIVE_INST_VALU'] / (cus * g):.3f} |")
         out += "\n" + "\n".join(t)
     return out
 
