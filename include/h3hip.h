@@ -89,16 +89,20 @@ int h3s_upload_wait(void* ctx);
 int h3s_int8_linear(void* ctx, const void* x, int x_dt, int64_t M, int64_t K, const int8_t* w, int64_t N,
                     const float* wscale, int64_t n_wscale, const float* bias, void* out, int out_dt, int group);
 
-/* Not implemented here (float GEMMs, weight prep): -1. Replace kernels/h3sycl.h:89-95. */
+/* Float linear layers (kernels/h3sycl.h:89-95): h3s_linear out = x w^T + bias, h3s_linear_acc out += x w^T + bias,
+ * h3s_scale_rows x[r] *= s[r]. The products run on rocBLAS (float32 accumulation, the context's stream); the bias and
+ * the old output are added in float32 and rounded once to the output type. */
 int h3s_linear_acc(void* ctx, const void* x, int dt, int64_t M, int64_t K, const void* w, int64_t N, const float* bias, void* out);
 int h3s_scale_rows(void* ctx, void* x, int dt, int64_t M, int64_t C, const float* s);
 int h3s_linear(void* ctx, const void* x, int dt, int64_t M, int64_t K, const void* w, int64_t N, const float* bias,
                void* out, int out_dt);
 
-/* Not implemented here (text encoder, upscalers, audio): -1. Replace kernels/h3sycl.h:106-158. */
-int h3s_dequant(void* ctx, const void* src, int qtype, int64_t n, void* out, int out_dt);
+/* Causal attention with grouped heads (kernels/h3sycl.h:104-108): Hq query heads over Hkv key/value heads, rows of
+ * q at stride qs and of k, v at stride kvs; the 16-bit form. Head sizes 64 and 128. */
 int h3s_attention_causal(void* ctx, const void* q, const void* k, const void* v, int dt, int64_t L, int64_t Hq, int64_t Hkv, int64_t D,
                          int64_t qs, int64_t kvs, void* out);
+/* Not implemented here (text encoder, upscalers, audio): -1. Replace kernels/h3sycl.h:106-158. */
+int h3s_dequant(void* ctx, const void* src, int qtype, int64_t n, void* out, int out_dt);
 int h3s_conv3d(void* ctx, const void* x, int dt, int64_t T, int64_t H, int64_t W, int64_t Ci, const void* w, int64_t Co, int64_t k,
                const float* bias, void* out);
 int h3s_group_norm_silu(void* ctx, const void* x, int dt, int64_t F, int64_t N, int64_t C, int64_t G, const float* weight, const float* bias,
@@ -136,8 +140,9 @@ int h3s_layer_norm(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, con
 int h3s_rms_norm_mod(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, const float* weight, float eps,
                      const int32_t* rows, const float* scale, const float* shift, void* out, int out_dt);
 /* Per-head RMS norm, then the rotary rotation of pairs (i, rot_dim/2 + i) by cs float32 [M, rot_dim/2, 2], in place;
- * row m at element m * stride. Replaces kernels/h3sycl.h:173-174. Here rot_dim/2 and D - rot_dim must be whole
- * 16-byte vectors. */
+ * row m at element m * stride. Replaces kernels/h3sycl.h:173-174. Any even rot_dim <= D that leaves an even
+ * remainder, as the reference; D and the stride must be whole 16-byte vectors (8 elements of a 16-bit type, 4 of
+ * float32), and a head at most 64 16-byte slots. */
 int h3s_rms_rope(void* ctx, void* x, int x_dt, int64_t M, int64_t H, int64_t D, int64_t stride, const float* weight,
                  float eps, const float* cs, int rot_dim);
 /* out[r, i] = silu(x[r, i]) * x[r, C + i]. Replaces kernels/h3sycl.h:178. */
@@ -146,7 +151,10 @@ int h3s_swiglu(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, void* o
 int h3s_gate_add(void* ctx, void* x, int x_dt, int64_t M, int64_t C, const void* other, int other_dt,
                  const int32_t* rows, const float* gate);
 
-/* Not implemented here (attention): -1. Replace kernels/h3sycl.h:190-200. */
+/* Attention over S tokens of H heads of D (64 or 128), rows at element stride `stride`, out [S, H D] (h3s_attention),
+ * and B independent sequences of S tokens each (h3s_attention_batch). The reference's choice of form: the int8
+ * (SageAttention) form from H3S_SAGE_MIN_S tokens (8192) on unless H3S_ATTN=onednn, the 16-bit form below it.
+ * Replace kernels/h3sycl.h:190-200. */
 int h3s_attention(void* ctx, const void* q, const void* k, const void* v, int dt, int64_t S, int64_t H, int64_t D,
                   int64_t stride, void* out, int out_dt);
 int h3s_attention_batch(void* ctx, const void* q, const void* k, const void* v, int dt, int64_t B, int64_t S, int64_t H,

@@ -1,6 +1,8 @@
 // attention.hip - h3s_attention, h3s_attention_batch (kernels/h3sycl.h:185-197, kernels/h3sycl.cpp:1433-1917) and
-// h3s_attention_causal (kernels/h3sycl.h:104-108) on the kernels of attn_impl.h. The form follows the reference's choice: the int8 (SageAttention) form for sequences of
-// at least H3S_SAGE_MIN_S tokens (8192) unless H3S_ATTN=onednn, the 16-bit form otherwise. Head sizes 64 and 128.
+// h3s_attention_causal (kernels/h3sycl.h:104-108) on the kernels of attn_impl.h. The form follows the reference's
+// choice: the int8 (SageAttention) form for sequences of at least H3S_SAGE_MIN_S tokens (8192) unless
+// H3S_ATTN=onednn, the 16-bit form otherwise. Any head size up to 256 (the causal form's limit, h3sycl.cpp:877): a
+// head runs in the kernel of 64, 128 or 256 features, zero-padded past D.
 #include <cmath>
 #include <cstdio>
 
@@ -8,33 +10,38 @@
 
 namespace h3 {
 
-// q of Hq heads (row stride qs) and k, v of Hkv heads (row stride kvs) prepared into aq [Hq, Sp, D], ak [Hkv, Sp, D]
-// (int8 codes with their scales for SAGE, else half) and av [Hkv, D, Sp] (half)
+// q of Hq heads (row stride qs) and k, v of Hkv heads (row stride kvs) prepared into aq [Hq, Sp, DK], ak [Hkv, Sp, DK]
+// (int8 codes with their scales for SAGE, else half) and av [Hkv, DK, Sp] (half), DK = attn_dk(D), zero past D
 template <int DT>
 static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S, int64_t Sp, int64_t Hq, int64_t Hkv, int D,
                  int64_t qs_stride, int64_t kv_stride, bool sage, int8_t* aq, int8_t* ak, uint16_t* av, float* qs, float* ks,
                  float* km) {
     const unsigned qblocks = (unsigned) (Hq * (Sp / kAttnRows)), kvblocks = (unsigned) (Hkv * (Sp / kAttnRows));
-    // 16-byte rows: every tensor aligned and the strides whole numbers of 16-byte vectors
+    const int DK = attn_dk(D);
+    // 16-byte rows: every tensor aligned, the strides whole numbers of 16-byte vectors, and a head of exactly 64, 128
+    // or 256 features (no padding)
     const bool vec = aligned16(q) && aligned16(k) && aligned16(v) && (qs_stride * elem_size(DT)) % 16 == 0 &&
-                     (kv_stride * elem_size(DT)) % 16 == 0;
+                     (kv_stride * elem_size(DT)) % 16 == 0 && D == DK;
     auto qk = [&](const void* src, int64_t stride, unsigned blocks, const float* mean, int8_t* dst, float* sc) {
 #define H3_QK(SG, DD) attn_qk_prep_vec_kernel<DT, SG, DD><<<blocks, 256, 0, c->stream>>>(src, S, Sp, stride, mean, dst, sc)
         if (!vec) {
-            if (sage) attn_qk_prep_kernel<DT, true><<<blocks, 256, 0, c->stream>>>(src, S, Sp, D, stride, mean, dst, sc);
-            else attn_qk_prep_kernel<DT, false><<<blocks, 256, 0, c->stream>>>(src, S, Sp, D, stride, mean, dst, sc);
+            if (sage) attn_qk_prep_kernel<DT, true><<<blocks, 256, 0, c->stream>>>(src, S, Sp, D, DK, stride, mean, dst, sc);
+            else attn_qk_prep_kernel<DT, false><<<blocks, 256, 0, c->stream>>>(src, S, Sp, D, DK, stride, mean, dst, sc);
         } else if (sage) {
-            if (D == 128) H3_QK(true, 128);
+            if (D == 256) H3_QK(true, 256);
+            else if (D == 128) H3_QK(true, 128);
             else H3_QK(true, 64);
         } else {
-            if (D == 128) H3_QK(false, 128);
+            if (D == 256) H3_QK(false, 256);
+            else if (D == 128) H3_QK(false, 128);
             else H3_QK(false, 64);
         }
 #undef H3_QK
     };
     if (sage) {
+        // k's mean per (head, feature) of the D features; the 16-byte form takes 32 features a block
         const int64_t hd = Hkv * D;
-        if (vec) attn_kmean_kernel<DT><<<(unsigned) (hd / kKmeanFeat), 256, 0, c->stream>>>(k, S, kv_stride, km);
+        if (vec && hd % kKmeanFeat == 0) attn_kmean_kernel<DT><<<(unsigned) (hd / kKmeanFeat), 256, 0, c->stream>>>(k, S, kv_stride, km);
         else attn_kmean_rows_kernel<DT><<<(unsigned) ((hd + 255) / 256), 256, 0, c->stream>>>(k, S, hd, kv_stride, km);
         qk(q, qs_stride, qblocks, nullptr, aq, qs);
         qk(k, kv_stride, kvblocks, km, ak, ks);
@@ -42,7 +49,8 @@ static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S,
         qk(q, qs_stride, qblocks, nullptr, aq, nullptr);
         qk(k, kv_stride, kvblocks, nullptr, ak, nullptr);
     }
-    if (!vec) attn_v_prep_kernel<DT><<<kvblocks, 256, 0, c->stream>>>(v, S, Sp, D, kv_stride, av);
+    if (!vec) attn_v_prep_kernel<DT><<<kvblocks, 256, 0, c->stream>>>(v, S, Sp, D, DK, kv_stride, av);
+    else if (D == 256) attn_v_prep_vec_kernel<DT, 256><<<kvblocks, 256, 0, c->stream>>>(v, S, Sp, kv_stride, av);
     else if (D == 128) attn_v_prep_vec_kernel<DT, 128><<<kvblocks, 256, 0, c->stream>>>(v, S, Sp, kv_stride, av);
     else attn_v_prep_vec_kernel<DT, 64><<<kvblocks, 256, 0, c->stream>>>(v, S, Sp, kv_stride, av);
 }
@@ -53,11 +61,11 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
                          int64_t Hkv, int64_t D, int64_t qs_stride, int64_t kv_stride, void* out, int out_dt, bool causal) {
     const bool sage = !causal && c->sage_want && S >= c->sage_min_s;
     const int64_t Sp = (S + kAttnQBlock - 1) / kAttnQBlock * kAttnQBlock, nbp = Sp / kAttnRows;
-    const int64_t esz = sage ? 1 : 2;
+    const int64_t esz = sage ? 1 : 2, DK = attn_dk(D);
     if (Hq * (Sp / kAttnQBlock) > 0x7fffffff) return fail(std::string(fn) + ": too many query blocks");
-    int8_t* aq = c->scratch<int8_t>(Ctx::ATT_Q, (size_t) (Sp * Hq * D * esz));
-    int8_t* ak = c->scratch<int8_t>(Ctx::ATT_K, (size_t) (Sp * Hkv * D * esz));
-    uint16_t* av = c->scratch<uint16_t>(Ctx::ATT_V, (size_t) (Sp * Hkv * D));
+    int8_t* aq = c->scratch<int8_t>(Ctx::ATT_Q, (size_t) (Sp * Hq * DK * esz));
+    int8_t* ak = c->scratch<int8_t>(Ctx::ATT_K, (size_t) (Sp * Hkv * DK * esz));
+    uint16_t* av = c->scratch<uint16_t>(Ctx::ATT_V, (size_t) (Sp * Hkv * DK));
     float* af = c->scratch<float>(Ctx::ATT_AUX, (size_t) ((Hq + Hkv) * nbp + Hkv * D));
     if (!aq || !ak || !av || !af) return -1;
     float *qs = af, *ks = af + Hq * nbp, *km = af + (Hq + Hkv) * nbp;
@@ -73,22 +81,30 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
     P.q = aq; P.k = ak; P.vt = av; P.qs = qs; P.ks = ks;
     P.S = S; P.Sp = Sp; P.H = Hq;
     P.c = (float) (1.4426950408889634 * (double) (1.0f / std::sqrt((float) D)));
-    P.out = out; P.out_dt = out_dt;
+    P.out = out; P.out_dt = out_dt; P.D = (int) D;
     P.nqb = (int) (Sp / kAttnQBlock);
     P.kvdiv = (int) (Hq / Hkv);
     P.Spk = Sp;
     const unsigned grid = (unsigned) (Hq * P.nqb);
     timer.mark();
-    if (causal) {
-        if (D == 128) attn_kernel<false, 128, true><<<grid, 256, 0, c->stream>>>(P);
-        else attn_kernel<false, 64, true><<<grid, 256, 0, c->stream>>>(P);
-    } else if (sage) {
-        if (D == 128) attn_kernel<true, 128><<<grid, 256, 0, c->stream>>>(P);
-        else attn_kernel<true, 64><<<grid, 256, 0, c->stream>>>(P);
-    } else {
-        if (D == 128) attn_kernel<false, 128><<<grid, 256, 0, c->stream>>>(P);
-        else attn_kernel<false, 64><<<grid, 256, 0, c->stream>>>(P);
+    // heads of 64, 128 or 256 features into an aligned out take the plain stores; others the masked ones
+    const bool pad = D != DK || !aligned16(out);
+#define H3_ATTN_D(SG, DD, CA)                                                                  \
+    {                                                                                          \
+        if (pad) attn_kernel<SG, DD, CA, true><<<grid, 256, 0, c->stream>>>(P);               \
+        else attn_kernel<SG, DD, CA, false><<<grid, 256, 0, c->stream>>>(P);                  \
     }
+#define H3_ATTN(SG, CA)                                                                        \
+    {                                                                                          \
+        if (DK == 256) H3_ATTN_D(SG, 256, CA)                                                  \
+        else if (DK == 128) H3_ATTN_D(SG, 128, CA)                                             \
+        else H3_ATTN_D(SG, 64, CA)                                                             \
+    }
+    if (causal) H3_ATTN(false, true)
+    else if (sage) H3_ATTN(true, false)
+    else H3_ATTN(false, false)
+#undef H3_ATTN
+#undef H3_ATTN_D
     if (launched(fn)) return -1;
     timer.mark();
     const std::vector<float> ms = timer.elapsed();
@@ -103,7 +119,7 @@ static int attention_checks(const char* fn, int dt, int64_t H, int64_t D, int64_
                             const void* k, const void* v, const void* out) {
     if (stride < H * D) return fail(std::string(fn) + ": the row stride is shorter than a row");
     if (!dt_ok(dt) || !dt_ok(out_dt)) return fail(std::string(fn) + ": unknown element type");
-    if (D != 64 && D != 128) return fail(std::string(fn) + ": head size " + std::to_string(D) + " (64 or 128 only)");
+    if (D > kAttnMaxD) return fail(std::string(fn) + ": head size " + std::to_string(D) + " (at most 256)");
     if (!q || !k || !v || !out) return fail(std::string(fn) + ": q, k, v and out are required");
     return 0;
 }
@@ -142,13 +158,13 @@ H3S_EXPORT int h3s_attention_batch(void* ctx, const void* q, const void* k, cons
 
 // The text encoder's causal attention with grouped key/value heads (kernels/h3sycl.h:104-108, kernels/h3sycl.cpp:873-898):
 // q rows of stride qs (Hq heads), k and v rows of stride kvs (Hkv heads), head h reads kv head h / (Hq / Hkv); out
-// [L, Hq * D] in dt. The 16-bit form with a causal mask; head sizes 64 and 128 (the reference takes D <= 256).
+// [L, Hq * D] in dt. The 16-bit form with a causal mask; any head size up to 256, as the reference.
 H3S_EXPORT int h3s_attention_causal(void* ctx, const void* q, const void* k, const void* v, int dt, int64_t L, int64_t Hq,
                                     int64_t Hkv, int64_t D, int64_t qs, int64_t kvs, void* out) try {
     const char* fn = "h3s_attention_causal";
-    if (L <= 0) return 0;
+    if (L <= 0 || D <= 0) return 0;
     if (Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0) return fail(std::string(fn) + ": Hq must be a multiple of Hkv");
-    if (D != 64 && D != 128) return fail(std::string(fn) + ": head size " + std::to_string(D) + " (64 or 128 only)");
+    if (D > kAttnMaxD) return fail(std::string(fn) + ": D <= 256, Hq a multiple of Hkv (head size " + std::to_string(D) + ")");
     if (qs < Hq * D || kvs < Hkv * D) return fail(std::string(fn) + ": a row stride is shorter than a row");
     if (!dt_ok(dt)) return fail(std::string(fn) + ": unknown element type");
     if (!q || !k || !v || !out) return fail(std::string(fn) + ": q, k, v and out are required");

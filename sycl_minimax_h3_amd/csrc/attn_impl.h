@@ -6,8 +6,9 @@
 // Both: v in IEEE half, the softmax online in float32 (base 2), P in half, P v on the f16 matrix cores, the result
 // divided by the row sum, rounded to half (the reference's result buffer is half) and stored in out's type.
 //
-// Layouts (prepared once per call, in the context's scratch): codes or halves of q and k [H, Sp, D], v transposed to
-// half [H, D, Sp], Sp = S rounded up to 128 with zero rows. One block = 4 wavefronts = 128 queries of one head; a
+// Layouts (prepared once per call, in the context's scratch): codes or halves of q and k [H, Sp, DK], v transposed to
+// half [H, DK, Sp], Sp = S rounded up to 128 with zero rows, DK = the head size D rounded up to 64, 128 or 256 with zero
+// features (which change no score and no block max); the output keeps the D features. One block = 4 wavefronts = 128 queries of one head; a
 // wavefront owns 32 queries and walks all keys 64 at a time. Per 64-key tile:
 //   S^T = K Q^T:  v_mfma_i32_32x32x32_i8 (or f32_32x32x16_f16) with K as the first operand, so every lane ends with
 //                 scores of one query (lane % 32) for 32 of the 64 keys (the other 32 in lane ^ 32);
@@ -17,8 +18,8 @@
 //                 after one v_permlane32_swap per register pair (each lane then holds 8 consecutive keys).
 // K and V^T tiles go global -> LDS by direct loads (global_load_lds_dwordx4) into two stages, the next tile in flight
 // while this one is computed. Tile rows are R bytes long (R / 16 chunks); chunk c of row r sits at chunk
-// c ^ ((r / (16 / (R / 16))) % (R / 16)) of its row, so the 16-byte fragment reads of 16 consecutive rows hit distinct
-// banks.
+// c ^ ((r / max(1, 16 / (R / 16))) % (R / 16)) of its row, so the 16-byte fragment reads of 16 consecutive rows hit
+// distinct banks.
 #pragma once
 
 #include <type_traits>
@@ -36,6 +37,9 @@ constexpr h2_a h2_one = {(_Float16) 1.0f, (_Float16) 1.0f};
 
 constexpr int kAttnRows = 64;            // the reference's scale block (kSageBlock, h3sycl.cpp:1681) and the key tile
 constexpr int kAttnQBlock = 128;         // queries of a block
+constexpr int kAttnMaxD = 256;           // the largest head: heads of D features run in kernels of 64, 128 or 256
+// the kernel head size of a head of D features (D <= kAttnMaxD)
+inline int attn_dk(int64_t D) { return D <= 64 ? 64 : D <= 128 ? 128 : 256; }
 
 // ---- preparation ----
 template <int DT> __device__ __forceinline__ float attn_elem(const void* p, int64_t i) {
@@ -149,20 +153,21 @@ __global__ __launch_bounds__(256) void attn_kmean_rows_kernel(const void* __rest
 }
 
 // q or k (- mean) of one head and 64 rows: SAGE to int8 codes with the block's scale (h3sycl.cpp:1735-1754), else to
-// half; rows past S become zeros (and a block entirely past S gets scale 0)
+// half; rows past S become zeros (and a block entirely past S gets scale 0). The head's D features land in a prepared
+// row of DK >= D (the kernel's head size), zero past D: zeros change neither a score nor a block's max.
 template <int DT, bool SAGE>
-__global__ __launch_bounds__(256) void attn_qk_prep_kernel(const void* __restrict__ src, int64_t S, int64_t Sp, int D,
+__global__ __launch_bounds__(256) void attn_qk_prep_kernel(const void* __restrict__ src, int64_t S, int64_t Sp, int D, int DK,
                                                            int64_t stride, const float* __restrict__ mean,
                                                            int8_t* __restrict__ dst, float* __restrict__ scales) {
     __shared__ float red[4];
     const int64_t nbp = Sp / kAttnRows, b = blockIdx.x % nbp, h = blockIdx.x / nbp, r0 = b * kAttnRows;
-    const int tid = threadIdx.x, n = kAttnRows * D;
+    const int tid = threadIdx.x, n = kAttnRows * DK;
     const int64_t base = r0 * stride + h * D;
     if constexpr (SAGE) {
         float m = 0.0f;
         for (int e = tid; e < n; e += 256) {
-            const int r = e / D, d = e % D;
-            if (r0 + r < S) m = fmaxf(m, fabsf(attn_elem<DT>(src, base + r * stride + d) - (mean ? mean[h * D + d] : 0.0f)));
+            const int r = e / DK, d = e % DK;
+            if (r0 + r < S && d < D) m = fmaxf(m, fabsf(attn_elem<DT>(src, base + r * stride + d) - (mean ? mean[h * D + d] : 0.0f)));
         }
         m = wave_max<64>(m);
         if ((tid & 63) == 0) red[tid >> 6] = m;
@@ -171,19 +176,20 @@ __global__ __launch_bounds__(256) void attn_qk_prep_kernel(const void* __restric
         const float inv = m > 0.0f ? 127.0f / m : 0.0f;
         if (tid == 0) scales[h * nbp + b] = m / 127.0f;
         for (int e = tid; e < n; e += 256) {
-            const int r = e / D, d = e % D;
+            const int r = e / DK, d = e % DK;
             float c = 0.0f;
-            if (r0 + r < S) {
+            if (r0 + r < S && d < D) {
                 c = roundf((attn_elem<DT>(src, base + r * stride + d) - (mean ? mean[h * D + d] : 0.0f)) * inv);
                 c = fminf(fmaxf(c, -127.0f), 127.0f);
             }
-            dst[(h * Sp + r0 + r) * D + d] = (int8_t) c;
+            dst[(h * Sp + r0 + r) * DK + d] = (int8_t) c;
         }
     } else {
         uint16_t* d16 = reinterpret_cast<uint16_t*>(dst);
         for (int e = tid; e < n; e += 256) {
-            const int r = e / D, d = e % D;
-            d16[(h * Sp + r0 + r) * D + d] = r0 + r < S ? half_bits(attn_elem<DT>(src, base + r * stride + d)) : (uint16_t) 0;
+            const int r = e / DK, d = e % DK;
+            d16[(h * Sp + r0 + r) * DK + d] =
+                r0 + r < S && d < D ? half_bits(attn_elem<DT>(src, base + r * stride + d)) : (uint16_t) 0;
         }
     }
 }
@@ -288,21 +294,21 @@ __global__ __launch_bounds__(256) void attn_v_prep_vec_kernel(const void* __rest
     }
 }
 
-// v of one head and 64 tokens to half, transposed: vt [H, D, Sp]; tokens past S become zeros
+// v of one head and 64 tokens to half, transposed: vt [H, DK, Sp]; tokens past S and features past D become zeros
 template <int DT>
-__global__ __launch_bounds__(256) void attn_v_prep_kernel(const void* __restrict__ v, int64_t S, int64_t Sp, int D,
+__global__ __launch_bounds__(256) void attn_v_prep_kernel(const void* __restrict__ v, int64_t S, int64_t Sp, int D, int DK,
                                                           int64_t stride, uint16_t* __restrict__ vt) {
-    __shared__ uint16_t tile[kAttnRows * (128 + 2)];
+    __shared__ uint16_t tile[kAttnRows * (kAttnMaxD + 2)];
     const int64_t nbp = Sp / kAttnRows, b = blockIdx.x % nbp, h = blockIdx.x / nbp, t0 = b * kAttnRows;
-    const int tid = threadIdx.x, n = kAttnRows * D, pitch = D + 2;
+    const int tid = threadIdx.x, n = kAttnRows * DK, pitch = DK + 2;
     for (int e = tid; e < n; e += 256) {
-        const int t = e / D, d = e % D;
-        tile[t * pitch + d] = t0 + t < S ? half_bits(attn_elem<DT>(v, (t0 + t) * stride + h * D + d)) : (uint16_t) 0;
+        const int t = e / DK, d = e % DK;
+        tile[t * pitch + d] = t0 + t < S && d < D ? half_bits(attn_elem<DT>(v, (t0 + t) * stride + h * D + d)) : (uint16_t) 0;
     }
     __syncthreads();
     for (int e = tid; e < n; e += 256) {
         const int d = e / kAttnRows, t = e % kAttnRows;
-        vt[(h * D + d) * Sp + t0 + t] = tile[t * pitch + d];
+        vt[(h * DK + d) * Sp + t0 + t] = tile[t * pitch + d];
     }
 }
 
@@ -317,13 +323,18 @@ struct AttnArgs {
     float c;                  // log2(e) * fl(1 / sqrt(D)): scores in base 2
     void* out;                // [S, H * D]
     int out_dt;
+    int D;                    // the heads' features (the kernel's DK of them are prepared, zero past D)
     int nqb;                  // blocks of 128 queries per head
     int kvdiv;                // query heads per key/value head: head h reads k and v of head h / kvdiv
     int64_t Spk;              // rows of the prepared k and v^T (Sp unless they come from another sequence)
 };
 
-// the chunk of row r (rows of CPR 16-byte chunks) where logical chunk c is stored
-template <int CPR> __device__ __forceinline__ int attn_swz(int r, int c) { return c ^ ((r / (16 / CPR)) % CPR); }
+// the chunk of row r (rows of CPR 16-byte chunks) where logical chunk c is stored: rows of fewer than 16 chunks
+// change the pattern every 16 / CPR rows, longer rows every row
+template <int CPR> __device__ __forceinline__ int attn_swz(int r, int c) {
+    constexpr int RPS = CPR >= 16 ? 1 : 16 / CPR;
+    return c ^ ((r / RPS) % CPR);
+}
 
 // {x of this lane, x of lane ^ 32} in some order
 __device__ __forceinline__ float attn_pair_max(float x) {
@@ -335,11 +346,13 @@ __device__ __forceinline__ float attn_pair_sum(float x) {
     return __int_as_float(r[0]) + __int_as_float(r[1]);
 }
 
-template <bool SAGE, int D, bool CAUSAL = false>
-__global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
-    constexpr int ESZ = SAGE ? 1 : 2, RB = D * ESZ, CPR = RB / 16, NQF = RB / 32;
-    constexpr int KTB = kAttnRows * RB, VTB = D * kAttnRows * 2, STAGE = KTB + VTB;
-    constexpr int NDT = D / 32;                               // 32-row tiles of V^T (32 features each)
+// PAD: heads of D < DK features, or rows of out not on 16-byte boundaries: the output stores only features below D,
+// four at a time where they stay aligned
+template <bool SAGE, int DK, bool CAUSAL = false, bool PAD = false>
+__global__ __launch_bounds__(256, DK == 256 ? 1 : 3) void attn_kernel(AttnArgs P) {
+    constexpr int ESZ = SAGE ? 1 : 2, RB = DK * ESZ, CPR = RB / 16, NQF = RB / 32;
+    constexpr int KTB = kAttnRows * RB, VTB = DK * kAttnRows * 2, STAGE = KTB + VTB;
+    constexpr int NDT = DK / 32;                               // 32-row tiles of V^T (32 features each)
     __shared__ __attribute__((aligned(16))) int8_t lds[2 * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hl = lane >> 5, ql = lane & 31;
     const int64_t h = blockIdx.x / P.nqb, qb = blockIdx.x % P.nqb, Sp = P.Sp, S = P.S;
@@ -352,16 +365,16 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
     // this lane's query fragments (second operand of the score products), held for the whole key walk
     v4i_a qf[NQF];
     {
-        const int8_t* qrow = P.q + ((h * Sp + q0 + ql) * D) * ESZ;
+        const int8_t* qrow = P.q + ((h * Sp + q0 + ql) * DK) * ESZ;
 #pragma unroll
         for (int kk = 0; kk < NQF; ++kk) qf[kk] = *reinterpret_cast<const v4i_a*>(qrow + 32 * kk + 16 * hl);
     }
     const float fq = SAGE ? P.qs[h * nbp + q0 / kAttnRows] * P.c : P.c;
 
-    // direct loads of key tile t into stage st: the K rows (64 x RB bytes) and the V^T rows (D x 128 bytes)
+    // direct loads of key tile t into stage st: the K rows (64 x RB bytes) and the V^T rows (DK x 128 bytes)
     const int64_t g = h / P.kvdiv, Spk = P.Spk;              // the key/value head and its rows
     const int8_t* kbase = P.k + g * Spk * RB;
-    const uint16_t* vbase = P.vt + g * D * Spk;
+    const uint16_t* vbase = P.vt + g * DK * Spk;
     auto issue = [&](int t, int st) {
         int8_t* s = lds + st * STAGE;
         constexpr int KI = CPR / 4;                            // K instructions a wavefront
@@ -372,7 +385,7 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) gk,
                                              (__attribute__((address_space(3))) void*) (s + 1024 * i), 16, 0, 0);
         }
-        constexpr int VI = D / 32;                              // V^T instructions a wavefront (D * 8 units / 64 / 4)
+        constexpr int VI = DK / 32;                              // V^T instructions a wavefront (DK * 8 units / 64 / 4)
 #pragma unroll
         for (int j = 0; j < VI; ++j) {
             const int i = wave * VI + j, u = 64 * i + lane, r = u / 8, c = attn_swz<8>(r, u % 8);
@@ -498,26 +511,38 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(AttnArgs P) {
     for (int t = 0; t < full; ++t) step(t, std::false_type{});
     for (int t = full; t < ntiles; ++t) step(t, std::true_type{});
 
-    // ---- out = O / l, rounded to half, in out's type ----
+    // ---- out = O / l, rounded to half, in out's type: the head's D features (of the DK computed) ----
     const float inv = 1.0f / attn_pair_sum(l);
     const int64_t qi = q0 + ql;
     if (qi < S) {
-        const int esz = P.out_dt == H3S_F32 ? 4 : 2;
+        const int esz = P.out_dt == H3S_F32 ? 4 : 2, D = PAD ? P.D : DK;
         char* orow = reinterpret_cast<char*>(P.out) + ((qi * P.H + h) * D) * esz;
+        // four features a store when D keeps every group of four on a 4-element boundary, else one at a time
+        const bool quads = !PAD || (D % 4 == 0 && (reinterpret_cast<uintptr_t>(P.out) & 15) == 0);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 // registers 4 g .. 4 g + 3 of o[dt]: features 32 dt + 8 g + 4 hl + (0..3)
+                const int f0 = 32 * dt + 8 * g + 4 * hl;
+                if (PAD && f0 >= D) continue;
                 float v[4];
 #pragma unroll
                 // the reference's result buffer is half for the two forms of h3s_attention; its causal kernel stores
                 // acc / l straight into out's type
                 for (int i = 0; i < 4; ++i) v[i] = CAUSAL ? o[dt][4 * g + i] * inv : round_f16(o[dt][4 * g + i] * inv);
-                char* at = orow + (32 * dt + 8 * g + 4 * hl) * esz;
-                if (P.out_dt == H3S_F32) *reinterpret_cast<float4*>(at) = make_float4(v[0], v[1], v[2], v[3]);
-                else if (P.out_dt == H3S_BF16) *reinterpret_cast<uint2*>(at) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
-                else *reinterpret_cast<uint2*>(at) = make_uint2(pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
+                char* at = orow + f0 * esz;
+                if (quads) {
+                    if (P.out_dt == H3S_F32) *reinterpret_cast<float4*>(at) = make_float4(v[0], v[1], v[2], v[3]);
+                    else if (P.out_dt == H3S_BF16) *reinterpret_cast<uint2*>(at) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+                    else *reinterpret_cast<uint2*>(at) = make_uint2(pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
+                } else if constexpr (PAD) {
+                    for (int i = 0; i < 4 && f0 + i < D; ++i) {
+                        if (P.out_dt == H3S_F32) reinterpret_cast<float*>(at)[i] = v[i];
+                        else if (P.out_dt == H3S_BF16) reinterpret_cast<uint16_t*>(at)[i] = (uint16_t) pack_bf16(v[i], 0.0f);
+                        else reinterpret_cast<uint16_t*>(at)[i] = (uint16_t) pack_f16(v[i], 0.0f);
+                    }
+                }
             }
     }
 }

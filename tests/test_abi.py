@@ -121,8 +121,13 @@ def test_out_of_scope_entry_points_refuse(api):
     assert api.attention_causal(None, None, None, None, 2, 4, 3, 2, 64, 192, 128, None) == -1
     assert "multiple" in api.error()
     # attention's argument checks run before the context is looked at
+    assert api.attention(None, None, None, None, 2, 1, 1, 300, 300, None, 2) == -1
+    assert "at most 256" in api.error()
+    assert api.attention_causal(None, None, None, None, 2, 4, 2, 2, 257, 514, 514, None) == -1
+    assert "D <= 256" in api.error()
+    # any head size up to 256 passes the size check (and then needs its buffers)
     assert api.attention(None, None, None, None, 2, 1, 1, 96, 96, None, 2) == -1
-    assert "64 or 128" in api.error()
+    assert "required" in api.error()
     assert api.attention(None, None, None, None, 2, 1, 2, 64, 100, None, 2) == -1
     assert "stride" in api.error()
     assert api.conv3d(None, None, 2, 1, 1, 1, 1, None, 1, 3, None, None) == -1

@@ -156,6 +156,36 @@ def test_attention_causal(dev, dt, L, Hq, Hkv, D):
 
 
 def test_attention_refuses(dev):
-    p = new(dev, "BF16", [64, 96])
-    with pytest.raises(Error, match="64 or 128"):
-        ops.attention(ops.Rows(p, 0, 96, 64, 1, 96), ops.Rows(p, 0, 96, 64, 1, 96), ops.Rows(p, 0, 96, 64, 1, 96), p)
+    p = new(dev, "BF16", [64, 600])
+    with pytest.raises(Error, match="at most 256"):
+        ops.attention(ops.Rows(p, 0, 600, 64, 2, 300), ops.Rows(p, 0, 600, 64, 2, 300), ops.Rows(p, 0, 600, 64, 2, 300), p)
+
+
+@pytest.mark.parametrize("sage", [True, False])
+@pytest.mark.parametrize("S,H,D,pad,out_dt", [(200, 2, 256, 0, o.BF16), (130, 3, 96, 0, o.F32), (77, 2, 80, 8, o.BF16),
+                                               (65, 2, 32, 0, o.F16), (150, 1, 200, 2, o.F32), (64, 2, 7, 1, o.BF16),
+                                               (300, 1, 130, 0, o.BF16)])
+def test_attention_head_sizes(dev_sage, dev_16, sage, S, H, D, pad, out_dt):
+    """Heads of any size up to 256: 256 in its own kernel, the others zero-padded to 64, 128 or 256 features in the
+    preparation and stored at their own size (odd sizes one feature at a time)."""
+    stride = H * D + pad
+    q, k, v = qkv(110 + D, S, H, D, o.BF16, stride)
+    want = o.attention(q, k, v, o.BF16, S, H, D, stride, out_dt=out_dt, sage=sage)
+    want = want[0] if sage else want
+    got = run(dev_sage if sage else dev_16, q, k, v, o.BF16, S, H, D, stride, out_dt)
+    check(got, want, out_dt, f"{'int8' if sage else '16-bit'} S={S} H={H} D={D}")
+
+
+@pytest.mark.parametrize("dt", [o.BF16, o.F32])
+@pytest.mark.parametrize("L,Hq,Hkv,D", [(50, 4, 2, 256), (129, 2, 1, 80), (33, 6, 3, 200), (70, 2, 2, 36)])
+def test_attention_causal_head_sizes(dev, dt, L, Hq, Hkv, D):
+    """The causal form at the head sizes the reference takes (D <= 256, kernels/h3sycl.cpp:877)."""
+    qs, kvs = Hq * D, 2 * Hkv * D
+    g = np.random.default_rng(131 + D)
+    q = o.to_dt(g.standard_normal(L * qs).astype(np.float32), dt)
+    kv = o.to_dt(g.standard_normal(L * kvs).astype(np.float32), dt)
+    want = o.attention_causal(q, kv, kv[Hkv * D:], dt, L, Hq, Hkv, D, qs, kvs)
+    qt, kvt = up(dev, q, DTS[dt], [L, qs]), up(dev, kv, DTS[dt], [L, kvs])
+    out = new(dev, DTS[dt], [L, Hq * D])
+    ops.attention_causal(ops.Rows(qt, 0, qs, L, Hq, D), ops.Rows(kvt, 0, kvs, L, Hkv, D), ops.Rows(kvt, Hkv * D, kvs, L, Hkv, D), out)
+    check(out.to_numpy().ravel(), want, dt, f"causal L={L} Hq={Hq} Hkv={Hkv} D={D}")
