@@ -446,9 +446,10 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
 //
 // The side inputs every wavefront of the block shares live in LDS, laid out [j][half][lane][4 floats] so that a
 // wavefront's 16-byte reads are consecutive: the weight, and one decoded table row (1 + scale and shift), the
-// table row of the block's first row at the current step. When that changes (a segment boundary of rows[]), the
-// block re-decodes it between two barriers (every wavefront computes the same condition); a row whose own table
-// row differs from the cached one decodes its values from memory.
+// table row of the block's first row at the current step. A step whose rows all share that table row (every step
+// but those a segment boundary of rows[] cuts) is one round. Otherwise the block takes one round per distinct table
+// row of the step, in the order of its rows: between two barriers it re-decodes the cached row when the round's
+// differs, and the wavefronts whose rows use it run them (every wavefront takes the same rounds and barriers).
 template <int CPL> constexpr size_t quant_wave_side_bytes(int f) {
     return (size_t) ((f & ROW_W) ? 1 : 0) * CPL * 2048 + (size_t) ((f & ROW_TAB) ? 2 : 0) * CPL * 2048;
 }
