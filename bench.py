@@ -17,11 +17,15 @@ its inputs in the cache. The headline's back-to-back figure on one set is report
 Each kernel first runs untimed for 0.15 s (``--settle``; the clocks ramp up over the first milliseconds of load), then
 W warm-up launches, then the K timed launches, bracketed by HIP events on the stream the kernels run on (the library
 context wraps PyTorch's current stream, h3s_create). Inputs are already in HBM. The other fused kernels are timed the
-same way and reported under ``kernels``; the int8 GEMM also as int8 TOPS and attention against the mixed
-int8 / fp16 matrix peak. ``roofline.traffic`` is the headline kernel's HBM bytes per launch from the rocprofv3
-FETCH_SIZE / WRITE_SIZE runs summarized in profiles/hbm_traffic_pmc.md (each counter scaled by what it reads for a
-1 GiB device copy). ``cpu_baseline`` times the CPU oracle (the C restatement of the reference arithmetic) on the same
-workload on this host.
+same way and reported under ``kernels``; the int8 GEMM also as int8 TOPS and attention against the mixed int8 / fp16
+matrix peak. The compute-bound ones (the int8 GEMM, attention) are timed after the HBM-bound ones, whose clock a third
+of a second of the GEMM would lower. ``roofline.traffic`` is the headline kernel's HBM bytes per launch from the
+rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarized in profiles/hbm_traffic_pmc.md (each counter scaled by what it reads
+for a 1 GiB device copy). ``cpu_baseline`` times the CPU oracle (the C restatement of the reference arithmetic) on the
+same workload on this host.
+
+``--copy-probe`` also times two plain device copies: 1 GiB (the attainable streaming rate, and the known-size kernel
+that scales the byte counters) and config 1's 26.5 MB (the floor a launch of that size reaches from a cold cache).
 
 ``--mark`` launches a one-cycle spin kernel right before and right after each timed region (outside its HIP
 events), so a rocprofv3 trace of the run can be cut into exactly the timed dispatches of each workload; the bench
@@ -148,8 +152,8 @@ def main() -> int:
     ap.add_argument("--only", default="", help="comma list of workload keys to time (default all)")
     ap.add_argument("--mark", action="store_true", help="bracket each timed region with a spin-kernel marker")
     ap.add_argument("--copy-probe", action="store_true",
-                    help="also time a plain device copy of 1 GiB (the attainable HBM rate; the known-size kernel that "
-                         "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
+                    help="also time plain device copies of 1 GiB (the attainable HBM rate; the known-size kernel that "
+                         "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters) and of config 1's 26.5 MB")
     ap.add_argument("--summarize-trace", default="", help="a rocprofv3 kernel trace csv of a --mark run: print a table")
     ap.add_argument("--summarize-pmc", nargs="+", default=[], help="rocprofv3 counter csv(s) of --mark runs")
     ap.add_argument("--bench-json", default="", help="the bench line of the profiled run (for --summarize-*)")
