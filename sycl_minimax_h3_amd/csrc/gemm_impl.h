@@ -34,6 +34,9 @@
 namespace h3 {
 
 constexpr int kGemmBM = 256, kGemmBN = 256, kGemmBK = 128, kGemmStages = 2;
+// eight wavefronts a block, two a SIMD, each 128 rows x kGemmWN columns of the tile: 4 x kGemmWJ accumulators of
+// 32 x 32 (128 registers), kGemmMF products a 32-deep slice, kGemmLoads direct loads of each operand a stage
+constexpr int kGemmThreads = 512, kGemmWN = 64, kGemmWJ = kGemmWN / 32, kGemmMF = 4 * kGemmWJ, kGemmLoads = 4;
 constexpr int kGemmStageBytes = (kGemmBM + kGemmBN) * kGemmBK;   // 64 KiB
 constexpr int kGemmLds = kGemmStages * kGemmStageBytes;          // 128 KiB
 
@@ -74,9 +77,9 @@ __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "
 
 
 template <int ACT, bool PER_N>
-__global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
+__global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
     __shared__ __attribute__((aligned(16))) int8_t lds[kGemmLds];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 2, wn = wave & 3;
     int im, in;
     gemm_tile((int) blockIdx.x, P.tm, P.tn, &im, &in);
     const int64_t m0 = (int64_t) im * kGemmBM, n0 = (int64_t) in * kGemmBN, K = P.K;
@@ -89,7 +92,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
     // K steps of 128 bytes, the last one 64 when K is an odd multiple of 64 (its two slices only)
     const int nk = (int) ((K + kGemmBK - 1) / kGemmBK);
     const bool half_last = K % kGemmBK != 0;
-    // Instruction q of wavefront w fills units 64 (8 w + q) .. + 63: rows 8 (8 w + q) + lane / 8 (clamped into the
+    // Instruction q of wavefront w fills units 64 (4 w + q) .. + 63: rows 8 (4 w + q) + lane / 8 (clamped into the
     // matrix), each lane the chunk its unit holds, so one instruction reads 8 whole 128-byte segments. A half step's
     // lanes of chunks 4-7 read chunks 0-3 again (inside the row; the slices that would read them are not run).
     auto issue = [&](int kt) {
@@ -99,27 +102,27 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
         const int8_t* w = baseW + k0;
         const int cmask = half_last && kt == nk - 1 ? 3 : 7;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int r = 8 * (8 * wave + q) + (lane >> 3), c = ((lane & 7) ^ ((r >> 1) & 7)) & cmask;
+        for (int q = 0; q < kGemmLoads; ++q) {
+            const int r = 8 * (kGemmLoads * wave + q) + (lane >> 3), c = ((lane & 7) ^ ((r >> 1) & 7)) & cmask;
             const int64_t ra = m0 + r < P.M ? r : P.M - 1 - m0;
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) (a + (uint32_t) (ra * K + 16 * c)),
-                                             (__attribute__((address_space(3))) void*) (st + (8 * wave + q) * 1024), 16, 0, 0);
+                                             (__attribute__((address_space(3))) void*) (st + (kGemmLoads * wave + q) * 1024), 16, 0, 0);
         }
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int r = 8 * (8 * wave + q) + (lane >> 3), c = ((lane & 7) ^ ((r >> 1) & 7)) & cmask;
+        for (int q = 0; q < kGemmLoads; ++q) {
+            const int r = 8 * (kGemmLoads * wave + q) + (lane >> 3), c = ((lane & 7) ^ ((r >> 1) & 7)) & cmask;
             const int64_t rw = n0 + r < P.N ? r : P.N - 1 - n0;
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) (w + (uint32_t) (rw * K + 16 * c)),
-                                             (__attribute__((address_space(3))) void*) (st + kGemmBM * kGemmBK + (8 * wave + q) * 1024),
+                                             (__attribute__((address_space(3))) void*) (st + kGemmBM * kGemmBK + (kGemmLoads * wave + q) * 1024),
                                              16, 0, 0);
         }
     };
 
-    v16i acc[4][4];
+    v16i acc[4][kGemmWJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = (v16i) 0;
+        for (int j = 0; j < kGemmWJ; ++j) acc[i][j] = (v16i) 0;
 
     // fragment bases (bytes in a stage) of slice kk: row l % 32 of the wavefront's first 32-row tile, chunk
     // 2 kk + l / 32; tile i is 4096 i further (32 rows of 128 bytes, the swizzle the same for every tile)
@@ -128,38 +131,40 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
     for (int kk = 0; kk < 4; ++kk) {
         const int c = 2 * kk + (lane >> 5);
         offA[kk] = gemm_unit(wm * 128 + (lane & 31), c) * 16;
-        offW[kk] = kGemmBM * kGemmBK + gemm_unit(wn * 128 + (lane & 31), c) * 16;
+        offW[kk] = kGemmBM * kGemmBK + gemm_unit(wn * kGemmWN + (lane & 31), c) * 16;
     }
 
-    // the fragments of one 32-deep slice kk of stage kt (four A and four W)
-    auto read_half = [&](int kt, int kk, v4i (&a)[4], v4i (&b)[4]) {
+    // the fragments of one 32-deep slice kk of stage kt (four of A and kGemmWJ of W)
+    auto read_half = [&](int kt, int kk, v4i (&a)[4], v4i (&b)[kGemmWJ]) {
         const int8_t* st = lds + (kt % kGemmStages) * kGemmStageBytes;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             a[i] = *reinterpret_cast<const v4i*>(st + offA[kk] + 4096 * i);
-            b[i] = *reinterpret_cast<const v4i*>(st + offW[kk] + 4096 * i);
+            if (i < kGemmWJ) b[i] = *reinterpret_cast<const v4i*>(st + offW[kk] + 4096 * i);
         }
     };
     // W's fragment as the first operand: acc[i][j] holds rows (columns of out) from W tile j and columns (rows of
     // out) from A tile i, so each lane ends with four consecutive output columns of one output row per register group
-    auto mfma = [&](const v4i (&a)[4], const v4i (&b)[4], int p) {
-        const int i = p / 4, j = p % 4;
+    auto mfma = [&](const v4i (&a)[4], const v4i (&b)[kGemmWJ], int p) {
+        const int i = p / kGemmWJ, j = p % kGemmWJ;
         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[j], a[i], acc[i][j], 0, 0, 0);
     };
     int issued = 0;
     for (; issued < kGemmStages && issued < nk; ++issued) issue(issued);
-    v4i xa[4], xb[4], ya[4], yb[4];
-    if (issued > 1) wait_vm<16>(); else wait_vm<0>();
+    v4i xa[4], xb[kGemmWJ], ya[4], yb[kGemmWJ];
+    if (issued > 1) wait_vm<2 * kGemmLoads>(); else wait_vm<0>();
     block_barrier();
     read_half(0, 0, xa, xb);
-    auto body16 = [&](const v4i (&a)[4], const v4i (&b)[4]) {
+    // a slice's products (kGemmMF) with the next slice's fragment reads (4 + kGemmWJ) between them
+    auto body16 = [&](const v4i (&a)[4], const v4i (&b)[kGemmWJ]) {
 #pragma unroll
-        for (int p = 0; p < 16; ++p) mfma(a, b, p);
+        for (int p = 0; p < kGemmMF; ++p) mfma(a, b, p);
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            __builtin_amdgcn_sched_group_barrier(0x0008, 2, 0);
+        for (int g = 0; g < 4 + kGemmWJ; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);
         }
+        __builtin_amdgcn_sched_group_barrier(0x0008, kGemmMF - 4 - kGemmWJ, 0);
     };
     // a step with the refill of stage kt + 2 (all but the last two steps) or without it, so that the loads sit in
     // the same scheduling region as the products they are interleaved with
@@ -171,30 +176,30 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
         body16(ya, yb);
         read_half(kt, 3, ya, yb);
         body16(xa, xb);
+        constexpr int PRE = kGemmMF / 4;      // the last slice's products before the barrier
 #pragma unroll
-        for (int p = 0; p < 4; ++p) mfma(ya, yb, p);
+        for (int p = 0; p < PRE; ++p) mfma(ya, yb, p);
         __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
         wait_vm<0>();                         // stage kt + 1 landed (the only one in flight)
         block_barrier();
         if constexpr (REFILL) issue(kt + 2);
         read_half(kt + 1, 0, xa, xb);
 #pragma unroll
-        for (int p = 4; p < 16; ++p) mfma(ya, yb, p);
+        for (int p = PRE; p < kGemmMF; ++p) mfma(ya, yb, p);
+        // the rest of the slice's products, with the refill loads and the next stage's first fragment reads between them
         if constexpr (REFILL) {
 #pragma unroll
-            for (int g = 0; g < 8; ++g) {
-                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);   // one product
-                __builtin_amdgcn_sched_group_barrier(0x0020, 2, 0);   // two direct loads
-                __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // one fragment read
+            for (int g = 0; g < kGemmMF - PRE; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x0020, (2 * kGemmLoads + kGemmMF - PRE - 1) / (kGemmMF - PRE), 0);
+                __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x0008, 4, 0);
         } else {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
+            for (int g = 0; g < kGemmMF - PRE; ++g) {
                 __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x0100, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x0008, 8, 0);
         }
     };
     int kt = 0;
@@ -210,7 +215,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
         body16(xa, xb);
     }
 #pragma unroll
-    for (int p = 0; p < 16; ++p) mfma(ya, yb, p);
+    for (int p = 0; p < kGemmMF; ++p) mfma(ya, yb, p);
     wait_vm<0>();
     __syncthreads();   // every stage read: the LDS is the epilogue's now
 
@@ -223,7 +228,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
     float* srow = reinterpret_cast<float*>(lds);            // s[m] of the block's 256 rows
     float* wcol = srow + kGemmBM;                           // wscale[n] of its 256 columns
     float* bcol = wcol + kGemmBN;                           // bias[n]
-    {
+    if (tid < kGemmBM) {
         const int64_t m = m0 + tid < P.M ? m0 + tid : P.M - 1, n = n0 + tid < P.N ? n0 + tid : P.N - 1;
         srow[tid] = P.sA[m];
         wcol[tid] = PER_N ? P.ws[n] : 0.0f;
@@ -234,21 +239,21 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
         constexpr int OUT = decltype(out_tag)::value;
         constexpr bool BIAS = decltype(bias_tag)::value;
         constexpr int esz = OUT == H3S_F32 ? 4 : 2;
-        constexpr int pitch = 128 * esz + 16;               // bytes a slice row (16 bytes of pad: distinct banks)
+        constexpr int pitch = kGemmWN * esz + 16;           // bytes a slice row (16 bytes of pad: distinct banks)
         int8_t* slice = lds + 3 * 1024 + wave * (32 * pitch);
         const float ws0 = PER_N ? 0.0f : P.ws[0];
         // rows of out start on 16-byte boundaries and the block's tile lies inside out: plain 16-byte stores
         const bool full = (P.N * esz) % 16 == 0 && m0 + kGemmBM <= P.M && n0 + kGemmBN <= P.N;
-        constexpr int per_row = 128 * esz / 16, epc = 16 / esz;
+        constexpr int per_row = kGemmWN * esz / 16, epc = 16 / esz;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float sr = srow[wm * 128 + i * 32 + (lane & 31)];
             const float f1 = sr * ws0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < kGemmWJ; ++j)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int cl = wn * 128 + j * 32 + 8 * g + 4 * (lane >> 5);    // first of the four columns
+                    const int cl = wn * kGemmWN + j * 32 + 8 * g + 4 * (lane >> 5);    // first of the four columns
                     float v[4];
                     if constexpr (PER_N) {
                         const float4 w4 = *reinterpret_cast<const float4*>(wcol + cl);
@@ -273,7 +278,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs P) {
                     else
                         *reinterpret_cast<uint2*>(at) = make_uint2(pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
                 }
-            const int64_t mt = m0 + wm * 128 + i * 32, nt = n0 + wn * 128;
+            const int64_t mt = m0 + wm * 128 + i * 32, nt = n0 + wn * kGemmWN;
 #pragma unroll
             for (int k = 0; k < 32 * per_row / 64; ++k) {
                 const int ch = lane + 64 * k, rr = ch / per_row, cg = ch % per_row;

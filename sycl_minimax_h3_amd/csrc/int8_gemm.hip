@@ -52,7 +52,7 @@ int launch_gemm(Ctx* c, const char* fn, const int8_t* q, const float* s, int64_t
     const GemmArgs P{q, s, M, K, w, N, wscale, bias, out, out_dt, (int) tm, (int) tn};
     const unsigned grid = (unsigned) (tm * tn);
     const bool per_n = n_wscale > 1;
-#define LG(ACT, PN) gemm_i8_kernel<ACT, PN><<<grid, 256, 0, c->stream>>>(P)
+#define LG(ACT, PN) gemm_i8_kernel<ACT, PN><<<grid, kGemmThreads, 0, c->stream>>>(P)
 #define LA(ACT)                    \
     if (per_n) LG(ACT, true);      \
     else LG(ACT, false);
