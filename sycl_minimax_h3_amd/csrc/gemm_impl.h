@@ -34,11 +34,15 @@
 namespace h3 {
 
 constexpr int kGemmBM = 256, kGemmBN = 256, kGemmBK = 128, kGemmStages = 2;
-// eight wavefronts a block, two a SIMD, each 128 rows x kGemmWN columns of the tile: 4 x kGemmWJ accumulators of
-// 32 x 32 (128 registers), kGemmMF products a 32-deep slice, kGemmLoads direct loads of each operand a stage
-constexpr int kGemmThreads = 512, kGemmWN = 64, kGemmWJ = kGemmWN / 32, kGemmMF = 4 * kGemmWJ, kGemmLoads = 4;
+// Each wavefront computes kGemmWM rows x kGemmWN columns of the tile: kGemmWI x kGemmWJ accumulators of 32 x 32,
+// kGemmMF products a 32-deep slice, kGemmLoads direct loads of each operand a stage.
+constexpr int kGemmWM = 128, kGemmWN = 64, kGemmWI = kGemmWM / 32, kGemmWJ = kGemmWN / 32, kGemmMF = kGemmWI * kGemmWJ;
+constexpr int kGemmWaves = (kGemmBM / kGemmWM) * (kGemmBN / kGemmWN), kGemmThreads = 64 * kGemmWaves;
+constexpr int kGemmLoads = 32 / kGemmWaves;
 constexpr int kGemmStageBytes = (kGemmBM + kGemmBN) * kGemmBK;   // 64 KiB
-constexpr int kGemmLds = kGemmStages * kGemmStageBytes;          // 128 KiB
+// the two stages, or the epilogue's scales and per-wavefront 32-row slices of float32 outputs, if larger
+constexpr int kGemmEpiBytes = 3 * 1024 + kGemmWaves * 32 * (kGemmWN * 4 + 16);
+constexpr int kGemmLds = kGemmStages * kGemmStageBytes > kGemmEpiBytes ? kGemmStages * kGemmStageBytes : kGemmEpiBytes;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -79,7 +83,8 @@ __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "
 template <int ACT, bool PER_N>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
     __shared__ __attribute__((aligned(16))) int8_t lds[kGemmLds];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 2, wn = wave & 3;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / (kGemmBN / kGemmWN), wn = wave % (kGemmBN / kGemmWN);
     int im, in;
     gemm_tile((int) blockIdx.x, P.tm, P.tn, &im, &in);
     const int64_t m0 = (int64_t) im * kGemmBM, n0 = (int64_t) in * kGemmBN, K = P.K;
@@ -118,9 +123,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
         }
     };
 
-    v16i acc[4][kGemmWJ];
+    v16i acc[kGemmWI][kGemmWJ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kGemmWI; ++i)
 #pragma unroll
         for (int j = 0; j < kGemmWJ; ++j) acc[i][j] = (v16i) 0;
 
@@ -130,41 +135,42 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
         const int c = 2 * kk + (lane >> 5);
-        offA[kk] = gemm_unit(wm * 128 + (lane & 31), c) * 16;
+        offA[kk] = gemm_unit(wm * kGemmWM + (lane & 31), c) * 16;
         offW[kk] = kGemmBM * kGemmBK + gemm_unit(wn * kGemmWN + (lane & 31), c) * 16;
     }
 
-    // the fragments of one 32-deep slice kk of stage kt (four of A and kGemmWJ of W)
-    auto read_half = [&](int kt, int kk, v4i (&a)[4], v4i (&b)[kGemmWJ]) {
+    // the fragments of one 32-deep slice kk of stage kt (kGemmWI of A and kGemmWJ of W)
+    auto read_half = [&](int kt, int kk, v4i (&a)[kGemmWI], v4i (&b)[kGemmWJ]) {
         const int8_t* st = lds + (kt % kGemmStages) * kGemmStageBytes;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            a[i] = *reinterpret_cast<const v4i*>(st + offA[kk] + 4096 * i);
+        for (int i = 0; i < (kGemmWI > kGemmWJ ? kGemmWI : kGemmWJ); ++i) {
+            if (i < kGemmWI) a[i] = *reinterpret_cast<const v4i*>(st + offA[kk] + 4096 * i);
             if (i < kGemmWJ) b[i] = *reinterpret_cast<const v4i*>(st + offW[kk] + 4096 * i);
         }
     };
     // W's fragment as the first operand: acc[i][j] holds rows (columns of out) from W tile j and columns (rows of
     // out) from A tile i, so each lane ends with four consecutive output columns of one output row per register group
-    auto mfma = [&](const v4i (&a)[4], const v4i (&b)[kGemmWJ], int p) {
+    auto mfma = [&](const v4i (&a)[kGemmWI], const v4i (&b)[kGemmWJ], int p) {
         const int i = p / kGemmWJ, j = p % kGemmWJ;
         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[j], a[i], acc[i][j], 0, 0, 0);
     };
     int issued = 0;
     for (; issued < kGemmStages && issued < nk; ++issued) issue(issued);
-    v4i xa[4], xb[kGemmWJ], ya[4], yb[kGemmWJ];
+    v4i xa[kGemmWI], xb[kGemmWJ], ya[kGemmWI], yb[kGemmWJ];
     if (issued > 1) wait_vm<2 * kGemmLoads>(); else wait_vm<0>();
     block_barrier();
     read_half(0, 0, xa, xb);
-    // a slice's products (kGemmMF) with the next slice's fragment reads (4 + kGemmWJ) between them
-    auto body16 = [&](const v4i (&a)[4], const v4i (&b)[kGemmWJ]) {
+    // a slice's products (kGemmMF) with the next slice's fragment reads (kGemmWI + kGemmWJ) between them
+    auto body16 = [&](const v4i (&a)[kGemmWI], const v4i (&b)[kGemmWJ]) {
+        constexpr int NR = kGemmWI + kGemmWJ;
 #pragma unroll
         for (int p = 0; p < kGemmMF; ++p) mfma(a, b, p);
 #pragma unroll
-        for (int g = 0; g < 4 + kGemmWJ; ++g) {
+        for (int g = 0; g < (NR < kGemmMF ? NR : kGemmMF); ++g) {
             __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x0100, NR <= kGemmMF ? 1 : (NR + kGemmMF - 1) / kGemmMF, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x0008, kGemmMF - 4 - kGemmWJ, 0);
+        if constexpr (kGemmMF > NR) __builtin_amdgcn_sched_group_barrier(0x0008, kGemmMF - NR, 0);
     };
     // a step with the refill of stage kt + 2 (all but the last two steps) or without it, so that the loads sit in
     // the same scheduling region as the products they are interleaved with
@@ -246,8 +252,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
         const bool full = (P.N * esz) % 16 == 0 && m0 + kGemmBM <= P.M && n0 + kGemmBN <= P.N;
         constexpr int per_row = kGemmWN * esz / 16, epc = 16 / esz;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float sr = srow[wm * 128 + i * 32 + (lane & 31)];
+        for (int i = 0; i < kGemmWI; ++i) {
+            const float sr = srow[wm * kGemmWM + i * 32 + (lane & 31)];
             const float f1 = sr * ws0;
 #pragma unroll
             for (int j = 0; j < kGemmWJ; ++j)
@@ -278,7 +284,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
                     else
                         *reinterpret_cast<uint2*>(at) = make_uint2(pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
                 }
-            const int64_t mt = m0 + wm * 128 + i * 32, nt = n0 + wn * kGemmWN;
+            const int64_t mt = m0 + wm * kGemmWM + i * 32, nt = n0 + wn * kGemmWN;
 #pragma unroll
             for (int k = 0; k < 32 * per_row / 64; ++k) {
                 const int ch = lane + 64 * k, rr = ch / per_row, cg = ch % per_row;
