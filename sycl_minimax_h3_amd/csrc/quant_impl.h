@@ -464,7 +464,6 @@ __global__ __launch_bounds__(512)
 __attribute__((amdgpu_waves_per_eu((F & ROW_TAB) && rot_kind(ROT) == H3S_ROT_NONE ? 4 : 1)))
 void quant_wave_kernel(QuantArgs A) {
     static_assert(XDT != H3S_F32 && !(F & (ROW_DYN | ROW_SWIGLU)), "quant_wave_kernel: 16-bit x, exact side inputs");
-    static_assert(!(ONE && (F & ROW_TAB)), "quant_wave_kernel: tables are cached by a grid-strided block");
     constexpr int V = 8;
     constexpr bool ROTATED = rot_kind(ROT) != H3S_ROT_NONE;
     constexpr bool NORM = !(F & ROW_RAW);
@@ -698,17 +697,22 @@ constexpr int kQuantNone = 0, kQuantW = ROW_W, kQuantWTab = ROW_W | ROW_TAB, kQu
 // The launch of quant_wave_kernel: blocks of 4 wavefronts (8 with tables, so one LDS copy of the side values
 // serves more rows).
 template <int XDT, int CPL, int ROT, int F> int quant_wave_one(Ctx* c, const char* fn, const QuantArgs& A) {
-    constexpr bool ONE = !(F & ROW_TAB);
-    const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, ONE>;
     const int threads = 64 * quant_wave_nw(F);
     const size_t lds = quant_wave_side_bytes<CPL>(F);
-    // with tables, as many blocks as the device holds (each decodes its table row once); without, one row a
-    // wavefront and nothing prefetched (config 4 at 47104 rows: 106 us, against 119 us grid-strided with the next
-    // row in flight; with tables, one row a wavefront measured 147 against 112 us for config 5a)
     const int64_t rows_blocks = (A.M + threads / 64 - 1) / (threads / 64);
-    const int64_t blocks = (F & ROW_TAB) ? std::min<int64_t>((int64_t) c->cus * blocks_per_cu(k, threads, lds), rows_blocks)
-                                         : rows_blocks;
-    quant_wave_kernel<XDT, CPL, ROT, F, ONE><<<(unsigned) blocks, threads, lds, c->stream>>>(A);
+    // One row a wavefront, nothing prefetched (config 4 at 47104 rows: 106 us, against 119 us grid-strided with the
+    // next row in flight): without tables, and with tables whose one row serves every token (rows NULL), each block
+    // decoding its side values once. With a table row per token, as many blocks as the device holds, grid-strided,
+    // each refilling its cached table row when the rows' table row changes.
+    if constexpr (F & ROW_TAB) {
+        if (A.rows) {
+            const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, false>;
+            const int64_t blocks = std::min<int64_t>((int64_t) c->cus * blocks_per_cu(k, threads, lds), rows_blocks);
+            quant_wave_kernel<XDT, CPL, ROT, F, false><<<(unsigned) blocks, threads, lds, c->stream>>>(A);
+            return launched(fn);
+        }
+    }
+    quant_wave_kernel<XDT, CPL, ROT, F, true><<<(unsigned) rows_blocks, threads, lds, c->stream>>>(A);
     return launched(fn);
 }
 template <int XDT, int CPL> int quant_wave_launch(Ctx* c, const char* fn, const QuantArgs& A, int f) {
