@@ -133,6 +133,9 @@ template <int N> __device__ __forceinline__ void wait_vm() {
 // across it (the clobber). __syncthreads would also wait for every global load in flight, draining the rows a
 // kernel has prefetched at each row statistic.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Orders a wavefront's own LDS accesses: those issued before it are complete, and the compiler moves no memory
+// access across it (for an LDS area only this wavefront uses, written by some lanes and read by others).
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // A value equal on every lane of the wavefront, taken from the first lane: the compiler then keeps it, and what is
 // computed from it, in scalar registers (loop control as scalar branches, loads indexed by it as scalar addresses).

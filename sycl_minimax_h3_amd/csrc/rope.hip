@@ -104,9 +104,7 @@ __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M
     }
 }
 
-// orders a wavefront's own LDS accesses: those issued before it are complete, and the compiler moves no memory
-// access across it. A wavefront's LDS staging area is its own, so no workgroup barrier is needed.
-__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// A wavefront's LDS staging area is its own, so wave_lds_sync (common.h), not a workgroup barrier, orders it.
 
 constexpr int kAnyStage = 2048;   // bytes of LDS a wavefront stages: 64 / P2 heads of D <= 2 P2 V elements
 
