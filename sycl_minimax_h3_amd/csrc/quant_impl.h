@@ -150,13 +150,15 @@ template <int V, bool SW = false> __device__ __forceinline__ void sylvester(floa
 template <int CTRL> __device__ __forceinline__ float quad(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
-// the digit of stride 1, inside a chunk
+// the digit of stride 1, inside a chunk; t - 2 x as one fma (2 x is exact below 2^127, so this is the value of
+// t - 2.0f * x; the digits across lanes keep the two instructions, whose partner values come through DPP)
 template <int V> __device__ __forceinline__ void reg_in(float (&v)[V]) {
 #pragma unroll
     for (int e = 0; e < V; e += 4) {
         const float x0 = v[e], x1 = v[e + 1], x2 = v[e + 2], x3 = v[e + 3];
         const float t = ((x0 + x1) + x2) + x3;
-        v[e] = t - 2.0f * x3; v[e + 1] = t - 2.0f * x2; v[e + 2] = t - 2.0f * x1; v[e + 3] = t - 2.0f * x0;
+        v[e] = __builtin_fmaf(-2.0f, x3, t); v[e + 1] = __builtin_fmaf(-2.0f, x2, t);
+        v[e + 2] = __builtin_fmaf(-2.0f, x1, t); v[e + 3] = __builtin_fmaf(-2.0f, x0, t);
     }
 }
 // the digit of stride 4 with V = 8: x0, x1 at e and e + 4 of an even lane, x2, x3 at e and e + 4 of the odd lane
