@@ -38,8 +38,8 @@ struct ChainArgs {
 // R rows a unit: with R > 1 (rows of 256 or 512 lanes, one unit a block) the block takes rows R b .. R b + R - 1.
 // It issues every row's x and residual together, loads the weights and the table rows once and uses them for all
 // its rows, reloading the table rows only for a row whose table row differs. The weights and tables are read from
-// L2 by every block. At 16896 x 4096 with the AdaLN's three tables, two rows a block measured 68.6 us against
-// 71.2 for one (cache-cold), and three or four rows were slower (more registers, fewer wavefronts a SIMD).
+// L2 by every block. At 16896 x 4096 with the AdaLN's three tables, two rows a block took the chain from 74.2 to
+// 70.8 us (cache-cold); three or four rows were slower (more registers, fewer wavefronts a SIMD).
 template <int XDT, int CPL, int F, int R = 1>
 __global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift) {
     constexpr int V = Vec<XDT>::V;

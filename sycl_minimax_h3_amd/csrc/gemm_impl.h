@@ -6,15 +6,16 @@
 //   N weight scales:   v = (acc * s[m]) * wscale[n]       (the post-op order of h3sycl.cpp:588-602)
 //   then + bias[n], then the activation, rounded once to out's type.
 //
-// Block: 256 threads (four wavefronts, 2 x 2), a 256 x 256 tile of out; each wavefront 128 x 128 as 4 x 4
-// v_mfma_i32_32x32x32_i8 accumulators (256 registers, one wavefront per SIMD). K advances 128 bytes a step (four
+// Block: 512 threads (eight wavefronts, 2 x 4, two a SIMD), a 256 x 256 tile of out; each wavefront 128 x 64 as
+// 4 x 2 v_mfma_i32_32x32x32_i8 accumulators (128 registers): while one wavefront of a SIMD waits (its fragment reads,
+// the step's barrier, its refill loads) the other issues products (four wavefronts of 128 x 128, one a SIMD, ran 6 %
+// slower; sixteen of 64 x 64, four a SIMD, 1.5 % slower). K advances 128 bytes a step (four
 // 32-deep slices) through two LDS stages (64 KiB each: the A and W rows of the step), filled by direct
 // global->LDS loads (global_load_lds_dwordx4), so no registers hold operands in flight; each load instruction reads
 // 8 rows x 128 bytes, whole lines (a 64-byte step, half lines per instruction and the other halves a step later,
 // measured 4 % slower with four stages). Each step runs its four slices' products with the next slice's fragment
 // reads between them, waits for the next stage and publishes it (one barrier), then refills the stage it just
-// finished and reads the next stage's first slice, both spread between its last products (the refill loads
-// issued in one burst left the matrix pipe idle at one wavefront per SIMD: 4 % slower).
+// finished and reads the next stage's first slice, both spread between its last products.
 //
 // LDS layout of an operand slice: 256 rows x 8 16-byte chunks; chunk c of row r at unit 8 r + (c ^ ((r / 2) % 8)).
 // A fragment read (32 consecutive rows, one chunk each) then touches 16 distinct 4-bank groups in each 16-lane
@@ -23,7 +24,7 @@
 //
 // Tile order: the 8 XCDs take blocks round robin; blocks are renumbered so that each XCD works on a contiguous
 // run of tiles, grouped 8 tiles high so that the resident blocks of an XCD share A and W panels in its L2.
-// Epilogue: per 32 x 128 slice of a wavefront's region, dequant + activation in registers, the slice through LDS,
+// Epilogue: per 32-row slice of a wavefront's region, dequant + activation in registers, the slice through LDS,
 // then 16-byte row-contiguous stores.
 #pragma once
 
