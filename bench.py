@@ -79,6 +79,7 @@ def bytes_cfg():
         "cfg5a_rmsnorm_mod_quant_16896": M2 * C * 2 + M2 * C + M2 * 4,
         "attn_sage_16896x32x128": 4 * M2 * 4096 * 2,     # q, k, v read, out written (the products are the bound)
         "attn_sage_47104x32x128": 4 * M4 * 4096 * 2,
+        "attn_f16_4096x32x128": 4 * 4096 * 4096 * 2,     # the 16-bit form (below 8192 tokens)
         "copy_probe_1GiB": 2 << 30,
         # a plain copy moving config 1's bytes (half read, half written): the floor a launch of that size reaches
         "copy_probe_cfg1_bytes": 2 * CFG1_COPY_ELEMS * 2,
@@ -358,6 +359,8 @@ def main() -> int:
         return make
     run("attn_sage_16896x32x128", make_attn(M2), 10)
     run("attn_sage_47104x32x128", make_attn(M4), 3)
+    # the 16-bit form, which the reference takes below 8192 tokens: 4096 tokens x 32 heads x 128
+    run("attn_f16_4096x32x128", make_attn(4096), 20)
 
     if args.copy_probe:
         def make_copy():
@@ -381,10 +384,12 @@ def main() -> int:
             tops = 2 * M4 * C * 16384 / (ms * 1e-3) / 1e12
             e.update({"TOPS_i8": round(tops, 1), "frac_i8_peak": round(tops / PEAK_I8_TOPS, 4)})
         if k.startswith("attn"):
-            # q k^T on the i8 cores (5 POPS) and P v on the f16 cores (2.5 PFLOP/s): the time both take at peak
-            S_ = M2 if "16896" in k else M4
+            # the int8 form: q k^T on the i8 cores (5 POPS) and P v on the f16 cores (2.5 PFLOP/s); the 16-bit form:
+            # both on the f16 cores. The time both take at peak.
+            S_ = int(re.search(r"_(\d+)x32x128", k).group(1))
             half_ops = 2.0 * S_ * S_ * 4096
-            t_peak = half_ops / (PEAK_I8_TOPS * 1e12) + half_ops / (PEAK_F16_TFLOPS * 1e12)
+            qk_peak = PEAK_F16_TFLOPS if k.startswith("attn_f16") else PEAK_I8_TOPS
+            t_peak = half_ops / (qk_peak * 1e12) + half_ops / (PEAK_F16_TFLOPS * 1e12)
             e.update({"TOPS": round(2 * half_ops / (ms * 1e-3) / 1e12, 1), "frac_mfma_peak": round(t_peak / (ms * 1e-3), 4)})
         per[k] = e
 
