@@ -7,15 +7,16 @@
 // divided by the row sum, rounded to half (the reference's result buffer is half) and stored in out's type.
 //
 // Layouts (prepared once per call, in the context's scratch): codes or halves of q and k [H, Sp, DK], v transposed to
-// half [H, DK, Sp], Sp = S rounded up to 128 with zero rows, DK = the head size D rounded up to 64, 128 or 256 with zero
+// half [H, DK, Sp] (keys permuted inside each group of 16: attn_vt_pos), Sp = S rounded up to 128 (256 for the
+// ping-pong kernel) with zero rows, DK = the head size D rounded up to 64, 128 or 256 with zero
 // features (which change no score and no block max); the output keeps the D features. One block = 4 wavefronts = 128 queries of one head; a
 // wavefront owns 32 queries and walks all keys 64 at a time. Per 64-key tile:
 //   S^T = K Q^T:  v_mfma_i32_32x32x32_i8 (or f32_32x32x16_f16) with K as the first operand, so every lane ends with
 //                 scores of one query (lane % 32) for 32 of the 64 keys (the other 32 in lane ^ 32);
 //   softmax:      the row max needs one exchange with lane ^ 32 (v_permlane32_swap); the exponents' reference
 //                 point moves only when a tile max passes it by 2^8; the row sum stays a per-lane partial until the end;
-//   O^T += V^T P^T: v_mfma_f32_32x32x16_f16 with V^T as the first operand; P's registers become the second operand
-//                 after one v_permlane32_swap per register pair (each lane then holds 8 consecutive keys).
+//   O^T += V^T P^T: v_mfma_f32_32x32x16_f16 with V^T as the first operand; P's registers are the second operand as
+//                 they are, since v^T stores each 16-key group's keys in the order the score registers hold them.
 // K and V^T tiles go global -> LDS by direct loads (global_load_lds_dwordx4) into two stages, the next tile in flight
 // while this one is computed. Tile rows are R bytes long (R / 16 chunks); chunk c of row r sits at chunk
 // c ^ ((r / max(1, 16 / (R / 16))) % (R / 16)) of its row, so the 16-byte fragment reads of 16 consecutive rows hit
@@ -195,6 +196,12 @@ __global__ __launch_bounds__(256) void attn_qk_prep_kernel(const void* __restric
 }
 
 // The same two preparations with 16-byte loads, for rows that are 16-byte aligned (the tensor and the stride): a
+// Where key t of a 64-key tile sits in its row of v^T: inside each group of 16 keys the middle two quads swap
+// (bits 2 and 3 of t). The score products leave key 16 s + 8 (j / 4) + 4 hl + j % 4 of a query in register 8 s + j
+// of lane half hl; the P v product's second operand takes 8 consecutive k-indices per lane half from the registers
+// as they are, so its first operand (a 16-byte chunk of a v^T row) must hold those same 8 keys, in that order.
+__host__ __device__ constexpr int attn_vt_pos(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
+
 // thread holds its chunks (V values each) of the block's 64 rows in registers between the max and the codes.
 template <int DT, bool SAGE, int D>
 __global__ __launch_bounds__(256) void attn_qk_prep_vec_kernel(const void* __restrict__ src, int64_t S, int64_t Sp,
@@ -285,12 +292,14 @@ __global__ __launch_bounds__(256) void attn_v_prep_vec_kernel(const void* __rest
         for (int e = 0; e < V; ++e) tile[(c * V + e) * PITCH + t] = half_bits(f[e]);
     }
     __syncthreads();
-    // output row d holds the 64 tokens: 8 chunks of 16 bytes
+    // output row d holds the 64 tokens in the key order attn_vt_pos sets: chunk 2 g + e (8 tokens) is tokens
+    // 16 g + 4 e + (0..3) then 16 g + 8 + 4 e + (0..3)
 #pragma unroll
     for (int k = 0; k < D * 8 / 256; ++k) {
-        const int u = tid + 256 * k, d = u / 8, c = u % 8;
-        const uint4 val = *reinterpret_cast<const uint4*>(tile + d * PITCH + 8 * c);
-        *reinterpret_cast<uint4*>(vt + (h * D + d) * Sp + t0 + 8 * c) = val;
+        const int u = tid + 256 * k, d = u / 8, c = u % 8, t = 16 * (c / 2) + 4 * (c % 2);
+        const uint2 lo = *reinterpret_cast<const uint2*>(tile + d * PITCH + t);
+        const uint2 hi = *reinterpret_cast<const uint2*>(tile + d * PITCH + t + 8);
+        *reinterpret_cast<uint4*>(vt + (h * D + d) * Sp + t0 + 8 * c) = make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
 }
 
@@ -308,8 +317,16 @@ __global__ __launch_bounds__(256) void attn_v_prep_kernel(const void* __restrict
     __syncthreads();
     for (int e = tid; e < n; e += 256) {
         const int d = e / kAttnRows, t = e % kAttnRows;
-        vt[(h * DK + d) * Sp + t0 + t] = tile[t * pitch + d];
+        vt[(h * DK + d) * Sp + t0 + attn_vt_pos(t)] = tile[t * pitch + d];
     }
+}
+
+// two floats to a pair of halves (round to nearest even), left for the compiler to place: the exponentials can then
+// be written straight into the register pair v_cvt_pk_f16_f32 reads
+__device__ __forceinline__ uint32_t attn_pack_h2(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2_a));
 }
 
 // ---- the attention kernel ----
@@ -324,7 +341,7 @@ struct AttnArgs {
     void* out;                // [S, H * D]
     int out_dt;
     int D;                    // the heads' features (the kernel's DK of them are prepared, zero past D)
-    int nqb;                  // blocks of 128 queries per head
+    int nqb;                  // query blocks per head (of 128 queries, or 256 in the ping-pong kernel)
     int kvdiv;                // query heads per key/value head: head h reads k and v of head h / kvdiv
     int64_t Spk;              // rows of the prepared k and v^T (Sp unless they come from another sequence)
 };
@@ -399,12 +416,16 @@ __global__ __launch_bounds__(256, DK == 256 ? 1 : 3) void attn_kernel(AttnArgs P
 #pragma unroll
     for (int i = 0; i < NDT; ++i) o[i] = (v16f_a) 0.0f;
     float m = -INFINITY, l = 0.0f;
+    float ks_cur = SAGE ? P.ks[g * nbp] : 0.0f;               // SAGE: k's scale of the tile being computed
 
     // one 64-key tile; TAIL: the last tile, which holds keys past S
     auto step = [&](int t, auto tail_tag) {
         constexpr bool TAIL = decltype(tail_tag)::value;
         wait_vm<0>();
         __syncthreads();                                       // tile t is in; every wavefront is done with tile t - 1
+        // SAGE: the next tile's k scale, loaded before the tile's direct loads and waited for with them at the next
+        // step (loaded after them, its wait here would wait for the whole tile)
+        const float ks_next = SAGE ? P.ks[g * nbp + (t + 1 < ntiles ? t + 1 : t)] : 0.0f;
         if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1);
         const int8_t* st = lds + (t & 1) * STAGE;
 
@@ -434,7 +455,7 @@ __global__ __launch_bounds__(256, DK == 256 ? 1 : 3) void attn_kernel(AttnArgs P
         }
         // register i of half j holds key 32 j + 8 (i / 4) + 4 hl + i % 4 of the tile. The scale f > 0 is applied after
         // the max (max(a f) = f max(a)) and inside the exponent: p = 2^(a f - m) with one fused multiply-add.
-        const float f = SAGE ? fq * P.ks[g * nbp + t] : fq;
+        const float f = SAGE ? fq * ks_cur : fq;
         // register i holds key 64 t + 4 hl + off(i); it is live below S and, CAUSAL, up to this lane's query
         int lim = (int) (S - (int64_t) t * kAttnRows) - 4 * hl;
         if constexpr (CAUSAL) {
@@ -477,17 +498,14 @@ __global__ __launch_bounds__(256, DK == 256 ? 1 : 3) void attn_kernel(AttnArgs P
         for (int s = 0; s < 4; ++s) {
             // keys 16 s + 4 hl + (0..3) and 16 s + 8 + 4 hl + (0..3) of this lane's query, as half pairs
             const int b = 16 * (s / 2) + 8 * (s % 2);
-            uint32_t a0 = pack_f16(x[b + 0], x[b + 1]), a1 = pack_f16(x[b + 2], x[b + 3]);
-            uint32_t b0 = pack_f16(x[b + 4], x[b + 5]), b1 = pack_f16(x[b + 6], x[b + 7]);
+            const uint32_t a0 = attn_pack_h2(x[b + 0], x[b + 1]), a1 = attn_pack_h2(x[b + 2], x[b + 3]);
+            const uint32_t b0 = attn_pack_h2(x[b + 4], x[b + 5]), b1 = attn_pack_h2(x[b + 6], x[b + 7]);
             // the row sum of the weights as rounded to half (the ones P v uses), two at a time
             ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, a0), h2_one, ls, false);
             ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, a1), h2_one, ls, false);
             ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, b0), h2_one, ls, false);
             ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, b1), h2_one, ls, false);
-            // the upper half's first group for the lower half's second: each lane then has keys 16 s + 8 hl + (0..7)
-            const auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
-            const auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
-            a0 = s0[0]; b0 = s0[1]; a1 = s1[0]; b1 = s1[1];
+            // as they are: v^T's keys are stored in this order (attn_vt_pos)
             v4i_a pf;
             pf[0] = (int) a0; pf[1] = (int) a1; pf[2] = (int) b0; pf[3] = (int) b1;
             const v8h_a pb = __builtin_bit_cast(v8h_a, pf);
@@ -503,6 +521,7 @@ __global__ __launch_bounds__(256, DK == 256 ? 1 : 3) void attn_kernel(AttnArgs P
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, vf[dt]), pb, o[dt], 0, 0, 0);
         }
         l = l + ls;
+        ks_cur = ks_next;
     };
     issue(0, 0);
     // tiles with no key past S (and, CAUSAL, none past the block's first query) need no mask
@@ -544,6 +563,289 @@ __global__ __launch_bounds__(256, DK == 256 ? 1 : 3) void attn_kernel(AttnArgs P
                     }
                 }
             }
+    }
+}
+
+
+// ---- the ping-pong form: heads of 128 features, no mask but the sequence's end ----
+// One block = 8 wavefronts = 256 queries of one head, 32 a wavefront as above; wavefronts w and w + 4 share SIMD
+// w % 4. The two groups (wavefronts 0-3 and 4-7) take turns, one phase apart: in each phase one group runs its
+// matrix products (the scores of key tile t + 1 and O += P_t v_t) while the other runs the softmax of the scores
+// it computed in its previous product phase (-> the half weights P_{t+1}); a workgroup barrier ends every phase.
+// So the matrix cores of a SIMD work on one wavefront's products while the vector unit runs the other's softmax,
+// instead of both wavefronts reaching the same part of the tile at once.
+// Key tile j is read in the product phases of steps j - 1 (its K) and j (its V^T) of both groups, phases 2 j to
+// 2 j + 3; a ring of NS stages holds it, and its stage is refilled (tile j + NS) at the start of phase 2 j + 4,
+// by every wavefront's share of the direct loads, waited for before the barrier that opens phase 2 (j + NS).
+// Every wavefront runs the same number of barriers (2 T + 4 for T key tiles).
+// One direct global -> LDS load (16 bytes a lane to lds + 16 lane) written as inline asm: the compiler then does
+// not track it, where for the builtin it makes every later LDS read wait for all direct loads in flight (it cannot
+// tell the stages apart), which would make each phase wait for the refill issued one phase earlier. The caller's
+// wait_vm before each barrier orders these loads; the memory clobber keeps the compiler from moving LDS accesses
+// across them.
+__device__ __forceinline__ void attn_dma16(const void* g, const void* lds_dst) {
+    const uint32_t m = (uint32_t) (uintptr_t) lds_dst;
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
+}
+
+constexpr int kAttnPPQ = 256;            // queries of a ping-pong block
+// 1.5 2^23: for |n| < 2^22 the float kScoreBias + n has the bits kScoreBiasBits + n, so int32 score products started
+// from kScoreBiasBits read as floats without a conversion; |score| <= 128 127^2 < 2^22 for heads of 128 features
+constexpr float kScoreBias = 12582912.0f;
+constexpr int kScoreBiasBits = 0x4B400000;
+constexpr int kAttnPPTiles = 4096;       // key tiles it takes (sequences of up to 262144 tokens)
+
+template <bool SAGE, int NS>
+__global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnArgs P) {
+    constexpr int DK = 128, ESZ = SAGE ? 1 : 2, RB = DK * ESZ, CPR = RB / 16, NQF = RB / 32;
+    constexpr int KTB = kAttnRows * RB, VTB = DK * kAttnRows * 2, STAGE = KTB + VTB;
+    constexpr int NDT = DK / 32;
+    constexpr int KI = KTB / 1024 / 8, VI = VTB / 1024 / 8;   // direct loads of a wavefront a tile (K, V^T)
+    constexpr int LATER = (NS - 3) * (KI + VI);                // loads of later tiles in flight at a tile's wait
+    static_assert(NS >= 3 && KI >= 1 && VI >= 1, "ring");
+    __shared__ __attribute__((aligned(16))) int8_t lds[NS * STAGE];
+    // SAGE: the key tiles' scales of the head, copied once (a global load in the loop would sit behind the ring's
+    // direct loads in the same wait counter)
+    __shared__ float ksl[SAGE ? kAttnPPTiles : 1];
+    const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, ql = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool second = wave >= 4;
+    // blocks go to the 8 XCDs round robin: renumbered so that each XCD takes a contiguous run (the blocks of few
+    // heads at a time, which then share K and V^T in its L2)
+    int b = (int) blockIdx.x;
+    if (gridDim.x % 8 == 0) b = (b % 8) * (int) (gridDim.x / 8) + b / 8;
+    const int64_t h = b / P.nqb, qb = b % P.nqb, Sp = P.Sp, S = P.S;
+    const int64_t q0 = qb * kAttnPPQ + 32 * wave;             // this wavefront's first query
+    const int64_t nbp = Sp / kAttnRows;
+    const int T = (int) ((S + kAttnRows - 1) / kAttnRows);
+
+    v4i_a qf[NQF];
+    {
+        const int8_t* qrow = P.q + ((h * Sp + q0 + ql) * DK) * ESZ;
+#pragma unroll
+        for (int kk = 0; kk < NQF; ++kk) qf[kk] = *reinterpret_cast<const v4i_a*>(qrow + 32 * kk + 16 * hl);
+    }
+    const float fq = SAGE ? P.qs[h * nbp + q0 / kAttnRows] * P.c : P.c;
+
+    const int64_t g = h / P.kvdiv, Spk = P.Spk;
+    if constexpr (SAGE)
+        for (int i = tid; i < T; i += 512) ksl[i] = P.ks[g * nbp + i];
+    const int8_t* kbase = P.k + g * Spk * RB;
+    const uint16_t* vbase = P.vt + g * DK * Spk;
+    // tile t into stage t % NS; a tile past the last loads the last one again (into a stage no tile uses then), so
+    // that every wavefront has the same loads in flight at every wait
+    auto issue = [&](int t) {
+        const int64_t tc = t < T ? t : T - 1;
+        int8_t* s = lds + (t % NS) * STAGE;
+#pragma unroll
+        for (int j = 0; j < KI; ++j) {
+            const int i = wave * KI + j, u = 64 * i + lane, r = u / CPR, c = attn_swz<CPR>(r, u % CPR);
+            const int8_t* gk = kbase + (tc * kAttnRows + r) * RB + 16 * c;
+            attn_dma16(gk, s + 1024 * i);
+        }
+#pragma unroll
+        for (int j = 0; j < VI; ++j) {
+            const int i = wave * VI + j, u = 64 * i + lane, r = u / 8, c = attn_swz<8>(r, u % 8);
+            const uint16_t* gv = vbase + (int64_t) r * Spk + tc * kAttnRows + 8 * c;
+            attn_dma16(gv, s + KTB + 1024 * i);
+        }
+    };
+
+    v16f_a o[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) o[i] = (v16f_a) 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    typedef typename std::conditional<SAGE, v16i_a, v16f_a>::type score_t;
+    score_t sc[2];                                             // the scores of the next tile, two 32-key halves
+    v8h_a pb[4];                                               // the weights of the tile whose P v products are next
+
+    // product phase of step t: the scores of tile t + 1 (DS) and O += P_t v_t (DPV). Sub-step u reads 2 K
+    // fragments (u < NQF) and 4 V^T fragments (u < 4) and runs their products; the reads of sub-step u + 1 sit
+    // between the products of sub-step u, so two sub-steps' fragments are live at a time.
+    auto products = [&](int t, auto s_tag, auto pv_tag) {
+        constexpr bool DS = decltype(s_tag)::value, DPV = decltype(pv_tag)::value;
+        constexpr int U = DS ? (NQF > 4 ? NQF : 4) : 4;
+        const int8_t* sk = lds + ((t + 1) % NS) * STAGE;
+        const int8_t* sv = lds + ((t + NS) % NS) * STAGE + KTB;
+        // SAGE: the score products start from kScoreBias's bits, so the int32 sums read as floats (kScoreBias + sum)
+        if constexpr (DS) sc[0] = sc[1] = SAGE ? (score_t) kScoreBiasBits : (score_t) 0;
+        auto nk = [](int u) { return DS && u < NQF ? 2 : 0; };
+        auto nv = [](int u) { return DPV && u < 4 ? NDT : 0; };
+        v4i_a fr[2][2 + NDT];
+        auto read = [&](int u, v4i_a (&f)[2 + NDT]) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                if (j < nk(u)) {
+                    const int r = 32 * j + ql;
+                    f[j] = *reinterpret_cast<const v4i_a*>(sk + (r * CPR + attn_swz<CPR>(r, 2 * u + hl)) * 16);
+                }
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+                if (dt < nv(u)) {
+                    const int r = 32 * dt + ql;
+                    f[2 + dt] = *reinterpret_cast<const v4i_a*>(sv + (r * 8 + attn_swz<8>(r, 2 * u + hl)) * 16);
+                }
+        };
+        read(0, fr[0]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            v4i_a (&f)[2 + NDT] = fr[u & 1];
+            // the next sub-step's reads go out before this sub-step's products (the fences keep the compiler from
+            // sinking each read to its product, which would expose every read's latency)
+            if (u + 1 < U) read(u + 1, fr[(u + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            // score halves and V^T tiles alternated: each accumulator's next product comes 6 products later
+#pragma unroll
+            for (int k = 0; k < 2 + NDT; ++k) {
+                const int j = k < 4 ? k / 2 : 2, dt = k < 4 ? k / 2 : k - 2;
+                if (k % 2 == 0 && k < 4 && j < nk(u)) {
+                    if constexpr (SAGE) sc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[j], qf[u], sc[j], 0, 0, 0);
+                    else sc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, f[j]),
+                                                                         __builtin_bit_cast(v8h_a, qf[u]), sc[j], 0, 0, 0);
+                }
+                if ((k % 2 == 1 || k >= 4) && dt < nv(u))
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, f[2 + dt]), pb[u], o[dt], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // softmax phase of step t: the scores of tile t + 1 -> its half weights (pb), the running max and row sum
+    auto softmax = [&](int t, auto tail_tag) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
+        const int tn = t + 1;
+        // register i holds key 64 tn + 32 (i / 16) + 8 ((i % 16) / 4) + 4 hl + i % 4. SAGE: its bits are those of
+        // the float kScoreBias + score (the score products start from kScoreBias's bits), read as they are.
+        float x[32];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            // the whole vector reinterpreted (an element-wise __builtin_bit_cast(float, sc[j][i]) compiled to copies
+            // of element 0 here)
+            const v16f_a xf = SAGE ? __builtin_bit_cast(v16f_a, sc[j]) : __builtin_convertvector(sc[j], v16f_a);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) x[16 * j + i] = xf[i];
+        }
+        const float f = SAGE ? fq * ksl[tn] : fq;
+        const int lim = (int) (S - (int64_t) tn * kAttnRows) - 4 * hl;
+        auto live = [&](int i) { return 32 * (i / 16) + 8 * ((i % 16) / 4) + i % 4 < lim; };
+        // The weights p = 2^(score f - m) rounded to half, packed into pb as the P v products take them, and their
+        // sum over this lane's keys. SAGE: score f - m = x f - (kScoreBias f + m), with one rounding of the offset
+        // (relative 2^-24 of kScoreBias f, far below half's rounding of p).
+        auto weights = [&]() {
+            const float c = SAGE ? __builtin_fmaf(kScoreBias, f, m) : m;
+            float ls[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                float p[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[8 * s + e], f, -c));
+                    if (TAIL && !live(8 * s + e)) p[e] = 0.0f;
+                }
+                const uint32_t a0 = attn_pack_h2(p[0], p[1]), a1 = attn_pack_h2(p[2], p[3]);
+                const uint32_t b0 = attn_pack_h2(p[4], p[5]), b1 = attn_pack_h2(p[6], p[7]);
+                ls[s] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, a0), h2_one, 0.0f, false);
+                ls[s] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, a1), h2_one, ls[s], false);
+                ls[s] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, b0), h2_one, ls[s], false);
+                ls[s] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, b1), h2_one, ls[s], false);
+                v4i_a pf;                                      // as they are (attn_vt_pos)
+                pf[0] = (int) a0; pf[1] = (int) a1; pf[2] = (int) b0; pf[3] = (int) b1;
+                pb[s] = __builtin_bit_cast(v8h_a, pf);
+            }
+            return (ls[0] + ls[1]) + (ls[2] + ls[3]);
+        };
+        // First against the current reference m, with no max: a weight past half's range (a score more than about
+        // 16 above m, or m not yet set) rounds to infinity and makes the lane's sum infinite. Only then the tile's
+        // max: m moves when it passes m by more than 8 (as in attn_kernel), O and l are rescaled and the weights
+        // computed again (each at most 1 then). O / l does not depend on m.
+        float lt = weights();
+        if (__any(!(lt <= 3.0e38f))) {
+            asm volatile("" ::: "memory");
+            float mt[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float u = TAIL && !live(i) ? -INFINITY : x[i], w = TAIL && !live(i + 16) ? -INFINITY : x[i + 16];
+                mt[i] = fmaxf(u, w);
+            }
+#pragma unroll
+            for (int w = 8; w >= 1; w /= 2)
+#pragma unroll
+                for (int i = 0; i < w; ++i) mt[i] = fmaxf(mt[i], mt[i + w]);
+            const float mx = (attn_pair_max(mt[0]) - (SAGE ? kScoreBias : 0.0f)) * f;
+            if (mx > m + 8.0f) {
+                const float mn = fmaxf(m, mx);
+                const float alpha = __builtin_amdgcn_exp2f(m - mn);
+                m = mn;
+                l = l * alpha;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) o[dt] = o[dt] * alpha;
+            }
+            lt = weights();
+        }
+        l = l + lt;
+    };
+    using yes = std::true_type;
+    using no = std::false_type;
+    const bool ragged = S % kAttnRows != 0;
+    // one step: its product phase, the barrier, its softmax phase (tile t + 1, TAIL when that is the ragged last
+    // tile), the barrier; the waits and refills of the ring as set out above
+    auto run = [&](int t, auto s_tag, auto pv_tag, auto soft_tag, auto tail_tag) {
+        if (!second && t >= 0) issue(t + NS - 1);
+        products(t, s_tag, pv_tag);
+        if (second) wait_vm<LATER>();
+        lds_barrier();
+        if (second) issue(t + NS);
+        if constexpr (decltype(soft_tag)::value) softmax(t, tail_tag);
+        if (!second) wait_vm<LATER>();
+        lds_barrier();
+    };
+
+    // q's fragments and the scales are in before the first direct load: the compiler's own wait counts then see
+    // nothing in flight inside the loop (the direct loads are not counted by it)
+    wait_vm<0>();
+    for (int t = 0; t < NS - 1; ++t) issue(t);
+    wait_vm<(NS - 2) * (KI + VI)>();
+    lds_barrier();                                             // tile 0 is in
+    if (second) lds_barrier();                                 // the second group sits out phase 0
+    // step -1: the scores of tile 0 only
+    if (T == 1 && ragged) run(-1, yes{}, no{}, yes{}, yes{});
+    else run(-1, yes{}, no{}, yes{}, no{});
+    int t = 0;
+    for (; t < T - 2; ++t) run(t, yes{}, yes{}, yes{}, no{});
+    if (t == T - 2) {                                          // the scores of the last tile
+        if (ragged) run(t, yes{}, yes{}, yes{}, yes{});
+        else run(t, yes{}, yes{}, yes{}, no{});
+        ++t;
+    }
+    run(t, no{}, yes{}, no{}, no{});                           // step T - 1: the last P v products
+    if (!second) lds_barrier();
+    wait_vm<0>();                                              // no direct load may land after the block ends
+
+    // ---- out = O / l, rounded to half, in out's type ----
+    const float inv = 1.0f / attn_pair_sum(l);
+    const int64_t qi = q0 + ql;
+    auto store = [&](auto dt_tag) {
+        constexpr int OUT = decltype(dt_tag)::value;
+        constexpr int esz = OUT == H3S_F32 ? 4 : 2;
+        char* orow = reinterpret_cast<char*>(P.out) + ((qi * P.H + h) * DK) * esz;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                // registers 4 gq .. 4 gq + 3 of o[dt]: features 32 dt + 8 gq + 4 hl + (0..3)
+                const int f0 = 32 * dt + 8 * gq + 4 * hl;
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = round_f16(o[dt][4 * gq + i] * inv);
+                char* at = orow + f0 * esz;
+                if constexpr (OUT == H3S_F32) *reinterpret_cast<float4*>(at) = make_float4(v[0], v[1], v[2], v[3]);
+                else if constexpr (OUT == H3S_BF16) *reinterpret_cast<uint2*>(at) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+                else *reinterpret_cast<uint2*>(at) = make_uint2(pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
+            }
+    };
+    if (qi < S) {
+        if (P.out_dt == H3S_F32) store(std::integral_constant<int, H3S_F32>{});
+        else if (P.out_dt == H3S_BF16) store(std::integral_constant<int, H3S_BF16>{});
+        else store(std::integral_constant<int, H3S_F16>{});
     }
 }
 
