@@ -106,6 +106,24 @@ def test_attention_peaked_and_shifted(dev_sage, dev_16, sage):
     check(got, want, o.F32, "peaked")
 
 
+@pytest.mark.parametrize("sage", [True, False])
+@pytest.mark.parametrize("per_tile", [12.0, 30.0])
+def test_attention_rising_scores(dev_sage, dev_16, sage, per_tile):
+    """Scores that rise along the keys by about per_tile (base 2) every 64 keys: at 12 the weights stay inside half's
+    range while the running reference lags behind the max; at 30 every tile passes the reference by more than half's
+    range (the int8 kernel's overflow path: the max, the rescale, the weights again)."""
+    S, H, D = 640, 2, 128
+    g = np.random.default_rng(71)
+    ramp = (np.arange(S, dtype=np.float32) / 64.0 * per_tile / (np.sqrt(D) * np.log2(np.e)))[:, None]
+    q = o.to_dt((1.0 + 0.05 * g.standard_normal((S, H * D))).astype(np.float32), o.BF16).ravel()
+    k = o.to_dt((ramp + 0.05 * g.standard_normal((S, H * D))).astype(np.float32), o.BF16).ravel()
+    v = o.to_dt(g.standard_normal((S, H * D)).astype(np.float32), o.BF16).ravel()
+    want = o.attention(q, k, v, o.BF16, S, H, D, out_dt=o.F32, sage=sage)
+    want = want[0] if sage else want
+    got = run(dev_sage if sage else dev_16, q, k, v, o.BF16, S, H, D, H * D, o.F32)
+    check(got, want, o.F32, f"rising scores, {per_tile} a tile")
+
+
 def test_attention_default_form_by_length(dev):
     """The default context: below 8192 tokens the 16-bit form, from 8192 on the int8 form (kernels/h3sycl.cpp:138, 1773)."""
     H, D = 1, 64
