@@ -60,8 +60,7 @@ static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S,
 static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, const void* v, int dt, int64_t S, int64_t Hq,
                          int64_t Hkv, int64_t D, int64_t qs_stride, int64_t kv_stride, void* out, int out_dt, bool causal) {
     const bool sage = !causal && c->sage_want && S >= c->sage_min_s;
-    // the int8 form with heads of 128 features into an aligned out: the ping-pong kernel (256 queries a block;
-    // measured 5 % faster at 47104 tokens, level at 16896; the 16-bit form ran 1-2 % slower in it)
+    // the int8 form with heads of 128 features into an aligned out: the pipelined kernel (256 queries a block)
     const bool pp = sage && D == 128 && aligned16(out) && S <= (int64_t) kAttnPPTiles * kAttnRows;
     const int64_t qblock = pp ? kAttnPPQ : kAttnQBlock;
     const int64_t Sp = (S + qblock - 1) / qblock * qblock, nbp = Sp / kAttnRows;
@@ -104,7 +103,7 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
         else if (DK == 128) H3_ATTN_D(SG, 128, CA)                                             \
         else H3_ATTN_D(SG, 64, CA)                                                             \
     }
-    if (pp) attn_pp_kernel<true, 4><<<grid, 512, 0, c->stream>>>(P);
+    if (pp) attn_pl_kernel<true, 4><<<grid, 512, 0, c->stream>>>(P);
     else if (causal) H3_ATTN(false, true)
     else if (sage) H3_ATTN(true, false)
     else H3_ATTN(false, false)

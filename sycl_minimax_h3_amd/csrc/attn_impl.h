@@ -8,7 +8,7 @@
 //
 // Layouts (prepared once per call, in the context's scratch): codes or halves of q and k [H, Sp, DK], v transposed to
 // half [H, DK, Sp] (keys permuted inside each group of 16: attn_vt_pos), Sp = S rounded up to 128 (256 for the
-// ping-pong kernel) with zero rows, DK = the head size D rounded up to 64, 128 or 256 with zero
+// pipelined kernel) with zero rows, DK = the head size D rounded up to 64, 128 or 256 with zero
 // features (which change no score and no block max); the output keeps the D features. One block = 4 wavefronts = 128 queries of one head; a
 // wavefront owns 32 queries and walks all keys 64 at a time. Per 64-key tile:
 //   S^T = K Q^T:  v_mfma_i32_32x32x32_i8 (or f32_32x32x16_f16) with K as the first operand, so every lane ends with
@@ -341,7 +341,7 @@ struct AttnArgs {
     void* out;                // [S, H * D]
     int out_dt;
     int D;                    // the heads' features (the kernel's DK of them are prepared, zero past D)
-    int nqb;                  // query blocks per head (of 128 queries, or 256 in the ping-pong kernel)
+    int nqb;                  // query blocks per head (of 128 queries, or 256 in the pipelined kernel)
     int kvdiv;                // query heads per key/value head: head h reads k and v of head h / kvdiv
     int64_t Spk;              // rows of the prepared k and v^T (Sp unless they come from another sequence)
 };
@@ -567,36 +567,35 @@ __global__ __launch_bounds__(256, DK == 256 ? 1 : 3) void attn_kernel(AttnArgs P
 }
 
 
-// ---- the ping-pong form: heads of 128 features, no mask but the sequence's end ----
-// One block = 8 wavefronts = 256 queries of one head, 32 a wavefront as above; wavefronts w and w + 4 share SIMD
-// w % 4. The two groups (wavefronts 0-3 and 4-7) take turns, one phase apart: in each phase one group runs its
-// matrix products (the scores of key tile t + 1 and O += P_t v_t) while the other runs the softmax of the scores
-// it computed in its previous product phase (-> the half weights P_{t+1}); a workgroup barrier ends every phase.
-// So the matrix cores of a SIMD work on one wavefront's products while the vector unit runs the other's softmax,
-// instead of both wavefronts reaching the same part of the tile at once.
-// Key tile j is read in the product phases of steps j - 1 (its K) and j (its V^T) of both groups, phases 2 j to
-// 2 j + 3; a ring of NS stages holds it, and its stage is refilled (tile j + NS) at the start of phase 2 j + 4,
-// by every wavefront's share of the direct loads, waited for before the barrier that opens phase 2 (j + NS).
-// Every wavefront runs the same number of barriers (2 T + 4 for T key tiles).
 // One direct global -> LDS load (16 bytes a lane to lds + 16 lane) written as inline asm: the compiler then does
 // not track it, where for the builtin it makes every later LDS read wait for all direct loads in flight (it cannot
-// tell the stages apart), which would make each phase wait for the refill issued one phase earlier. The caller's
-// wait_vm before each barrier orders these loads; the memory clobber keeps the compiler from moving LDS accesses
-// across them.
+// tell the stages apart), which would make each step wait for the refill issued at its start. The caller's wait_vm
+// before each barrier orders these loads; the memory clobber keeps the compiler from moving LDS accesses across
+// them.
 __device__ __forceinline__ void attn_dma16(const void* g, const void* lds_dst) {
     const uint32_t m = (uint32_t) (uintptr_t) lds_dst;
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
 }
 
-constexpr int kAttnPPQ = 256;            // queries of a ping-pong block
+constexpr int kAttnPPQ = 256;            // queries of a pipelined block
 // 1.5 2^23: for |n| < 2^22 the float kScoreBias + n has the bits kScoreBiasBits + n, so int32 score products started
 // from kScoreBiasBits read as floats without a conversion; |score| <= 128 127^2 < 2^22 for heads of 128 features
 constexpr float kScoreBias = 12582912.0f;
 constexpr int kScoreBiasBits = 0x4B400000;
 constexpr int kAttnPPTiles = 4096;       // key tiles it takes (sequences of up to 262144 tokens)
 
+
+// ---- the pipelined form: the int8 form, heads of 128 features, no mask but the sequence's end ----
+// One block = 8 wavefronts = 256 queries of one head, 32 a wavefront as above, two wavefronts a SIMD. Each step a
+// wavefront computes the scores of key tile t + 1, then tile t's P v products with the softmax of tile t + 1 (the
+// two are independent) between them: a wavefront issues a few VALU instructions between its own matrix products at
+// no cost to them, and both wavefronts of a SIMD do so. One workgroup barrier a step.
+// Key tile j is read in steps j - 1 (its K) and j (its V^T); a ring of NS stages holds it; its stage is refilled
+// (tile j + NS) at the start of step j + 1, every wavefront issuing its share of the direct loads, which it waits for
+// before the barrier that publishes them. The ring's loads are inline asm (attn_dma16), the head's k scales are
+// copied into LDS once, and the int8 score products start from kScoreBias's bits: see the helpers above.
 template <bool SAGE, int NS>
-__global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnArgs P) {
+__global__ __launch_bounds__(512, 1) void attn_pl_kernel(AttnArgs P) {
     constexpr int DK = 128, ESZ = SAGE ? 1 : 2, RB = DK * ESZ, CPR = RB / 16, NQF = RB / 32;
     constexpr int KTB = kAttnRows * RB, VTB = DK * kAttnRows * 2, STAGE = KTB + VTB;
     constexpr int NDT = DK / 32;
@@ -609,7 +608,6 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnArgs P) {
     __shared__ float ksl[SAGE ? kAttnPPTiles : 1];
     const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, ql = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool second = wave >= 4;
     // blocks go to the 8 XCDs round robin: renumbered so that each XCD takes a contiguous run (the blocks of few
     // heads at a time, which then share K and V^T in its L2)
     int b = (int) blockIdx.x;
@@ -657,60 +655,48 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnArgs P) {
     float m = -INFINITY, l = 0.0f;
     typedef typename std::conditional<SAGE, v16i_a, v16f_a>::type score_t;
     score_t sc[2];                                             // the scores of the next tile, two 32-key halves
-    v8h_a pb[4];                                               // the weights of the tile whose P v products are next
+    v8h_a pb[4];                                               // the weights of the tile whose P v products run now
+    v8h_a pn[4];                                               // the weights being formed for the next tile
 
-    // product phase of step t: the scores of tile t + 1 (DS) and O += P_t v_t (DPV). Sub-step u reads 2 K
-    // fragments (u < NQF) and 4 V^T fragments (u < 4) and runs their products; the reads of sub-step u + 1 sit
-    // between the products of sub-step u, so two sub-steps' fragments are live at a time.
-    auto products = [&](int t, auto s_tag, auto pv_tag) {
-        constexpr bool DS = decltype(s_tag)::value, DPV = decltype(pv_tag)::value;
-        constexpr int U = DS ? (NQF > 4 ? NQF : 4) : 4;
+    // the scores of tile t + 1 (K of its stage), two 32-key halves, started from kScoreBias's bits (SAGE)
+    auto scores = [&](int t) {
         const int8_t* sk = lds + ((t + 1) % NS) * STAGE;
-        const int8_t* sv = lds + ((t + NS) % NS) * STAGE + KTB;
-        // SAGE: the score products start from kScoreBias's bits, so the int32 sums read as floats (kScoreBias + sum)
-        if constexpr (DS) sc[0] = sc[1] = SAGE ? (score_t) kScoreBiasBits : (score_t) 0;
-        auto nk = [](int u) { return DS && u < NQF ? 2 : 0; };
-        auto nv = [](int u) { return DPV && u < 4 ? NDT : 0; };
-        v4i_a fr[2][2 + NDT];
-        auto read = [&](int u, v4i_a (&f)[2 + NDT]) {
+        sc[0] = sc[1] = SAGE ? (score_t) kScoreBiasBits : (score_t) 0;
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                if (j < nk(u)) {
-                    const int r = 32 * j + ql;
-                    f[j] = *reinterpret_cast<const v4i_a*>(sk + (r * CPR + attn_swz<CPR>(r, 2 * u + hl)) * 16);
-                }
+        for (int u = 0; u < NQF; ++u) {
+            v4i_a kf[2];
 #pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-                if (dt < nv(u)) {
-                    const int r = 32 * dt + ql;
-                    f[2 + dt] = *reinterpret_cast<const v4i_a*>(sv + (r * 8 + attn_swz<8>(r, 2 * u + hl)) * 16);
-                }
-        };
-        read(0, fr[0]);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            v4i_a (&f)[2 + NDT] = fr[u & 1];
-            // the next sub-step's reads go out before this sub-step's products (the fences keep the compiler from
-            // sinking each read to its product, which would expose every read's latency)
-            if (u + 1 < U) read(u + 1, fr[(u + 1) & 1]);
-            __builtin_amdgcn_sched_barrier(0);
-            // score halves and V^T tiles alternated: each accumulator's next product comes 6 products later
-#pragma unroll
-            for (int k = 0; k < 2 + NDT; ++k) {
-                const int j = k < 4 ? k / 2 : 2, dt = k < 4 ? k / 2 : k - 2;
-                if (k % 2 == 0 && k < 4 && j < nk(u)) {
-                    if constexpr (SAGE) sc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[j], qf[u], sc[j], 0, 0, 0);
-                    else sc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, f[j]),
-                                                                         __builtin_bit_cast(v8h_a, qf[u]), sc[j], 0, 0, 0);
-                }
-                if ((k % 2 == 1 || k >= 4) && dt < nv(u))
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, f[2 + dt]), pb[u], o[dt], 0, 0, 0);
+            for (int j = 0; j < 2; ++j) {
+                const int r = 32 * j + ql;
+                kf[j] = *reinterpret_cast<const v4i_a*>(sk + (r * CPR + attn_swz<CPR>(r, 2 * u + hl)) * 16);
             }
-            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if constexpr (SAGE) sc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j], qf[u], sc[j], 0, 0, 0);
+                else sc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, kf[j]),
+                                                                     __builtin_bit_cast(v8h_a, qf[u]), sc[j], 0, 0, 0);
+            }
         }
     };
-    // softmax phase of step t: the scores of tile t + 1 -> its half weights (pb), the running max and row sum
-    auto softmax = [&](int t, auto tail_tag) {
+    // O += P_t v_t: 16 products (V^T of tile t's stage)
+    auto pv = [&](int t) {
+        const int8_t* sv = lds + (t % NS) * STAGE + KTB;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            v4i_a vf[NDT];
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const int r = 32 * dt + ql;
+                vf[dt] = *reinterpret_cast<const v4i_a*>(sv + (r * 8 + attn_swz<8>(r, 2 * u + hl)) * 16);
+            }
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, vf[dt]), pb[u], o[dt], 0, 0, 0);
+        }
+    };
+    // the softmax of the scores of tile t + 1 -> its half weights (pn), the running max and row sum; sets alpha when
+    // O is to be rescaled (after this step's P v products, which use the old reference)
+    auto softmax = [&](int t, auto tail_tag, float& alpha) {
         constexpr bool TAIL = decltype(tail_tag)::value;
         const int tn = t + 1;
         // register i holds key 64 tn + 32 (i / 16) + 8 ((i % 16) / 4) + 4 hl + i % 4. SAGE: its bits are those of
@@ -730,11 +716,8 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnArgs P) {
         // The weights p = 2^(score f - m) rounded to half, packed into pb as the P v products take them, and their
         // sum over this lane's keys. SAGE: score f - m = x f - (kScoreBias f + m), with one rounding of the offset
         // (relative 2^-24 of kScoreBias f, far below half's rounding of p).
-        auto weights = [&]() {
-            const float c = SAGE ? __builtin_fmaf(kScoreBias, f, m) : m;
-            float ls[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
+        // chunk s: the weights of registers 8 s .. 8 s + 7 into pn[s], their sum
+        auto chunk = [&](int s, float c) {
                 float p[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -743,14 +726,20 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnArgs P) {
                 }
                 const uint32_t a0 = attn_pack_h2(p[0], p[1]), a1 = attn_pack_h2(p[2], p[3]);
                 const uint32_t b0 = attn_pack_h2(p[4], p[5]), b1 = attn_pack_h2(p[6], p[7]);
-                ls[s] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, a0), h2_one, 0.0f, false);
-                ls[s] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, a1), h2_one, ls[s], false);
-                ls[s] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, b0), h2_one, ls[s], false);
-                ls[s] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, b1), h2_one, ls[s], false);
+                float ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, a0), h2_one, 0.0f, false);
+                ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, a1), h2_one, ls, false);
+                ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, b0), h2_one, ls, false);
+                ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_a, b1), h2_one, ls, false);
                 v4i_a pf;                                      // as they are (attn_vt_pos)
                 pf[0] = (int) a0; pf[1] = (int) a1; pf[2] = (int) b0; pf[3] = (int) b1;
-                pb[s] = __builtin_bit_cast(v8h_a, pf);
-            }
+                pn[s] = __builtin_bit_cast(v8h_a, pf);
+                return ls;
+        };
+        auto weights = [&]() {
+            const float c = SAGE ? __builtin_fmaf(kScoreBias, f, m) : m;
+            float ls[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) ls[s] = chunk(s, c);
             return (ls[0] + ls[1]) + (ls[2] + ls[3]);
         };
         // First against the current reference m, with no max: a weight past half's range (a score more than about
@@ -773,11 +762,9 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnArgs P) {
             const float mx = (attn_pair_max(mt[0]) - (SAGE ? kScoreBias : 0.0f)) * f;
             if (mx > m + 8.0f) {
                 const float mn = fmaxf(m, mx);
-                const float alpha = __builtin_amdgcn_exp2f(m - mn);
+                alpha = __builtin_amdgcn_exp2f(m - mn);
                 m = mn;
                 l = l * alpha;
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) o[dt] = o[dt] * alpha;
             }
             lt = weights();
         }
@@ -786,16 +773,26 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnArgs P) {
     using yes = std::true_type;
     using no = std::false_type;
     const bool ragged = S % kAttnRows != 0;
-    // one step: its product phase, the barrier, its softmax phase (tile t + 1, TAIL when that is the ragged last
-    // tile), the barrier; the waits and refills of the ring as set out above
-    auto run = [&](int t, auto s_tag, auto pv_tag, auto soft_tag, auto tail_tag) {
-        if (!second && t >= 0) issue(t + NS - 1);
-        products(t, s_tag, pv_tag);
-        if (second) wait_vm<LATER>();
-        lds_barrier();
-        if (second) issue(t + NS);
-        if constexpr (decltype(soft_tag)::value) softmax(t, tail_tag);
-        if (!second) wait_vm<LATER>();
+    // Step t: refill the ring (tile t + NS - 1); the scores of tile t + 1 (DS); tile t's P v products (DPV) with the
+    // softmax of tile t + 1 (independent of them) between them; O's rescale, if the softmax moved the reference; the
+    // wait for tile t + 2 and one barrier. Tile j is read in steps j - 1 (K) and j (V^T); its stage is refilled at
+    // step j + 1, after the barrier that ends step j.
+    auto step = [&](int t, auto s_tag, auto pv_tag, auto tail_tag) {
+        constexpr bool DS = decltype(s_tag)::value, DPV = decltype(pv_tag)::value;
+        if (t >= 0) issue(t + NS - 1);
+        if constexpr (DS) scores(t);
+        if constexpr (DPV) pv(t);
+        float alpha = 1.0f;
+        if constexpr (DS) softmax(t, tail_tag, alpha);       // the compiler places it between the P v products
+        if constexpr (DPV) {
+            if (alpha != 1.0f) {
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) o[dt] = o[dt] * alpha;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pb[u] = pn[u];
+        wait_vm<LATER>();                                      // tile t + 2 is in (the barrier publishes it)
         lds_barrier();
     };
 
@@ -805,19 +802,16 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnArgs P) {
     for (int t = 0; t < NS - 1; ++t) issue(t);
     wait_vm<(NS - 2) * (KI + VI)>();
     lds_barrier();                                             // tile 0 is in
-    if (second) lds_barrier();                                 // the second group sits out phase 0
-    // step -1: the scores of tile 0 only
-    if (T == 1 && ragged) run(-1, yes{}, no{}, yes{}, yes{});
-    else run(-1, yes{}, no{}, yes{}, no{});
+    if (T == 1 && ragged) step(-1, yes{}, no{}, yes{});
+    else step(-1, yes{}, no{}, no{});
     int t = 0;
-    for (; t < T - 2; ++t) run(t, yes{}, yes{}, yes{}, no{});
+    for (; t < T - 2; ++t) step(t, yes{}, yes{}, no{});
     if (t == T - 2) {                                          // the scores of the last tile
-        if (ragged) run(t, yes{}, yes{}, yes{}, yes{});
-        else run(t, yes{}, yes{}, yes{}, no{});
+        if (ragged) step(t, yes{}, yes{}, yes{});
+        else step(t, yes{}, yes{}, no{});
         ++t;
     }
-    run(t, no{}, yes{}, no{}, no{});                           // step T - 1: the last P v products
-    if (!second) lds_barrier();
+    step(t, no{}, yes{}, no{});                                // step T - 1: the last P v products
     wait_vm<0>();                                              // no direct load may land after the block ends
 
     // ---- out = O / l, rounded to half, in out's type ----
