@@ -60,8 +60,8 @@ static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S,
 static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, const void* v, int dt, int64_t S, int64_t Hq,
                          int64_t Hkv, int64_t D, int64_t qs_stride, int64_t kv_stride, void* out, int out_dt, bool causal) {
     const bool sage = !causal && c->sage_want && S >= c->sage_min_s;
-    // the int8 form with heads of 128 features into an aligned out: the pipelined kernel (256 queries a block)
-    const bool pp = sage && D == 128 && aligned16(out) && S <= (int64_t) kAttnPPTiles * kAttnRows;
+    // heads of 128 features into an aligned out, no causal mask: the pipelined kernel (256 queries a block)
+    const bool pp = !causal && D == 128 && aligned16(out) && S <= (int64_t) kAttnPPTiles * kAttnRows;
     const int64_t qblock = pp ? kAttnPPQ : kAttnQBlock;
     const int64_t Sp = (S + qblock - 1) / qblock * qblock, nbp = Sp / kAttnRows;
     const int64_t esz = sage ? 1 : 2, DK = attn_dk(D);
@@ -103,8 +103,10 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
         else if (DK == 128) H3_ATTN_D(SG, 128, CA)                                             \
         else H3_ATTN_D(SG, 64, CA)                                                             \
     }
-    if (pp) attn_pl_kernel<true, 4><<<grid, 512, 0, c->stream>>>(P);
-    else if (causal) H3_ATTN(false, true)
+    if (pp) {
+        if (sage) attn_pl_kernel<true, 4><<<grid, 512, 0, c->stream>>>(P);
+        else attn_pl_kernel<false, 4><<<grid, 512, 0, c->stream>>>(P);
+    } else if (causal) H3_ATTN(false, true)
     else if (sage) H3_ATTN(true, false)
     else H3_ATTN(false, false)
 #undef H3_ATTN

@@ -585,7 +585,7 @@ constexpr int kScoreBiasBits = 0x4B400000;
 constexpr int kAttnPPTiles = 4096;       // key tiles it takes (sequences of up to 262144 tokens)
 
 
-// ---- the pipelined form: the int8 form, heads of 128 features, no mask but the sequence's end ----
+// ---- the pipelined form: heads of 128 features, no mask but the sequence's end (both forms) ----
 // One block = 8 wavefronts = 256 queries of one head, 32 a wavefront as above, two wavefronts a SIMD. Each step a
 // wavefront computes the scores of key tile t + 1, then tile t's P v products with the softmax of tile t + 1 (the
 // two are independent) between them: a wavefront issues a few VALU instructions between its own matrix products at
