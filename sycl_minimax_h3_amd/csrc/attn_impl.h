@@ -662,20 +662,28 @@ __global__ __launch_bounds__(512, 1) void attn_pl_kernel(AttnArgs P) {
     auto scores = [&](int t) {
         const int8_t* sk = lds + ((t + 1) % NS) * STAGE;
         sc[0] = sc[1] = SAGE ? (score_t) kScoreBiasBits : (score_t) 0;
-#pragma unroll
-        for (int u = 0; u < NQF; ++u) {
-            v4i_a kf[2];
+        v4i_a kf[2][2];
+        auto kread = [&](int u, v4i_a (&d)[2]) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int r = 32 * j + ql;
-                kf[j] = *reinterpret_cast<const v4i_a*>(sk + (r * CPR + attn_swz<CPR>(r, 2 * u + hl)) * 16);
+                d[j] = *reinterpret_cast<const v4i_a*>(sk + (r * CPR + attn_swz<CPR>(r, 2 * u + hl)) * 16);
             }
+        };
+        kread(0, kf[0]);
+#pragma unroll
+        for (int u = 0; u < NQF; ++u) {
+            // the next sub-step's two K fragments read ahead of this one's products, fenced (the scheduler sinks
+            // each read to its product otherwise, and its latency comes before the product)
+            if (u + 1 < NQF) kread(u + 1, kf[(u + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                if constexpr (SAGE) sc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j], qf[u], sc[j], 0, 0, 0);
-                else sc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, kf[j]),
+                if constexpr (SAGE) sc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[u & 1][j], qf[u], sc[j], 0, 0, 0);
+                else sc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_a, kf[u & 1][j]),
                                                                      __builtin_bit_cast(v8h_a, qf[u]), sc[j], 0, 0, 0);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
     // O += P_t v_t: 16 products (V^T of tile t's stage)
