@@ -3,8 +3,8 @@
  * Drop-in for kernels/h3sycl.h of maxfridbe/sycl_minimax_h3. Every function of that header is declared here with the
  * same name, argument list and return convention, so engine/h3-sys (engine/h3-sys/src/lib.rs:215-283, which
  * resolves 48 of these names and refuses a library missing any) loads this library unchanged, found through
- * $H3SYCL_LIB (engine/h3-sys/src/lib.rs:181-193). Functions that have no HIP implementation here (convolutions,
- * attention, the float GEMMs, the audio ops, k-quant expansion) return -1 with a message naming them.
+ * $H3SYCL_LIB (engine/h3-sys/src/lib.rs:181-193). Functions that have no HIP implementation here (the convolutions,
+ * the upscaler's and the audio decoder's ops, k-quant expansion) return -1 with a message naming them.
  *
  * Conventions, as kernels/h3sycl.h:1-9:
  *  - every data pointer is device memory of the context's GPU;
@@ -151,7 +151,8 @@ int h3s_swiglu(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, void* o
 int h3s_gate_add(void* ctx, void* x, int x_dt, int64_t M, int64_t C, const void* other, int other_dt,
                  const int32_t* rows, const float* gate);
 
-/* Attention over S tokens of H heads of D (64 or 128), rows at element stride `stride`, out [S, H D] (h3s_attention),
+/* Attention over S tokens of H heads of D (any head size up to 256), rows at element stride `stride`, out [S, H D]
+ * (h3s_attention),
  * and B independent sequences of S tokens each (h3s_attention_batch). The reference's choice of form: the int8
  * (SageAttention) form from H3S_SAGE_MIN_S tokens (8192) on unless H3S_ATTN=onednn, the 16-bit form below it.
  * Replace kernels/h3sycl.h:190-200. */
