@@ -152,8 +152,7 @@ int h3s_gate_add(void* ctx, void* x, int x_dt, int64_t M, int64_t C, const void*
                  const int32_t* rows, const float* gate);
 
 /* Attention over S tokens of H heads of D (any head size up to 256), rows at element stride `stride`, out [S, H D]
- * (h3s_attention),
- * and B independent sequences of S tokens each (h3s_attention_batch). The reference's choice of form: the int8
+ * (h3s_attention), and B independent sequences of S tokens each (h3s_attention_batch). The reference's choice of form: the int8
  * (SageAttention) form from H3S_SAGE_MIN_S tokens (8192) on unless H3S_ATTN=onednn, the 16-bit form below it.
  * Replace kernels/h3sycl.h:190-200. */
 int h3s_attention(void* ctx, const void* q, const void* k, const void* v, int dt, int64_t S, int64_t H, int64_t D,
