@@ -390,7 +390,7 @@ def test_norm_quant_full_size(dev, config):
 # ---- h3s_swiglu_quant: swiglu -> the MLP's act scratch -> fc2's quantizer, in one pass ----
 @pytest.mark.parametrize("rot,group", [(o.ROT_NONE, 0), (o.ROT_REGULAR, 256), (o.ROT_REGULAR, 16), (o.ROT_SYLVESTER, 128)])
 @pytest.mark.parametrize("x_dt,h_dt", [(o.BF16, o.BF16), (o.F16, o.F16), (o.F32, o.F32), (o.F32, o.BF16), (o.BF16, o.F32)])
-@pytest.mark.parametrize("M,C", [(23, 2048), (7, 4096), (6, 8192), (3, 16384), (5, 64), (9, 528)])
+@pytest.mark.parametrize("M,C", [(23, 2048), (7, 4096), (6, 8192), (3, 16384), (11, 1792), (5, 64), (9, 528)])
 def test_swiglu_quant(dev, rot, group, x_dt, h_dt, M, C):
     if group and C % group:
         pytest.skip("group does not divide C")
