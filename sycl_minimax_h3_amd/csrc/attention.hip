@@ -39,7 +39,7 @@ static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S,
 #undef H3_QK
     };
     if (sage) {
-        // k's mean per (head, feature) of the D features; the 16-byte form takes 32 features a block
+        // k's mean per (head, feature) of the D features; the 16-byte form takes 16 features a block
         const int64_t hd = Hkv * D;
         if (vec && hd % kKmeanFeat == 0) attn_kmean_kernel<DT><<<(unsigned) (hd / kKmeanFeat), 256, 0, c->stream>>>(k, S, kv_stride, km);
         else attn_kmean_rows_kernel<DT><<<(unsigned) ((hd + 255) / 256), 256, 0, c->stream>>>(k, S, hd, kv_stride, km);

@@ -55,84 +55,128 @@ __device__ __forceinline__ uint16_t half_bits(float x) {
     return b;
 }
 
+// One direct global -> LDS load (16 bytes a lane to lds + 16 lane) written as inline asm: the compiler then does
+// not track it, where for the builtin it makes every later LDS read wait for all direct loads in flight (it cannot
+// tell the stages apart), which would make a ring's reads of a landed stage wait for the refills issued after it. The
+// caller's wait_vm before each barrier orders these loads; the memory clobber keeps the compiler from moving LDS
+// accesses across them.
+__device__ __forceinline__ void attn_dma16(const void* g, const void* lds_dst) {
+    const uint32_t m = (uint32_t) (uintptr_t) lds_dst;
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
+}
+
 // k's mean over the sequence per (head, feature): a float32 sum in token order, / S (h3sycl.cpp:1732-1737). Each
-// feature's sum is one serial chain of S additions, so the kernel is built to run that chain at the adder's latency:
-// a block takes 32 features (128 blocks at 4096 features). Wavefronts 1-3 fill a ring of four 12 KiB row chunks with
-// direct loads (global_load_lds_dwordx4, three chunks in flight); wavefront 0 runs the 32 sums, one feature a lane,
-// with ordinary LDS reads 16 rows ahead of the additions. Wavefront 0 issues no global loads, so the waits the
-// compiler places before its LDS reads are exact and never wait on the ring's loads. Needs the rows 16-byte aligned
-// (k and the stride); attn_kmean_rows_kernel is the general form.
-constexpr int kKmeanFeat = 32, kKmeanStages = 4, kKmeanChunk = 12288, kKmeanLoaders = 192;
+// feature's sum is one serial chain of S additions (a wavefront issues a dependent v_add_f32 every 4.9 cycles), and
+// the features are few (4096 at 32 heads of 128), so the kernel spreads them thin to use every CU's memory
+// parallelism: a block takes 16 features (256 blocks at 4096 features; a block's loads in flight, not HBM, bound the
+// rate), one a lane of wavefront 0, which only reads four float32 rows of its feature at a time (ds_read_b128) and
+// adds them in order. Wavefronts 1-3 keep seven row chunks in flight with direct loads (attn_dma16) into a ring of
+// eight 12 KiB stages (row-major, as in memory) and turn each landed chunk into float32 rows per feature
+// (feature-major, padded) in one of two buffers. One barrier a chunk: after barrier i, wavefront 0 sums chunk i - 1
+// while the others convert chunk i, refill chunk i - 1's stage with chunk i + 7 and wait for chunk i + 1. A chunk
+// past the last loads the last one again (into a stage no chunk uses then), so the wait is the same at every chunk.
+// Blocks of neighbouring features (which share 128-byte lines) are numbered onto one XCD. Needs the rows 16-byte
+// aligned (k and the stride); attn_kmean_rows_kernel is the general form.
+constexpr int kKmeanFeat = 16, kKmeanStages = 8, kKmeanChunk = 12288, kKmeanLoaders = 192;
 template <int DT>
 __global__ __launch_bounds__(256) void attn_kmean_kernel(const void* __restrict__ k, int64_t S, int64_t stride,
                                                          float* __restrict__ mean) {
-    constexpr int ESZ = DT == H3S_F32 ? 4 : 2, RB = kKmeanFeat * ESZ;          // bytes of a row's 32 features
+    constexpr int F = kKmeanFeat, ESZ = DT == H3S_F32 ? 4 : 2, RB = F * ESZ;   // bytes of a row's F features
     constexpr int SEG = RB / 16, ROWS = kKmeanChunk / RB, LPT = kKmeanChunk / (kKmeanLoaders * 16);
+    constexpr int VS = 16 / ESZ;                 // values of a 16-byte segment
+    constexpr int TS = ROWS + 4;                 // floats a feature takes in a converted buffer
+    constexpr int SUB = 32;                      // rows a sub-batch of the sums (8 reads in flight)
     static_assert(kKmeanChunk % RB == 0 && kKmeanChunk % (kKmeanLoaders * 16) == 0, "attn_kmean_kernel: chunk shape");
+    static_assert(kKmeanLoaders % SEG == 0 && kKmeanLoaders / SEG * 4 == ROWS && ROWS % SUB == 0,
+                  "attn_kmean_kernel: a loader converts 4 rows of a segment");
     __shared__ __attribute__((aligned(16))) uint8_t ring[kKmeanStages * kKmeanChunk];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t c0 = (int64_t) blockIdx.x * kKmeanFeat, nch = (S + ROWS - 1) / ROWS;
+    __shared__ __attribute__((aligned(16))) float conv[2][F * TS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // blocks go to the 8 XCDs round robin: renumbered so that each XCD takes a contiguous run of features
+    int64_t b = blockIdx.x;
+    if (gridDim.x % 8 == 0) b = (b % 8) * (gridDim.x / 8) + b / 8;
+    const int64_t c0 = b * F, nch = (S + ROWS - 1) / ROWS;
     const char* base = reinterpret_cast<const char*>(k) + c0 * ESZ;
-    // loader thread p = tid - 64, load i: unit u = p + 192 i of the chunk (row u / SEG, 16-byte segment u % SEG),
-    // landing at byte 16 u of the stage: the chunk is row-major, RB bytes a row
+    // loader thread p = tid - 64, load j: unit u = p + 192 j of the chunk (row u / SEG, 16-byte segment u % SEG),
+    // landing at byte 16 u of the stage (1024 (3 j + wave - 1) + 16 lane): the stage is the chunk row-major
     auto issue = [&](int64_t ch) {
+        const int64_t cc = ch < nch ? ch : nch - 1;
         uint8_t* st = ring + (ch % kKmeanStages) * kKmeanChunk;
 #pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int u = (tid - 64) + kKmeanLoaders * i;
-            int64_t row = ch * ROWS + u / SEG;
+        for (int j = 0; j < LPT; ++j) {
+            const int u = (tid - 64) + kKmeanLoaders * j;
+            int64_t row = cc * ROWS + u / SEG;
             row = row < S ? row : S - 1;
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*) (base + row * stride * ESZ + 16 * (u % SEG)),
-                                             (__attribute__((address_space(3))) void*) (st + (3 * i + wave - 1) * 1024), 16, 0, 0);
+            attn_dma16(base + row * stride * ESZ + 16 * (u % SEG), st + (3 * j + wave - 1) * 1024);
         }
     };
-    // the value of row r of a stage for this lane's feature, as float32
-    auto at = [&](const uint8_t* st, int r) -> float {
-        const uint8_t* e = st + r * RB + lane * ESZ;
-        if constexpr (DT == H3S_F32) return *reinterpret_cast<const float*>(e);
-        else if constexpr (DT == H3S_BF16) return bf16_lo(*reinterpret_cast<const uint16_t*>(e));
-        else return f16_lo(*reinterpret_cast<const uint16_t*>(e));
+    // loader thread p converts rows 4 g .. 4 g + 3 of segment s (g = p / SEG, s = p % SEG): four 16-byte reads, then
+    // four rows of each of the segment's VS features as one 16-byte write
+    auto convert = [&](int64_t ch) {
+        const int p = tid - 64, sg = p % SEG, g = p / SEG;
+        const uint8_t* st = ring + (ch % kKmeanStages) * kKmeanChunk;
+        float* cv = conv[ch & 1];
+        uint4 raw[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) raw[r] = *reinterpret_cast<const uint4*>(st + (4 * g + r) * RB + 16 * sg);
+        float x[4][VS];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t w[4] = {raw[r].x, raw[r].y, raw[r].z, raw[r].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (DT == H3S_F32) x[r][i] = __uint_as_float(w[i]);
+                else if constexpr (DT == H3S_BF16) { x[r][2 * i] = bf16_lo(w[i]); x[r][2 * i + 1] = bf16_hi(w[i]); }
+                else { x[r][2 * i] = f16_lo(w[i]); x[r][2 * i + 1] = f16_hi(w[i]); }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < VS; ++e)
+            *reinterpret_cast<float4*>(cv + (VS * sg + e) * TS + 4 * g) = make_float4(x[0][e], x[1][e], x[2][e], x[3][e]);
     };
     float sum = 0.0f;
-    if (wave > 0)
-        for (int64_t ch = 0; ch < kKmeanStages - 1 && ch < nch; ++ch) issue(ch);
-    for (int64_t ch = 0; ch < nch; ++ch) {
-        if (wave > 0) {
-            // this chunk has landed once the loads of the (at most two) chunks issued after it are all that is left
-            const int64_t after = (nch - 1 - ch) < kKmeanStages - 2 ? nch - 1 - ch : kKmeanStages - 2;
-            if (after >= 2) wait_vm<2 * LPT>();
-            else if (after == 1) wait_vm<LPT>();
-            else wait_vm<0>();
-        }
-        lds_barrier();                       // chunk ch is in; wavefront 0's reads of chunk ch - 1 are complete
-        if (wave > 0 && ch + kKmeanStages - 1 < nch) issue(ch + kKmeanStages - 1);   // into chunk ch - 1's stage
-        if (wave == 0 && lane < kKmeanFeat) {
-            const uint8_t* st = ring + (ch % kKmeanStages) * kKmeanChunk;
-            const int rows = S - ch * ROWS < ROWS ? (int) (S - ch * ROWS) : ROWS;
-            const int full = rows / 16 * 16;
-            float va[16], vb[16];
-            if (full > 0)
+    if (wave > 0) {
+        for (int64_t ch = 0; ch < kKmeanStages - 1; ++ch) issue(ch);
+        wait_vm<(kKmeanStages - 2) * LPT>();     // chunk 0 has landed
+    }
+    lds_barrier();
+    for (int64_t i = 0; i <= nch; ++i) {
+        if (wave == 0) {
+            if (i >= 1 && lane < F) {
+                const float* cf = conv[(i - 1) & 1] + lane * TS;
+                const int rows = S - (i - 1) * ROWS < ROWS ? (int) (S - (i - 1) * ROWS) : ROWS;
+                if (rows == ROWS) {
+                    // sub-batches of SUB rows, the next one's reads in flight during this one's additions
+                    float4 f[2][SUB / 4];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) va[i] = at(st, i);
-            for (int r = 0; r < full; r += 32) {
-                const bool b1 = r + 16 < full, b2 = r + 32 < full;
-                if (b1)
+                    for (int r = 0; r < SUB / 4; ++r) f[0][r] = *reinterpret_cast<const float4*>(cf + 4 * r);
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) vb[i] = at(st, r + 16 + i);
+                    for (int sb = 0; sb < ROWS / SUB; ++sb) {
+                        if (sb + 1 < ROWS / SUB)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) sum = sum + va[i];
-                if (b1) {
-                    if (b2)
+                            for (int r = 0; r < SUB / 4; ++r)
+                                f[(sb + 1) & 1][r] = *reinterpret_cast<const float4*>(cf + (sb + 1) * SUB + 4 * r);
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) va[i] = at(st, r + 32 + i);
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) sum = sum + vb[i];
+                        for (int r = 0; r < SUB / 4; ++r) {
+                            sum = sum + f[sb & 1][r].x;
+                            sum = sum + f[sb & 1][r].y;
+                            sum = sum + f[sb & 1][r].z;
+                            sum = sum + f[sb & 1][r].w;
+                        }
+                    }
+                } else {
+                    for (int r = 0; r < rows; ++r) sum = sum + cf[r];
                 }
             }
-            for (int r = full; r < rows; ++r) sum = sum + at(st, r);
+        } else if (i < nch) {
+            convert(i);
+            issue(i + kKmeanStages - 1);         // into chunk i - 1's stage, converted before the last barrier
+            wait_vm<(kKmeanStages - 2) * LPT>(); // chunk i + 1 has landed
         }
+        lds_barrier();                           // chunk i converted, chunk i + 1 in, chunk i - 1's sums read
     }
-    if (wave == 0 && lane < kKmeanFeat) mean[c0 + lane] = sum / (float) S;
+    if (wave > 0) wait_vm<0>();                  // no direct load outlives the block
+    else if (lane < F) mean[c0 + lane] = sum / (float) S;
 }
 // the same sums with element loads, for rows that are not 16-byte aligned
 template <int DT>
@@ -567,15 +611,6 @@ __global__ __launch_bounds__(256, DK == 256 ? 1 : 3) void attn_kernel(AttnArgs P
 }
 
 
-// One direct global -> LDS load (16 bytes a lane to lds + 16 lane) written as inline asm: the compiler then does
-// not track it, where for the builtin it makes every later LDS read wait for all direct loads in flight (it cannot
-// tell the stages apart), which would make each step wait for the refill issued at its start. The caller's wait_vm
-// before each barrier orders these loads; the memory clobber keeps the compiler from moving LDS accesses across
-// them.
-__device__ __forceinline__ void attn_dma16(const void* g, const void* lds_dst) {
-    const uint32_t m = (uint32_t) (uintptr_t) lds_dst;
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
-}
 
 constexpr int kAttnPPQ = 256;            // queries of a pipelined block
 // 1.5 2^23: for |n| < 2^22 the float kScoreBias + n has the bits kScoreBiasBits + n, so int32 score products started

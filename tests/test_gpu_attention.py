@@ -106,6 +106,32 @@ def test_attention_peaked_and_shifted(dev_sage, dev_16, sage):
     check(got, want, o.F32, "peaked")
 
 
+@pytest.mark.parametrize("dt", [o.BF16, o.F16, o.F32])
+@pytest.mark.parametrize("S,H,D", [(1, 2, 128), (191, 1, 64), (192, 2, 64), (384, 1, 128), (385, 2, 128),
+                                   (2017, 3, 64), (5000, 1, 64)])
+def test_attention_kmean(dev_sage, dt, S, H, D):
+    """k's mean (h3sycl.cpp:1732-1737), seen through the output. A per-feature constant taken from k moves all of a
+    query's scores alike and the softmax cancels it, so in ordinary inputs a wrong mean only shows through the
+    quantization. Here each feature of k is a large power of two C_f plus or minus C_f 2^-7 in pairs of rows of
+    opposite sign: the float32 sum in token order is exact and the mean is C_f, so k - mean is +-C_f 2^-7. A mean
+    that misses one row then moves the output by a relative L2 of about 8e-2 (a CPU model of the scores from the
+    oracle's quantizer), a missed chunk or mixed-up features by 0.15 to 1. Lengths around the 384- and 192-row
+    chunks of the 16-bit and float32 inputs, and past the eight-chunk ring."""
+    stride = H * D
+    g = np.random.default_rng(S + 7 * H)
+    q = o.to_dt(g.standard_normal((S, stride)).astype(np.float32), dt).ravel()
+    C = 2.0 ** ((10 if dt == o.F16 else 14) + g.integers(0, 4, stride))          # C (1 +- 2^-7) exact in every type
+    sgn = g.choice([-1.0, 1.0], (S // 2, stride))
+    e = np.zeros((S, stride))
+    e[0:2 * (S // 2):2], e[1:2 * (S // 2):2] = sgn, -sgn
+    k = o.to_dt((C * (1.0 + e * 2.0 ** -7)).astype(np.float32), dt).ravel()
+    v = o.to_dt(g.standard_normal((S, stride)).astype(np.float32), dt).ravel()
+    want, _, _, _, _, km = o.attention(q, k, v, dt, S, H, D, stride, out_dt=o.F32, sage=True)
+    assert np.array_equal(km, C.astype(np.float32)), "the oracle's mean is the constant"
+    got = run(dev_sage, q, k, v, dt, S, H, D, stride, o.F32)
+    check(got, want, o.F32, f"k mean S={S} H={H} D={D}")
+
+
 @pytest.mark.parametrize("sage", [True, False])
 @pytest.mark.parametrize("per_tile", [12.0, 30.0])
 def test_attention_rising_scores(dev_sage, dev_16, sage, per_tile):
