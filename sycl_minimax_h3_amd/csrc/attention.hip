@@ -88,7 +88,26 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
     P.nqb = (int) (Sp / qblock);
     P.kvdiv = (int) (Hq / Hkv);
     P.Spk = Sp;
-    const unsigned grid = (unsigned) (Hq * P.nqb);
+    const int64_t nblocks = Hq * P.nqb;
+    P.nfull = nblocks; P.nsplit = 1; P.ts = 0; P.po = nullptr; P.pml = nullptr;
+    // the pipelined kernel's last round: when it would fill at most half the CUs, its blocks each become up to
+    // c->attn_split blocks of consecutive key tiles, whose results attn_merge_kernel combines
+    int64_t tail = 0;
+    if (pp) {
+        const int64_t cus = c->cus, T = (S + kAttnRows - 1) / kAttnRows, last = nblocks % cus;
+        const int64_t want = std::min<int64_t>({(int64_t) c->attn_split, last ? cus / last : 1, T});
+        if (last > 0 && 2 * last <= cus && want > 1) {
+            const int64_t ts = (T + want - 1) / want, ns = (T + ts - 1) / ts;
+            if (ns > 1) {
+                P.po = c->scratch<float>(Ctx::ATT_PART, (size_t) (last * ns * kAttnPPQ * (128 + 2)));
+                if (!P.po) return -1;
+                P.pml = P.po + last * ns * kAttnPPQ * 128;
+                tail = last;
+                P.nfull = nblocks - last; P.nsplit = (int) ns; P.ts = (int) ts;
+            }
+        }
+    }
+    const unsigned grid = (unsigned) (P.nfull + tail * P.nsplit);
     timer.mark();
     // heads of 64, 128 or 256 features into an aligned out take the plain stores; others the masked ones
     const bool pad = D != DK || !aligned16(out);
@@ -106,6 +125,7 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
     if (pp) {
         if (sage) attn_pl_kernel<true, 4><<<grid, 512, 0, c->stream>>>(P);
         else attn_pl_kernel<false, 4><<<grid, 512, 0, c->stream>>>(P);
+        if (tail) attn_merge_kernel<<<(unsigned) ((tail * kAttnPPQ * 32 + 255) / 256), 256, 0, c->stream>>>(P, tail);
     } else if (causal) H3_ATTN(false, true)
     else if (sage) H3_ATTN(true, false)
     else H3_ATTN(false, false)

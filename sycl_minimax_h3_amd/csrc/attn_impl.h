@@ -388,6 +388,13 @@ struct AttnArgs {
     int nqb;                  // query blocks per head (of 128 queries, or 256 in the pipelined kernel)
     int kvdiv;                // query heads per key/value head: head h reads k and v of head h / kvdiv
     int64_t Spk;              // rows of the prepared k and v^T (Sp unless they come from another sequence)
+    // the pipelined kernel's split of the last round: blocks [nfull, nfull + tail * nsplit) each take key tiles
+    // [s ts, s ts + ts) of query block nfull + (b - nfull) / nsplit (s = (b - nfull) % nsplit) and leave O, m and l
+    // in po / pml for attn_merge_kernel; nfull = the grid and nsplit = 1 when nothing is split
+    int64_t nfull;
+    int nsplit, ts;
+    float* po;                // [tail * nsplit, 256, DK] O before the division by l
+    float* pml;               // [tail * nsplit, 256, 2] m and l
 };
 
 // the chunk of row r (rows of CPR 16-byte chunks) where logical chunk c is stored: rows of fewer than 16 chunks
@@ -629,6 +636,8 @@ constexpr int kAttnPPTiles = 4096;       // key tiles it takes (sequences of up 
 // (tile j + NS) at the start of step j + 1, every wavefront issuing its share of the direct loads, which it waits for
 // before the barrier that publishes them. The ring's loads are inline asm (attn_dma16), the head's k scales are
 // copied into LDS once, and the int8 score products start from kScoreBias's bits: see the helpers above.
+// A block of a split last round (AttnArgs::nfull) walks only its range of key tiles, counted from its first, and
+// leaves O, m and l to attn_merge_kernel.
 template <bool SAGE, int NS>
 __global__ __launch_bounds__(512, 1) void attn_pl_kernel(AttnArgs P) {
     constexpr int DK = 128, ESZ = SAGE ? 1 : 2, RB = DK * ESZ, CPR = RB / 16, NQF = RB / 32;
@@ -645,12 +654,23 @@ __global__ __launch_bounds__(512, 1) void attn_pl_kernel(AttnArgs P) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // blocks go to the 8 XCDs round robin: renumbered so that each XCD takes a contiguous run (the blocks of few
     // heads at a time, which then share K and V^T in its L2)
+    // (32-bit block arithmetic: the host keeps the grid below 2^31; 64-bit divisions here delayed every block's start)
     int b = (int) blockIdx.x;
-    if (gridDim.x % 8 == 0) b = (b % 8) * (int) (gridDim.x / 8) + b / 8;
+    // a block of the split last round: its query block and its range of key tiles (slot: its partial sums)
+    int slot = -1, t0 = 0;
+    const int nfull = (int) P.nfull, Tall = (int) ((P.S + kAttnRows - 1) / kAttnRows);
+    int T = Tall;
+    if (b < nfull) {
+        if (nfull % 8 == 0) b = (b % 8) * (nfull / 8) + b / 8;
+    } else {
+        slot = b - nfull;
+        b = nfull + slot / P.nsplit;
+        t0 = (slot % P.nsplit) * P.ts;
+        T = Tall - t0 < P.ts ? Tall - t0 : P.ts;
+    }
     const int64_t h = b / P.nqb, qb = b % P.nqb, Sp = P.Sp, S = P.S;
     const int64_t q0 = qb * kAttnPPQ + 32 * wave;             // this wavefront's first query
     const int64_t nbp = Sp / kAttnRows;
-    const int T = (int) ((S + kAttnRows - 1) / kAttnRows);
 
     v4i_a qf[NQF];
     {
@@ -662,9 +682,10 @@ __global__ __launch_bounds__(512, 1) void attn_pl_kernel(AttnArgs P) {
 
     const int64_t g = h / P.kvdiv, Spk = P.Spk;
     if constexpr (SAGE)
-        for (int i = tid; i < T; i += 512) ksl[i] = P.ks[g * nbp + i];
-    const int8_t* kbase = P.k + g * Spk * RB;
-    const uint16_t* vbase = P.vt + g * DK * Spk;
+        for (int i = tid; i < T; i += 512) ksl[i] = P.ks[g * nbp + t0 + i];
+    // tiles are counted from t0 (this block's first key tile) from here on
+    const int8_t* kbase = P.k + (g * Spk + (int64_t) t0 * kAttnRows) * RB;
+    const uint16_t* vbase = P.vt + g * DK * Spk + (int64_t) t0 * kAttnRows;
     // tile t into stage t % NS; a tile past the last loads the last one again (into a stage no tile uses then), so
     // that every wavefront has the same loads in flight at every wait
     auto issue = [&](int t) {
@@ -754,7 +775,7 @@ __global__ __launch_bounds__(512, 1) void attn_pl_kernel(AttnArgs P) {
             for (int i = 0; i < 16; ++i) x[16 * j + i] = xf[i];
         }
         const float f = SAGE ? fq * ksl[tn] : fq;
-        const int lim = (int) (S - (int64_t) tn * kAttnRows) - 4 * hl;
+        const int lim = (int) (S - (int64_t) (t0 + tn) * kAttnRows) - 4 * hl;
         auto live = [&](int i) { return 32 * (i / 16) + 8 * ((i % 16) / 4) + i % 4 < lim; };
         // The weights p = 2^(score f - m) rounded to half, packed into pb as the P v products take them, and their
         // sum over this lane's keys. SAGE: score f - m = x f - (kScoreBias f + m), with one rounding of the offset
@@ -815,7 +836,7 @@ __global__ __launch_bounds__(512, 1) void attn_pl_kernel(AttnArgs P) {
     };
     using yes = std::true_type;
     using no = std::false_type;
-    const bool ragged = S % kAttnRows != 0;
+    const bool ragged = S % kAttnRows != 0 && t0 + T == Tall;   // this range ends with the sequence's cut tile
     // Step t: refill the ring (tile t + NS - 1); the scores of tile t + 1 (DS); tile t's P v products (DPV) with the
     // softmax of tile t + 1 (independent of them) between them; O's rescale, if the softmax moved the reference; the
     // wait for tile t + 2 and one barrier. Tile j is read in steps j - 1 (K) and j (V^T); its stage is refilled at
@@ -857,6 +878,21 @@ __global__ __launch_bounds__(512, 1) void attn_pl_kernel(AttnArgs P) {
     step(t, no{}, yes{}, no{});                                // step T - 1: the last P v products
     wait_vm<0>();                                              // no direct load may land after the block ends
 
+    // ---- a split block: O, m and l of its key range for attn_merge_kernel ----
+    if (slot >= 0) {
+        const int64_t row = (int64_t) slot * kAttnPPQ + 32 * wave + ql;
+        float* po = P.po + row * DK;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq)
+                *reinterpret_cast<float4*>(po + 32 * dt + 8 * gq + 4 * hl) =
+                    make_float4(o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2], o[dt][4 * gq + 3]);
+        const float lsum = attn_pair_sum(l);                   // m is the same in both lanes of the query
+        if (hl == 0) *reinterpret_cast<float2*>(P.pml + 2 * row) = make_float2(m, lsum);
+        return;
+    }
+
     // ---- out = O / l, rounded to half, in out's type ----
     const float inv = 1.0f / attn_pair_sum(l);
     const int64_t qi = q0 + ql;
@@ -884,6 +920,40 @@ __global__ __launch_bounds__(512, 1) void attn_pl_kernel(AttnArgs P) {
         else if (P.out_dt == H3S_BF16) store(std::integral_constant<int, H3S_BF16>{});
         else store(std::integral_constant<int, H3S_F16>{});
     }
+}
+
+// The split blocks' results combined: per query, M = max m_s, O = sum 2^(m_s - M) O_s, l = sum 2^(m_s - M) l_s,
+// out = O / l rounded to half, in out's type (as the pipelined kernel's own epilogue). One thread a query and four
+// features of the DK = 128.
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs P, int64_t tail) {
+    constexpr int DK = 128;
+    const int64_t id = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    const int f0 = 4 * (int) (id % (DK / 4));
+    const int64_t qq = id / (DK / 4);                          // query row among the split blocks' query blocks
+    if (qq >= tail * kAttnPPQ) return;
+    const int64_t tb = qq / kAttnPPQ, ob = P.nfull + tb, h = ob / P.nqb, qi = (ob % P.nqb) * kAttnPPQ + qq % kAttnPPQ;
+    if (qi >= P.S) return;
+    float M = -INFINITY;
+    for (int s = 0; s < P.nsplit; ++s) M = fmaxf(M, P.pml[2 * ((tb * P.nsplit + s) * kAttnPPQ + qq % kAttnPPQ)]);
+    float l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < P.nsplit; ++s) {
+        const int64_t row = (tb * P.nsplit + s) * kAttnPPQ + qq % kAttnPPQ;
+        const float2 ml = *reinterpret_cast<const float2*>(P.pml + 2 * row);
+        const float w = __builtin_amdgcn_exp2f(ml.x - M);
+        const float4 x = *reinterpret_cast<const float4*>(P.po + row * DK + f0);
+        l = __builtin_fmaf(w, ml.y, l);
+        o[0] = __builtin_fmaf(w, x.x, o[0]); o[1] = __builtin_fmaf(w, x.y, o[1]);
+        o[2] = __builtin_fmaf(w, x.z, o[2]); o[3] = __builtin_fmaf(w, x.w, o[3]);
+    }
+    const float inv = 1.0f / l;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = round_f16(o[i] * inv);
+    const int esz = P.out_dt == H3S_F32 ? 4 : 2;
+    char* at = reinterpret_cast<char*>(P.out) + ((qi * P.H + h) * DK + f0) * esz;
+    if (P.out_dt == H3S_F32) *reinterpret_cast<float4*>(at) = make_float4(v[0], v[1], v[2], v[3]);
+    else if (P.out_dt == H3S_BF16) *reinterpret_cast<uint2*>(at) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+    else *reinterpret_cast<uint2*>(at) = make_uint2(pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
 }
 
 }  // namespace h3

@@ -63,6 +63,7 @@ struct Ctx {
         ATT_K,       //   k prepared
         ATT_V,       //   v as half, transposed [H, D, Sp]
         ATT_AUX,     //   the block scales and k's mean
+        ATT_PART,    //   the split blocks' partial sums (O, m, l)
         LIN_F32,     // h3s_linear / h3s_linear_acc: the float32 product of a row chunk
         N_REGIONS
     };
@@ -71,6 +72,7 @@ struct Ctx {
     void* blas = nullptr;                  // h3s_linear: the rocBLAS handle, on this context's stream
     bool sage_want = true;                 // H3S_ATTN=onednn: false
     int64_t sage_min_s = 8192;             // H3S_SAGE_MIN_S
+    int attn_split = 8;                    // H3S_ATTN_SPLIT: most key ranges a block of a short last round takes (1: none)
     int64_t quant_wave_min = 8192;         // H3S_QUANT_WAVE_MIN_ROWS: fewest rows for the one-wavefront-a-row quantizer
     // H3S_PROFILE (kernels/h3sycl.cpp:117, 228): the int8 linear's time by pass, summed over its row chunks and
     // reported at h3s_destroy; attention's time by phase, reported per call

@@ -104,6 +104,7 @@ static const char* region_name(Ctx::Region r) {
         case Ctx::ATT_K: return "attention scratch (k)";
         case Ctx::ATT_V: return "attention scratch (v)";
         case Ctx::ATT_AUX: return "attention scratch (scales and k's mean)";
+        case Ctx::ATT_PART: return "attention scratch (partial sums)";
         case Ctx::LIN_F32: return "linear scratch (float32 product)";
         default: return "scratch";
     }
@@ -145,6 +146,8 @@ static void init(Ctx& c) {
         if (c.name.empty() || c.name.find("gfx") == 0) c.name = std::string(p.gcnArchName);
         if (p.multiProcessorCount > 0) c.cus = p.multiProcessorCount;
     }
+    // H3S_CUS: the compute units that grids are sized by (fewer than the device's: tests of the grid shapes)
+    if (const char* e = std::getenv("H3S_CUS")) c.cus = std::max(1, std::min(c.cus, std::atoi(e)));
     size_t free_b = 0, total = 0;
     (void) hipMemGetInfo(&free_b, &total);
     double frac = 0.94;
@@ -159,6 +162,9 @@ static void init(Ctx& c) {
     // H3S_SAGE_MIN_S sets the shortest sequence that takes the int8 (SageAttention) form
     if (const char* e = std::getenv("H3S_ATTN")) c.sage_want = std::strcmp(e, "onednn") != 0;
     if (const char* e = std::getenv("H3S_SAGE_MIN_S")) c.sage_min_s = std::max<int64_t>(0, std::atoll(e));
+    // the pipelined attention kernel: a last round of blocks that fills at most half the CUs is split into up to this
+    // many key ranges a block (1: never)
+    if (const char* e = std::getenv("H3S_ATTN_SPLIT")) c.attn_split = std::max(1, std::min(64, std::atoi(e)));
     // the row quantizer's layout: one wavefront a row from this many rows on (four wavefronts a row below)
     if (const char* e = std::getenv("H3S_QUANT_WAVE_MIN_ROWS")) c.quant_wave_min = std::max<int64_t>(0, std::atoll(e));
 }

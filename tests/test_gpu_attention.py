@@ -132,6 +132,39 @@ def test_attention_kmean(dev_sage, dt, S, H, D):
     check(got, want, o.F32, f"k mean S={S} H={H} D={D}")
 
 
+@pytest.fixture(scope="module")
+def dev_split():
+    """Contexts for the pipelined kernel's split of a short last round, per form: no split (H3S_ATTN_SPLIT=1), the
+    default, and the default with grids sized for 16 or 12 compute units (H3S_CUS), so that a few hundred tokens
+    make full rounds and a split last one (at 12, full blocks that the XCD renumbering leaves in order)."""
+    modes = {"none": {"H3S_ATTN_SPLIT": "1"}, "default": {}, "cus16": {"H3S_CUS": "16"}, "cus12": {"H3S_CUS": "12"}}
+    ds = {}
+    for sage in (True, False):
+        form = {"H3S_SAGE_MIN_S": "0"} if sage else {"H3S_ATTN": "onednn"}
+        for name, env in modes.items():
+            ds[(sage, name)] = _open_with({**form, **env})
+    yield ds
+    for d in ds.values():
+        d.close()
+
+
+@pytest.mark.parametrize("sage", [True, False])
+@pytest.mark.parametrize("mode", ["none", "default", "cus16", "cus12"])
+@pytest.mark.parametrize("S,H", [(64, 1), (777, 3), (2000, 5)])
+def test_attention_split_last_round(dev_split, sage, mode, S, H):
+    """Heads of 128 features (the pipelined kernel). The grids: 64 tokens, one block of one key tile (never split);
+    777 tokens x 3 heads, 12 blocks of 13 tiles (split 7 ways on 256 CUs, not at all on 16 or 12); 2000 x 5, 40 blocks
+    of 32 tiles (6 ways on 256 CUs; on 16, 32 full blocks and 8 split in 2; on 12, 36 full blocks and 4 split in
+    3). The split blocks' partial sums are merged by attn_merge_kernel."""
+    D = 128
+    stride = H * D
+    q, k, v = qkv(90 + S, S, H, D, o.BF16, stride)
+    want = o.attention(q, k, v, o.BF16, S, H, D, stride, out_dt=o.BF16, sage=sage)
+    want = want[0] if sage else want
+    got = run(dev_split[(sage, mode)], q, k, v, o.BF16, S, H, D, stride, o.BF16)
+    check(got, want, o.BF16, f"{'int8' if sage else '16-bit'} {mode} S={S} H={H}")
+
+
 @pytest.mark.parametrize("sage", [True, False])
 @pytest.mark.parametrize("per_tile", [12.0, 30.0])
 def test_attention_rising_scores(dev_sage, dev_16, sage, per_tile):
