@@ -6,8 +6,9 @@
 // its pairs, so the rotation needs no exchange - and pass-through slot q the features [rot + qV, min(rot + qV + V,
 // D)). A head takes P2 lanes (its slot count rounded up to a power of two), so a wave holds 64 / P2 heads side by
 // side; the head's sum of squares is the lane's own (its first features, then their partners), then an xor
-// butterfly over its P2 lanes: the canonical order of the CPU oracle. One wave per token: it reads the token's
-// cos/sin row once and the weights once, then every head of q and of k. Two kernels:
+// butterfly over its P2 lanes: the canonical order of the CPU oracle. One wave per token, or two that take half its
+// (tensor, head group) units each: a wave reads the token's cos/sin row and the weights once, then its heads. Two
+// kernels:
 //   rope_kernel      half and D - rot whole 16-byte vectors (rot = D, 96 or 48 at D = 128, the VAE's 48 at 64):
 //                    a slot is whole chunks, read and written straight from and to memory with 16-byte accesses;
 //   rope_any_kernel  any even rot (the DiT's rot = 6 x its frequencies, e.g. 126 for 21): a head is copied to
@@ -20,15 +21,18 @@ namespace h3 {
 
 constexpr int kUnits = 8;   // (tensor, head group) units whose loads are in flight together
 
-template <int XDT, int P2>
+// PARTS: wavefronts a token (2: each takes half its (tensor, head group) units); KU: units whose loads are in
+// flight together
+template <int XDT, int P2, int PARTS, int KU = kUnits / PARTS>
 __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M, int H, int D, int64_t stride,
                                                    const float* __restrict__ w0, const float* __restrict__ w1, float eps,
                                                    const float* __restrict__ cs, int rot) {
     constexpr int V = Vec<XDT>::V;
     constexpr int HPW = kWave / P2;   // heads side by side in a wave
     const int lane = threadIdx.x & 63;
-    const int64_t tok = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t wid = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6), tok = wid / PARTS;
     if (tok >= M) return;
+    const int part = (int) (wid - tok * PARTS);
     const int half = rot / 2, nrot = half / V, npass = (D - rot) / V, P = nrot + npass;
     const int slot = lane % P2, hh = lane / P2;
     const bool active = slot < P, rotated = slot < nrot;
@@ -46,23 +50,23 @@ __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M
     }
     const int ngroups = (H + HPW - 1) / HPW;
     const int ntens = x1 ? 2 : 1;
-    const int nunits = ntens * ngroups;
-    for (int u0 = 0; u0 < nunits; u0 += kUnits) {
-        uint4 ra[kUnits], rb[kUnits];
+    const int per = ntens * ngroups / PARTS, ubeg = part * per, uend = ubeg + per;   // this wavefront's units
+    for (int u0 = ubeg; u0 < uend; u0 += KU) {
+        uint4 ra[KU], rb[KU];
 #pragma unroll
-        for (int k = 0; k < kUnits; ++k) {
+        for (int k = 0; k < KU; ++k) {
             // every lane loads from a valid place (idle lanes and units past the end read head 0 / the last unit
             // again, and their values are never used): no branch between the loads
-            const int u = u0 + k < nunits ? u0 + k : nunits - 1, t = u / ngroups, h0 = (u % ngroups) * HPW + hh;
+            const int u = u0 + k < uend ? u0 + k : uend - 1, t = u / ngroups, h0 = (u % ngroups) * HPW + hh;
             const int head = active && h0 < H ? h0 : 0;
             const uint16_t* base = (const uint16_t*) (t ? x1 : x0) + (tok * stride + (int64_t) head * D) * (16 / V / 2);
             ra[k] = ld_nt(base + (active ? off0 : 0) * (16 / V / 2));
             rb[k] = ld_nt(base + (rotated ? off1 : 0) * (16 / V / 2));
         }
 #pragma unroll
-        for (int k = 0; k < kUnits; ++k) {
+        for (int k = 0; k < KU; ++k) {
             const int u = u0 + k;
-            if (u >= nunits) break;   // uniform across the wave
+            if (u >= uend) break;     // uniform across the wave
             const int t = u / ngroups, head = (u % ngroups) * HPW + hh;
             const bool ok = active && head < H;
             float a[V], b[V];
@@ -240,11 +244,19 @@ static int rope_launch(const char* fn, void* ctx, void* x0, void* x1, int x_dt, 
         if (p && !aligned16(p)) return fail(std::string(fn) + ": tensors must be 16-byte aligned");
     Ctx* c = ctx_of(ctx, fn);
     if (!c) return -1;
-    const unsigned grid = (unsigned) ((M + 3) / 4);
     // whole-chunk slots go straight through memory; any other split through the wavefront's LDS stage
     const bool whole = half % V == 0 && (D - rot_dim) % V == 0;
+    // a token's units (tensor, group of 64 / P2 heads) in two wavefronts where they split evenly (whole-chunk
+    // slots) and the launch is short: twice the wavefronts, each holding half the loads, so the last of them end
+    // sooner (16896 tokens of q and k: 100.5 -> 96.3 us; at 47104 tokens one wavefront a token stays 0.5 % faster)
+    const int64_t nunits = (x1 ? 2 : 1) * ((H + kWave / P2 - 1) / (kWave / P2));
+    const int parts = whole && nunits % 2 == 0 && M <= 32768 ? 2 : 1;
+    const unsigned grid = (unsigned) ((M * parts + 3) / 4);
 #define LP(XDT, PP)                                                                                               \
-    if (whole) rope_kernel<XDT, PP><<<grid, 256, 0, c->stream>>>(x0, x1, M, (int) H, (int) D, stride, w0, w1, eps, cs, rot_dim); \
+    if (whole && parts == 2)                                                                                      \
+        rope_kernel<XDT, PP, 2><<<grid, 256, 0, c->stream>>>(x0, x1, M, (int) H, (int) D, stride, w0, w1, eps, cs, rot_dim); \
+    else if (whole)                                                                                               \
+        rope_kernel<XDT, PP, 1><<<grid, 256, 0, c->stream>>>(x0, x1, M, (int) H, (int) D, stride, w0, w1, eps, cs, rot_dim); \
     else rope_any_kernel<XDT, PP><<<grid, 256, 0, c->stream>>>(x0, x1, M, (int) H, (int) D, stride, w0, w1, eps, cs, rot_dim)
 #define LD(XDT)                         \
     switch (P2) {                       \

@@ -173,6 +173,26 @@ def test_rms_rope(dev, x_dt, H, D, rot, pad):
     assert_bits_equal(xt.to_numpy(), want, "rms_rope")
 
 
+def test_rms_rope_long(dev):
+    """Past 32768 tokens a token's heads run in one wavefront (shorter launches split them over two): q alone and
+    the fused q and k, 33000 tokens of 16 heads of 128, all features rotated."""
+    M, H, D, rot = 33000, 16, 128, 128
+    w_ = H * D
+    qk = inputs(17, M * 2 * w_, o.BF16)
+    wq, wk = weight(18, D), weight(19, D)
+    cs = cs_table(20, M, rot)
+    want_q = o.rms_rope(qk, o.BF16, M, H, D, 2 * w_, wq, 1e-5, cs, rot)
+    want = o.rms_rope(want_q[w_:], o.BF16, M, H, D, 2 * w_, wk, 1e-5, cs, rot)
+    want = np.concatenate([want_q[:w_], want])
+    t = up(dev, qk, "BF16", [M * 2 * w_])
+    ops.qk_rms_rope(ops.Rows(t, 0, 2 * w_, M, H, D), ops.Rows(t, w_, 2 * w_, M, H, D), up(dev, wq, "F32", [D]),
+                    up(dev, wk, "F32", [D]), 1e-5, up(dev, cs, "F32", [cs.size]), rot)
+    assert_bits_equal(t.to_numpy(), want, "qk_rms_rope, 33000 tokens")
+    t2 = up(dev, qk, "BF16", [M * 2 * w_])
+    ops.rms_rope(ops.Rows(t2, 0, 2 * w_, M, H, D), up(dev, wq, "F32", [D]), 1e-5, up(dev, cs, "F32", [cs.size]), rot)
+    assert_bits_equal(t2.to_numpy(), want_q, "rms_rope, 33000 tokens")
+
+
 def test_qk_rms_rope_in_a_qkv_buffer(dev):
     """q and k inside the qkv linear's output, stride 3 H D (engine/h3-core/src/dit.rs:345-348)."""
     M, H, D, rot = 37, 32, 128, 128
