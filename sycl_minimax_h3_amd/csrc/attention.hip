@@ -98,9 +98,8 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
         const int64_t want = std::min<int64_t>({(int64_t) c->attn_split, last ? cus / last : 1, T});
         if (last > 0 && 2 * last <= cus && want > 1) {
             const int64_t ts = (T + want - 1) / want, ns = (T + ts - 1) / ts;
-            if (ns > 1) {
-                P.po = c->scratch<float>(Ctx::ATT_PART, (size_t) (last * ns * kAttnPPQ * (128 + 2)));
-                if (!P.po) return -1;
+            // (no room for the partial sums under the memory cap: the last round runs unsplit)
+            if (ns > 1 && (P.po = c->scratch<float>(Ctx::ATT_PART, (size_t) (last * ns * kAttnPPQ * (128 + 2))))) {
                 P.pml = P.po + last * ns * kAttnPPQ * 128;
                 tail = last;
                 P.nfull = nblocks - last; P.nsplit = (int) ns; P.ts = (int) ts;
