@@ -256,6 +256,20 @@ __global__ __launch_bounds__(256) void attn_qk_prep_vec_kernel(const void* __res
     const int64_t nbp = Sp / kAttnRows, b = blockIdx.x % nbp, h = blockIdx.x / nbp, r0 = b * kAttnRows;
     const int tid = threadIdx.x;
     const char* base = reinterpret_cast<const char*>(src) + (r0 * stride + h * D) * (int64_t) (16 / V);
+    // k's mean at this thread's chunks, loaded before the rows so that both are in flight together (loaded after
+    // them, each chunk's mean waited for the rows and then for itself)
+    float mk[N][V];
+    if constexpr (SAGE) {
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const int c = (tid + 256 * k) % CPR;
+#pragma unroll
+            for (int e = 0; e < V; e += 4) {
+                const float4 t = mean ? *reinterpret_cast<const float4*>(mean + h * D + c * V + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+                mk[k][e] = t.x; mk[k][e + 1] = t.y; mk[k][e + 2] = t.z; mk[k][e + 3] = t.w;
+            }
+        }
+    }
     float v[N][V];
 #pragma unroll
     for (int k = 0; k < N; ++k) {
@@ -268,10 +282,10 @@ __global__ __launch_bounds__(256) void attn_qk_prep_vec_kernel(const void* __res
         float m = 0.0f;
 #pragma unroll
         for (int k = 0; k < N; ++k) {
-            const int u = tid + 256 * k, r = u / CPR, c = u % CPR;
+            const int u = tid + 256 * k, r = u / CPR;
             if (mean) {
 #pragma unroll
-                for (int e = 0; e < V; ++e) v[k][e] = v[k][e] - mean[h * D + c * V + e];
+                for (int e = 0; e < V; ++e) v[k][e] = v[k][e] - mk[k][e];
             }
             if (r0 + r < S)
 #pragma unroll
