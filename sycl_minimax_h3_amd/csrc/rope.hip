@@ -20,6 +20,7 @@
 namespace h3 {
 
 constexpr int kUnits = 8;   // (tensor, head group) units whose loads are in flight together
+constexpr int kRopeMaxD = 1024;   // the largest head rope_kernel takes: 64 slots of V pairs (16-bit types)
 
 // PARTS: wavefronts a token (2: each takes half its (tensor, head group) units); KU: units whose loads are in
 // flight together
@@ -31,23 +32,30 @@ __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M
     constexpr int HPW = kWave / P2;   // heads side by side in a wave
     const int lane = threadIdx.x & 63;
     const int64_t wid = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6), tok = wid / PARTS;
-    if (tok >= M) return;
     const int part = (int) (wid - tok * PARTS);
     const int half = rot / 2, nrot = half / V, npass = (D - rot) / V, P = nrot + npass;
     const int slot = lane % P2, hh = lane / P2;
     const bool active = slot < P, rotated = slot < nrot;
+    // the token's cos/sin pairs of this lane's slot, in flight during the weights' staging below and taken apart
+    // only where the rotation uses them
+    float4 csv[V / 2];
+    if (rotated && tok < M) {
+        const float* c = cs + (tok * half + (int64_t) slot * V) * 2;
+#pragma unroll
+        for (int k = 0; k < V / 2; ++k) csv[k] = *reinterpret_cast<const float4*>(c + 4 * k);
+    }
+    // the norm weights of both tensors, staged once a block (every thread, before any wavefront leaves): read
+    // from global memory after each unit's reduction, their wait also waited for the batch's remaining rows
+    __shared__ __attribute__((aligned(16))) float wl[2][kRopeMaxD];
+    for (int i = threadIdx.x; i < D; i += 256) {
+        wl[0][i] = w0[i];
+        if (x1) wl[1][i] = w1[i];
+    }
+    __syncthreads();
+    if (tok >= M) return;
     const int off0 = rotated ? slot * V : rot + (slot - nrot) * V;   // this lane's chunk(s) inside the head
     const int off1 = half + slot * V;
 
-    float co[V], si[V];
-    if (rotated) {
-        const float* c = cs + (tok * half + (int64_t) slot * V) * 2;
-#pragma unroll
-        for (int k = 0; k < 2 * V; k += 4) {
-            const float4 t = *reinterpret_cast<const float4*>(c + k);
-            co[k / 2] = t.x; si[k / 2] = t.y; co[k / 2 + 1] = t.z; si[k / 2 + 1] = t.w;
-        }
-    }
     const int ngroups = (H + HPW - 1) / HPW;
     const int ntens = x1 ? 2 : 1;
     const int per = ntens * ngroups / PARTS, ubeg = part * per, uend = ubeg + per;   // this wavefront's units
@@ -83,13 +91,17 @@ __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M
             s = wave_sum<P2>(s);
             if (!ok) continue;
             const float inv = inv_root(s, (float) D, eps);
-            const float* w = t ? w1 : w0;
+            const float* w = wl[t];
             float wa[V];
             load_f32x(w + off0, wa, V);
             uint16_t* base = (uint16_t*) (t ? x1 : x0) + (tok * stride + (int64_t) head * D) * (16 / V / 2);
             if (rotated) {
-                float wb[V], oa[V], ob[V];
+                float wb[V], oa[V], ob[V], co[V], si[V];
                 load_f32x(w + off1, wb, V);
+#pragma unroll
+                for (int k = 0; k < V / 2; ++k) {
+                    co[2 * k] = csv[k].x; si[2 * k] = csv[k].y; co[2 * k + 1] = csv[k].z; si[2 * k + 1] = csv[k].w;
+                }
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
                     const float A = a[e] * inv * wa[e], B = b[e] * inv * wb[e];
@@ -236,7 +248,7 @@ static int rope_launch(const char* fn, void* ctx, void* x0, void* x1, int x_dt, 
         return fail(std::string(fn) + ": D and the stride must be whole 16-byte vectors (multiples of " + std::to_string(V) + ")");
     const int P = (int) ((half + V - 1) / V + (D - rot_dim + V - 1) / V);
     const int P2 = pow2ceil(P);
-    if (P2 > kWave) return fail(std::string(fn) + ": a head of more than 64 slots is not supported");
+    if (P2 > kWave || D > kRopeMaxD) return fail(std::string(fn) + ": a head of more than 64 slots is not supported");
     if (H > (1 << 24)) return fail(std::string(fn) + ": too many heads");
     if (!w0 || (x1 && !w1)) return fail(std::string(fn) + ": the norm weight is required");
     if (rot_dim > 0 && !cs) return fail(std::string(fn) + ": the rotation table is required");
