@@ -259,10 +259,9 @@ static int rope_launch(const char* fn, void* ctx, void* x0, void* x1, int x_dt, 
     // whole-chunk slots go straight through memory; any other split through the wavefront's LDS stage
     const bool whole = half % V == 0 && (D - rot_dim) % V == 0;
     // a token's units (tensor, group of 64 / P2 heads) in two wavefronts where they split evenly (whole-chunk
-    // slots) and the launch is short: twice the wavefronts, each holding half the loads, so the last of them end
-    // sooner (16896 tokens of q and k: 100.5 -> 96.3 us; at 47104 tokens one wavefront a token stays 0.5 % faster)
+    // slots): twice the wavefronts, each holding half the loads, so the last of them end sooner
     const int64_t nunits = (x1 ? 2 : 1) * ((H + kWave / P2 - 1) / (kWave / P2));
-    const int parts = whole && nunits % 2 == 0 && M <= 32768 ? 2 : 1;
+    const int parts = whole && nunits % 2 == 0 ? 2 : 1;
     const unsigned grid = (unsigned) ((M * parts + 3) / 4);
 #define LP(XDT, PP)                                                                                               \
     if (whole && parts == 2)                                                                                      \

@@ -174,8 +174,8 @@ def test_rms_rope(dev, x_dt, H, D, rot, pad):
 
 
 def test_rms_rope_long(dev):
-    """Past 32768 tokens a token's heads run in one wavefront (shorter launches split them over two): q alone and
-    the fused q and k, 33000 tokens of 16 heads of 128, all features rotated."""
+    """A long launch, two wavefronts a token: q alone and the fused q and k, 33000 tokens of 16 heads of 128, all
+    features rotated."""
     M, H, D, rot = 33000, 16, 128, 128
     w_ = H * D
     qk = inputs(17, M * 2 * w_, o.BF16)
