@@ -12,10 +12,11 @@ namespace h3 {
 
 // q of Hq heads (row stride qs) and k, v of Hkv heads (row stride kvs) prepared into aq [Hq, Sp, DK], ak [Hkv, Sp, DK]
 // (int8 codes with their scales for SAGE, else half) and av [Hkv, DK, Sp] (half), DK = attn_dk(D), zero past D
+// (q_in_kernel: the pipelined kernel forms q's fragments from q itself, so q is not prepared)
 template <int DT>
 static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S, int64_t Sp, int64_t Hq, int64_t Hkv, int D,
-                 int64_t qs_stride, int64_t kv_stride, bool sage, int8_t* aq, int8_t* ak, uint16_t* av, float* qs, float* ks,
-                 float* km) {
+                 int64_t qs_stride, int64_t kv_stride, bool sage, bool q_in_kernel, int8_t* aq, int8_t* ak, uint16_t* av,
+                 float* qs, float* ks, float* km) {
     const unsigned qblocks = (unsigned) (Hq * (Sp / kAttnRows)), kvblocks = (unsigned) (Hkv * (Sp / kAttnRows));
     const int DK = attn_dk(D);
     // 16-byte rows: every tensor aligned, the strides whole numbers of 16-byte vectors, and a head of exactly 64, 128
@@ -43,10 +44,10 @@ static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S,
         const int64_t hd = Hkv * D;
         if (vec && hd % kKmeanFeat == 0) attn_kmean_kernel<DT><<<(unsigned) (hd / kKmeanFeat), 256, 0, c->stream>>>(k, S, kv_stride, km);
         else attn_kmean_rows_kernel<DT><<<(unsigned) ((hd + 255) / 256), 256, 0, c->stream>>>(k, S, hd, kv_stride, km);
-        qk(q, qs_stride, qblocks, nullptr, aq, qs);
+        if (!q_in_kernel) qk(q, qs_stride, qblocks, nullptr, aq, qs);
         qk(k, kv_stride, kvblocks, km, ak, ks);
     } else {
-        qk(q, qs_stride, qblocks, nullptr, aq, nullptr);
+        if (!q_in_kernel) qk(q, qs_stride, qblocks, nullptr, aq, nullptr);
         qk(k, kv_stride, kvblocks, nullptr, ak, nullptr);
     }
     if (!vec) attn_v_prep_kernel<DT><<<kvblocks, 256, 0, c->stream>>>(v, S, Sp, D, DK, kv_stride, av);
@@ -72,12 +73,14 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
     float* af = c->scratch<float>(Ctx::ATT_AUX, (size_t) ((Hq + Hkv) * nbp + Hkv * D));
     if (!aq || !ak || !av || !af) return -1;
     float *qs = af, *ks = af + Hq * nbp, *km = af + (Hq + Hkv) * nbp;
+    // the pipelined kernel reads q's rows itself where they are whole 16-byte vectors
+    const bool q_in_kernel = pp && aligned16(q) && (qs_stride * elem_size(dt)) % 16 == 0;
     PhaseTimer timer(c);
     timer.mark();
     switch (dt) {
-        case H3S_BF16: prep<H3S_BF16>(c, q, k, v, S, Sp, Hq, Hkv, (int) D, qs_stride, kv_stride, sage, aq, ak, av, qs, ks, km); break;
-        case H3S_F16: prep<H3S_F16>(c, q, k, v, S, Sp, Hq, Hkv, (int) D, qs_stride, kv_stride, sage, aq, ak, av, qs, ks, km); break;
-        default: prep<H3S_F32>(c, q, k, v, S, Sp, Hq, Hkv, (int) D, qs_stride, kv_stride, sage, aq, ak, av, qs, ks, km); break;
+        case H3S_BF16: prep<H3S_BF16>(c, q, k, v, S, Sp, Hq, Hkv, (int) D, qs_stride, kv_stride, sage, q_in_kernel, aq, ak, av, qs, ks, km); break;
+        case H3S_F16: prep<H3S_F16>(c, q, k, v, S, Sp, Hq, Hkv, (int) D, qs_stride, kv_stride, sage, q_in_kernel, aq, ak, av, qs, ks, km); break;
+        default: prep<H3S_F32>(c, q, k, v, S, Sp, Hq, Hkv, (int) D, qs_stride, kv_stride, sage, q_in_kernel, aq, ak, av, qs, ks, km); break;
     }
     if (launched(fn)) return -1;
     AttnArgs P;
@@ -88,6 +91,9 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
     P.nqb = (int) (Sp / qblock);
     P.kvdiv = (int) (Hq / Hkv);
     P.Spk = Sp;
+    P.qraw = q_in_kernel ? q : nullptr;
+    P.qstride = qs_stride;
+    P.q_dt = dt;
     const int64_t nblocks = Hq * P.nqb;
     P.nfull = nblocks; P.nsplit = 1; P.ts = 0; P.po = nullptr; P.pml = nullptr;
     // the pipelined kernel's last round: when it would fill at most half the CUs, its blocks each become up to

@@ -411,6 +411,11 @@ struct AttnArgs {
     int nsplit, ts;
     float* po;                // [tail * nsplit, 256, DK] O before the division by l
     float* pml;               // [tail * nsplit, 256, 2] m and l
+    // the pipelined kernel with qraw set reads q from the caller's rows (stride qstride elements of type q_dt, 16-byte
+    // aligned) and forms its fragments itself, as attn_qk_prep_vec_kernel would (q and qs are then unused)
+    const void* qraw;
+    int64_t qstride;
+    int q_dt;
 };
 
 // the chunk of row r (rows of CPR 16-byte chunks) where logical chunk c is stored: rows of fewer than 16 chunks
@@ -689,12 +694,63 @@ __global__ __launch_bounds__(512, 1) void attn_pl_kernel(AttnArgs P) {
     const int64_t nbp = Sp / kAttnRows;
 
     v4i_a qf[NQF];
-    {
+    float fq = P.c;
+    // With P.qraw: this lane's 64 features of its query straight from the caller's rows (fragment kk: FR features from
+    // 32 kk + 16 hl for int8 codes, 16 kk + 8 hl for halves), turned into the fragments attn_qk_prep_vec_kernel would
+    // have written: halves here; int8 codes after the prologue's barrier, where the two wavefronts of a 64-row scale
+    // block (wavefronts 2j, 2j + 1) have each left their 32 rows' max in qmax. Rows past S are zeros.
+    constexpr int FR = SAGE ? 16 : 8;
+    __shared__ float qmax[8];
+    float qx[NQF * FR];
+    float qm = 0.0f;
+    if (P.qraw) {
+        const int64_t qi = q0 + ql;
+        const int qes = P.q_dt == H3S_F32 ? 4 : 2;
+        const char* qrow = reinterpret_cast<const char*>(P.qraw) + (qi * P.qstride + h * DK) * qes;
+#pragma unroll
+        for (int kk = 0; kk < NQF; ++kk) {
+            const int f0 = SAGE ? 32 * kk + 16 * hl : 16 * kk + 8 * hl;
+#pragma unroll
+            for (int c8 = 0; c8 < FR; c8 += 8) {
+                float* x = qx + kk * FR + c8;
+                if (qi >= S) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+                } else if (P.q_dt == H3S_F32) {
+                    const float4 a = *reinterpret_cast<const float4*>(qrow + (f0 + c8) * 4);
+                    const float4 b = *reinterpret_cast<const float4*>(qrow + (f0 + c8) * 4 + 16);
+                    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+                } else {
+                    const uint4 u = *reinterpret_cast<const uint4*>(qrow + (f0 + c8) * 2);
+                    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        x[2 * i] = P.q_dt == H3S_BF16 ? bf16_lo(w[i]) : f16_lo(w[i]);
+                        x[2 * i + 1] = P.q_dt == H3S_BF16 ? bf16_hi(w[i]) : f16_hi(w[i]);
+                    }
+                }
+            }
+        }
+        if constexpr (SAGE) {
+#pragma unroll
+            for (int i = 0; i < NQF * FR; ++i) qm = fmaxf(qm, fabsf(qx[i]));
+            qm = wave_max<64>(qm);
+            if (lane == 0) qmax[wave] = qm;
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < NQF; ++kk) {
+                v4i_a w;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[i] = (int) pack_f16(qx[kk * FR + 2 * i], qx[kk * FR + 2 * i + 1]);
+                qf[kk] = w;
+            }
+        }
+    } else {
         const int8_t* qrow = P.q + ((h * Sp + q0 + ql) * DK) * ESZ;
 #pragma unroll
         for (int kk = 0; kk < NQF; ++kk) qf[kk] = *reinterpret_cast<const v4i_a*>(qrow + 32 * kk + 16 * hl);
+        if constexpr (SAGE) fq = P.qs[h * nbp + q0 / kAttnRows] * P.c;
     }
-    const float fq = SAGE ? P.qs[h * nbp + q0 / kAttnRows] * P.c : P.c;
 
     const int64_t g = h / P.kvdiv, Spk = P.Spk;
     if constexpr (SAGE)
@@ -881,7 +937,30 @@ __global__ __launch_bounds__(512, 1) void attn_pl_kernel(AttnArgs P) {
     wait_vm<0>();
     for (int t = 0; t < NS - 1; ++t) issue(t);
     wait_vm<(NS - 2) * (KI + VI)>();
-    lds_barrier();                                             // tile 0 is in
+    lds_barrier();                                             // tile 0 is in; qmax is written
+    if constexpr (SAGE) {
+        if (P.qraw) {
+            // q's codes (attn_qk_prep_vec_kernel's arithmetic): the 64-row block's max over both wavefronts
+            const float m = fmaxf(qm, qmax[wave ^ 1]);
+            const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < NQF; ++kk) {
+                v4i_a w;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    uint32_t b = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float cc = fminf(fmaxf(roundf(qx[kk * FR + 4 * i + e] * inv), -127.0f), 127.0f);
+                        b |= (uint32_t) ((int) cc & 255) << (8 * e);
+                    }
+                    w[i] = (int) b;
+                }
+                qf[kk] = w;
+            }
+            fq = m / 127.0f * P.c;
+        }
+    }
     if (T == 1 && ragged) step(-1, yes{}, no{}, yes{});
     else step(-1, yes{}, no{}, no{});
     int t = 0;
