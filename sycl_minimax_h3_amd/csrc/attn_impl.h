@@ -989,32 +989,49 @@ __global__ __launch_bounds__(512, 1) void attn_pl_kernel(AttnArgs P) {
     }
 
     // ---- out = O / l, rounded to half, in out's type ----
+    // Through LDS, so that the stores are whole rows: each wavefront stages its 32 queries, 256 bytes of features a
+    // row per pass (all 128 features of a 16-bit out, 64 of a float32 one), into an area of its own in the ring
+    // (free once every wavefront is past its last P v products), then reads it back as 16-byte chunks, four rows an
+    // instruction.
     const float inv = 1.0f / attn_pair_sum(l);
-    const int64_t qi = q0 + ql;
+    lds_barrier();
+    constexpr int OPITCH = 256 + 16;                           // bytes a staged row (16 of pad: rows on other banks)
+    static_assert(8 * 32 * OPITCH <= NS * STAGE, "the output staging fits in the ring");
+    int8_t* ost = lds + wave * 32 * OPITCH;
     auto store = [&](auto dt_tag) {
         constexpr int OUT = decltype(dt_tag)::value;
         constexpr int esz = OUT == H3S_F32 ? 4 : 2;
-        char* orow = reinterpret_cast<char*>(P.out) + ((qi * P.H + h) * DK) * esz;
+        constexpr int FP = 256 / esz, NPASS = DK / FP, DTP = FP / 32;   // features, passes, o[] registers a pass
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
+        for (int pass = 0; pass < NPASS; ++pass) {
 #pragma unroll
-            for (int gq = 0; gq < 4; ++gq) {
-                // registers 4 gq .. 4 gq + 3 of o[dt]: features 32 dt + 8 gq + 4 hl + (0..3)
-                const int f0 = 32 * dt + 8 * gq + 4 * hl;
-                float v[4];
+            for (int d = 0; d < DTP; ++d)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = round_f16(o[dt][4 * gq + i] * inv);
-                char* at = orow + f0 * esz;
-                if constexpr (OUT == H3S_F32) *reinterpret_cast<float4*>(at) = make_float4(v[0], v[1], v[2], v[3]);
-                else if constexpr (OUT == H3S_BF16) *reinterpret_cast<uint2*>(at) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
-                else *reinterpret_cast<uint2*>(at) = make_uint2(pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
+                for (int gq = 0; gq < 4; ++gq) {
+                    // registers 4 gq .. 4 gq + 3 of o[dt]: features 32 dt + 8 gq + 4 hl + (0..3)
+                    const int dt = pass * DTP + d;
+                    float v[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = round_f16(o[dt][4 * gq + i] * inv);
+                    int8_t* at = ost + ql * OPITCH + (32 * d + 8 * gq + 4 * hl) * esz;
+                    if constexpr (OUT == H3S_F32) *reinterpret_cast<float4*>(at) = make_float4(v[0], v[1], v[2], v[3]);
+                    else if constexpr (OUT == H3S_BF16) *reinterpret_cast<uint2*>(at) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+                    else *reinterpret_cast<uint2*>(at) = make_uint2(pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
+                }
+            wave_lds_sync();
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int ch = lane + 64 * k, r = ch / 16, c = ch % 16;
+                const uint4 val = *reinterpret_cast<const uint4*>(ost + r * OPITCH + 16 * c);
+                const int64_t qr = q0 + r;
+                if (qr < S) *reinterpret_cast<uint4*>(reinterpret_cast<char*>(P.out) + ((qr * P.H + h) * DK + pass * FP) * esz + 16 * c) = val;
             }
+            wave_lds_sync();
+        }
     };
-    if (qi < S) {
-        if (P.out_dt == H3S_F32) store(std::integral_constant<int, H3S_F32>{});
-        else if (P.out_dt == H3S_BF16) store(std::integral_constant<int, H3S_BF16>{});
-        else store(std::integral_constant<int, H3S_F16>{});
-    }
+    if (P.out_dt == H3S_F32) store(std::integral_constant<int, H3S_F32>{});
+    else if (P.out_dt == H3S_BF16) store(std::integral_constant<int, H3S_BF16>{});
+    else store(std::integral_constant<int, H3S_F16>{});
 }
 
 // The split blocks' results combined: per query, M = max m_s, O = sum 2^(m_s - M) O_s, l = sum 2^(m_s - M) l_s,
