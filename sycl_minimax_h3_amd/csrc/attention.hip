@@ -67,14 +67,14 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
     const int64_t Sp = (S + qblock - 1) / qblock * qblock, nbp = Sp / kAttnRows;
     const int64_t esz = sage ? 1 : 2, DK = attn_dk(D);
     if (Hq * (Sp / qblock) > 0x7fffffff) return fail(std::string(fn) + ": too many query blocks");
-    int8_t* aq = c->scratch<int8_t>(Ctx::ATT_Q, (size_t) (Sp * Hq * DK * esz));
+    // the pipelined kernel reads q's rows itself where they are whole 16-byte vectors (no prepared q then)
+    const bool q_in_kernel = pp && aligned16(q) && (qs_stride * elem_size(dt)) % 16 == 0;
+    int8_t* aq = q_in_kernel ? nullptr : c->scratch<int8_t>(Ctx::ATT_Q, (size_t) (Sp * Hq * DK * esz));
     int8_t* ak = c->scratch<int8_t>(Ctx::ATT_K, (size_t) (Sp * Hkv * DK * esz));
     uint16_t* av = c->scratch<uint16_t>(Ctx::ATT_V, (size_t) (Sp * Hkv * DK));
     float* af = c->scratch<float>(Ctx::ATT_AUX, (size_t) ((Hq + Hkv) * nbp + Hkv * D));
-    if (!aq || !ak || !av || !af) return -1;
+    if ((!aq && !q_in_kernel) || !ak || !av || !af) return -1;
     float *qs = af, *ks = af + Hq * nbp, *km = af + (Hq + Hkv) * nbp;
-    // the pipelined kernel reads q's rows itself where they are whole 16-byte vectors
-    const bool q_in_kernel = pp && aligned16(q) && (qs_stride * elem_size(dt)) % 16 == 0;
     PhaseTimer timer(c);
     timer.mark();
     switch (dt) {
