@@ -98,7 +98,8 @@ int h3s_linear(void* ctx, const void* x, int dt, int64_t M, int64_t K, const voi
                void* out, int out_dt);
 
 /* Causal attention with grouped heads (kernels/h3sycl.h:104-108): Hq query heads over Hkv key/value heads, rows of
- * q at stride qs and of k, v at stride kvs; the 16-bit form. Head sizes 64 and 128. */
+ * q at stride qs and of k, v at stride kvs; the 16-bit form. Any head size up to 256 (zero-padded to 64, 128 or 256
+ * features inside, the output stored at D). */
 int h3s_attention_causal(void* ctx, const void* q, const void* k, const void* v, int dt, int64_t L, int64_t Hq, int64_t Hkv, int64_t D,
                          int64_t qs, int64_t kvs, void* out);
 /* Not implemented here (text encoder, upscalers, audio): -1. Replace kernels/h3sycl.h:106-158. */
@@ -153,7 +154,8 @@ int h3s_gate_add(void* ctx, void* x, int x_dt, int64_t M, int64_t C, const void*
 
 /* Attention over S tokens of H heads of D (any head size up to 256), rows at element stride `stride`, out [S, H D]
  * (h3s_attention), and B independent sequences of S tokens each (h3s_attention_batch). The reference's choice of form: the int8
- * (SageAttention) form from H3S_SAGE_MIN_S tokens (8192) on unless H3S_ATTN=onednn, the 16-bit form below it.
+ * (SageAttention) form from H3S_SAGE_MIN_S tokens (8192) on for heads of 64 or 128 features unless H3S_ATTN=onednn
+ * (kernels/h3sycl.cpp:1706), the 16-bit form otherwise.
  * Replace kernels/h3sycl.h:190-200. */
 int h3s_attention(void* ctx, const void* q, const void* k, const void* v, int dt, int64_t S, int64_t H, int64_t D,
                   int64_t stride, void* out, int out_dt);
@@ -182,6 +184,11 @@ int h3s_norm_quant(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, con
  * q int8 [M, C], s float32 [M]: the inputs of h3s_int8_gemm_dequant for fc2. */
 int h3s_swiglu_quant(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, int h_dt, int rot, int group, int8_t* q,
                      float* s);
+
+/* h3s_int8_linear's quantizer on its own, the first of its two passes (kernels/h3sycl.cpp:404-474, 521-575):
+ * x [M, K] in x_dt, rotated per group of `group` features by the regular Hadamard (0: no rotation), then
+ * s[r] = max(max|y| / 127, 1e-30), q = rint(y / s[r]). q int8 [M, K], s float32 [M]: the inputs of h3s_int8_gemm_dequant. */
+int h3s_int8_quantize(void* ctx, const void* x, int x_dt, int64_t M, int64_t K, int group, int8_t* q, float* s);
 
 /* What a sampler step fixes for every block, on the device instead of the reference's host loops:
  * h3s_adaln_tables (engine/h3-core/src/dit.rs:155-174, Block::tables): the six AdaLN tables of one block for R timestep
@@ -243,9 +250,15 @@ int h3s_layout(void* ctx, int64_t text_len, int64_t latent_t, int64_t latent_h, 
  * results as h3s_int8_linear; the quantized rows go into a fixed device array of the library (64 MiB of codes and
  * 65536 row scales, held on each GPU the library runs on until the process ends) instead of the context's scratch.
  * Any M (rows go through in chunks that fit the array); K at most 65536, else -1 with the reason. Calls on one GPU
- * share its array: calls that overlap on one GPU (two streams or two contexts at once) race. */
+ * share its array: calls that overlap on one GPU (two streams or two contexts at once) race. The array (64.25 MiB a
+ * GPU) is part of the library's code object, not of a context: it is outside the H3S_MEM_FRACTION cap and is not
+ * counted by h3s_mem_used. */
 int h3s_int8_linear_noalloc(void* ctx, const void* x, int x_dt, int64_t M, int64_t K, const int8_t* w, int64_t N,
                             const float* wscale, int64_t n_wscale, const float* bias, void* out, int out_dt, int group);
+/* How many device and host allocations, events, streams and library handles libh3hip has made in this process, counted
+ * as they are attempted. No counterpart in the reference: a diagnostic, for tests and callers that must show a call
+ * path allocates nothing (h3s_int8_linear_noalloc leaves it unchanged). */
+uint64_t h3s_alloc_count(void);
 
 #ifdef __cplusplus
 }

@@ -84,6 +84,8 @@ ADDITIONS = {
     "h3s_qk_rms_rope": (i32, [vp, vp, vp, i32, i64, i64, i64, i64, vp, vp, f32, vp, i32]),
     "h3s_int8_gemm_dequant": (i32, [vp, vp, vp, i64, i64, vp, i64, vp, i64, vp, i32, vp, i32]),
     "h3s_int8_linear_noalloc": (i32, [vp, vp, i32, i64, i64, vp, i64, vp, i64, vp, vp, i32, i32]),
+    "h3s_int8_quantize": (i32, [vp, vp, i32, i64, i64, i32, vp, vp]),
+    "h3s_alloc_count": (u64, []),
     "h3s_layout_plan": (i64, [i64, i64, i64, i64, i64, vp, i64, vp, i64, vp, vp, vp, i64]),
     "h3s_layout": (i32, [vp, i64, i64, i64, i64, i64, vp, i64, vp, i64, vp, vp, vp, i64]),
 }

@@ -1,8 +1,8 @@
 // attention.hip - h3s_attention, h3s_attention_batch (kernels/h3sycl.h:185-197, kernels/h3sycl.cpp:1433-1917) and
 // h3s_attention_causal (kernels/h3sycl.h:104-108) on the kernels of attn_impl.h. The form follows the reference's
-// choice: the int8 (SageAttention) form for sequences of at least H3S_SAGE_MIN_S tokens (8192) unless
-// H3S_ATTN=onednn, the 16-bit form otherwise. Any head size up to 256 (the causal form's limit, h3sycl.cpp:877): a
-// head runs in the kernel of 64, 128 or 256 features, zero-padded past D.
+// choice: the int8 (SageAttention) form for sequences of at least H3S_SAGE_MIN_S tokens (8192) with heads of 64 or
+// 128 features unless H3S_ATTN=onednn (kernels/h3sycl.cpp:1706), the 16-bit form otherwise. Any head size up to 256
+// (the causal form's limit, h3sycl.cpp:877): a head runs in the kernel of 64, 128 or 256 features, zero-padded past D.
 #include <cmath>
 #include <cstdio>
 
@@ -60,7 +60,9 @@ static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S,
 // causal: query i sees keys 0 .. i (the 16-bit form, as the reference's causal kernel computes in float)
 static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, const void* v, int dt, int64_t S, int64_t Hq,
                          int64_t Hkv, int64_t D, int64_t qs_stride, int64_t kv_stride, void* out, int out_dt, bool causal) {
-    const bool sage = !causal && c->sage_want && S >= c->sage_min_s;
+    // the int8 form as the reference takes it (kernels/h3sycl.cpp:1706): heads of 64 or 128 features, and S * D * H
+    // within int32; every other call runs the 16-bit form
+    const bool sage = !causal && c->sage_want && S >= c->sage_min_s && (D == 64 || D == 128) && S <= INT32_MAX / D / Hq;
     // heads of 128 features into an aligned out, no causal mask: the pipelined kernel (256 queries a block)
     const bool pp = !causal && D == 128 && aligned16(out) && S <= (int64_t) kAttnPPTiles * kAttnRows;
     const int64_t qblock = pp ? kAttnPPQ : kAttnQBlock;
@@ -132,8 +134,11 @@ static int attention_one(Ctx* c, const char* fn, const void* q, const void* k, c
         else attn_pl_kernel<false, 4><<<grid, 512, 0, c->stream>>>(P);
         if (tail) attn_merge_kernel<<<(unsigned) ((tail * kAttnPPQ * 32 + 255) / 256), 256, 0, c->stream>>>(P, tail);
     } else if (causal) H3_ATTN(false, true)
-    else if (sage) H3_ATTN(true, false)
-    else H3_ATTN(false, false)
+    else if (sage) {
+        // (the int8 form only at 64 or 128 features, above)
+        if (DK == 128) H3_ATTN_D(true, 128, false)
+        else H3_ATTN_D(true, 64, false)
+    } else H3_ATTN(false, false)
 #undef H3_ATTN
 #undef H3_ATTN_D
     if (launched(fn)) return -1;

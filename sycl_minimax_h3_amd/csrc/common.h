@@ -102,6 +102,8 @@ class PhaseTimer {
     std::vector<hipEvent_t> ev_;
 };
 
+// one more device allocation, event, stream or library handle made by the library (h3s_alloc_count)
+void count_alloc();
 // the context of an entry point: NULL with an error when ctx is NULL; makes its device current
 Ctx* ctx_of(void* ctx, const char* fn);
 // the status of the last launch on this thread, as an error naming fn

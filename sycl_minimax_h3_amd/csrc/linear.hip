@@ -17,6 +17,7 @@ void release_blas(Ctx* c) {
 static rocblas_handle blas_of(Ctx* c) {
     if (!c->blas) {
         rocblas_handle h = nullptr;
+        count_alloc();
         if (rocblas_create_handle(&h) != rocblas_status_success) { set_error("rocBLAS: no handle"); return nullptr; }
         if (rocblas_set_stream(h, c->stream) != rocblas_status_success) {
             (void) rocblas_destroy_handle(h);

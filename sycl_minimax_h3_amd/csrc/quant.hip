@@ -66,6 +66,21 @@ H3S_EXPORT int h3s_norm_quant(void* ctx, const void* x, int x_dt, int64_t M, int
     return dispatch(c, fn, x_dt, A, QUANT_NORM, p);
 } catch (const std::exception& e) { return fail(e.what()); }
 
+// h3s_int8_linear's first pass on its own (kernels/h3sycl.cpp:404-474, 521-575): x [M, K] rotated per group (0: none,
+// else the regular Hadamard of that size) and quantized to codes q [M, K] and row scales s [M].
+H3S_EXPORT int h3s_int8_quantize(void* ctx, const void* x, int x_dt, int64_t M, int64_t K, int group, int8_t* q, float* s) try {
+    if (M <= 0 || K <= 0) return 0;
+    const char* fn = "h3s_int8_quantize";
+    if (!dt_ok(x_dt)) return fail(std::string(fn) + ": unknown element type");
+    if (group < 0 || (group > 0 && (group > 256 || K % group != 0 || (group & (group - 1)) != 0 || (__builtin_ctz((unsigned) group) & 1))))
+        return fail(std::string(fn) + ": unsupported ConvRot group size (0, or a power of 4 at most 256 dividing K)");
+    if (!x || !q || !s) return fail(std::string(fn) + ": x, q and s are required");
+    if (!aligned16(x) || !aligned16(q)) return fail(std::string(fn) + ": tensors must be 16-byte aligned");
+    Ctx* c = ctx_of(ctx, fn);
+    if (!c) return -1;
+    return launch_quantize(c, x, x_dt, M, K, group, q, s);
+} catch (const std::exception& e) { return fail(e.what()); }
+
 H3S_EXPORT int h3s_swiglu_quant(void* ctx, const void* x, int x_dt, int64_t M, int64_t C, int h_dt, int rot, int group,
                                 int8_t* q, float* s) try {
     if (M <= 0 || C <= 0) return 0;

@@ -1,6 +1,7 @@
 // runtime.hip - contexts, device memory, copies and the error convention of libh3hip.so (the HIP counterpart of
 // kernels/h3sycl.cpp:77-402), and the entry points of kernels/h3sycl.h that have no implementation here.
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <map>
@@ -11,6 +12,8 @@
 namespace h3 {
 
 thread_local std::string g_err;
+static std::atomic<uint64_t> g_allocs{0};
+void count_alloc() { g_allocs.fetch_add(1, std::memory_order_relaxed); }
 void set_error(const std::string& msg) { g_err = msg; }
 int fail(const std::string& msg) { g_err = msg; return -1; }
 
@@ -51,6 +54,7 @@ PhaseTimer::~PhaseTimer() {
 void PhaseTimer::mark() {
     if (!on_) return;
     hipEvent_t e = nullptr;
+    count_alloc();
     if (hipEventCreate(&e) != hipSuccess) { on_ = false; (void) hipGetLastError(); return; }
     ev_.push_back(e);
     (void) hipEventRecord(e, c_->stream);
@@ -126,6 +130,7 @@ void* Ctx::scratch_bytes(Region r, size_t bytes) {
     }
     if (!budget.take(want, region_name(r))) return nullptr;
     void* p = nullptr;
+    count_alloc();
     if (hipMalloc(&p, want) != hipSuccess || !p) {
         (void) hipGetLastError();
         budget.give_back(want);
@@ -176,6 +181,7 @@ static Ctx* open_on(int index) {
     if (hipSetDevice(index) != hipSuccess) { set_error("hipSetDevice failed"); return nullptr; }
     auto* c = new Ctx;
     c->device = index;
+    count_alloc();
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         set_error("could not create a stream");
@@ -245,6 +251,7 @@ H3S_EXPORT void* h3s_alloc(void* ctx, uint64_t bytes) try {
     if (!c) return nullptr;
     if (!c->budget.take(bytes, "h3s_alloc")) return nullptr;
     void* p = nullptr;
+    count_alloc();
     if (hipMalloc(&p, bytes ? bytes : 256) != hipSuccess || !p) {
         (void) hipGetLastError();
         c->budget.give_back(bytes);
@@ -308,6 +315,7 @@ H3S_EXPORT void* h3s_alloc_host(void* ctx, uint64_t bytes) {
     Ctx* c = ctx_of(ctx, "h3s_alloc_host");
     if (!c) return nullptr;
     void* p = nullptr;
+    count_alloc();
     if (hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault) != hipSuccess) {
         set_error("h3s_alloc_host: the runtime refused " + std::to_string(bytes >> 20) + " MiB of pinned memory");
         return nullptr;
@@ -322,6 +330,10 @@ H3S_EXPORT void h3s_free_host(void* ctx, void* p) {
     (void) hipHostFree(p);
 }
 
+// Device allocations, host allocations, events, streams and library handles the library has made in this process,
+// counted as they are attempted: a diagnostic that shows a call path allocates nothing.
+H3S_EXPORT uint64_t h3s_alloc_count(void) { return g_allocs.load(std::memory_order_relaxed); }
+
 H3S_EXPORT int h3s_upload(void* ctx, void* dst, const void* src_pinned, uint64_t bytes) {
     Ctx* c = ctx_of(ctx, "h3s_upload");
     if (!c) return -1;
@@ -333,6 +345,7 @@ H3S_EXPORT int h3s_upload(void* ctx, void* dst, const void* src_pinned, uint64_t
     }
     {
         std::lock_guard<std::mutex> l(c->copy_mu);
+        if (!c->copy_stream) count_alloc();
         if (!c->copy_stream && hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking) != hipSuccess)
             return fail("h3s_upload: could not create the copy stream");
     }

@@ -31,7 +31,8 @@ def declared():
 
 def test_header_and_library_agree(api):
     names = declared()
-    assert len(names) == 60          # the 49 of kernels/h3sycl.h, 10 additions, the allocation-free int8 linear
+    # the 49 of kernels/h3sycl.h, 11 additions, the allocation-free int8 linear and the allocation counter
+    assert len(names) == 62
     out = subprocess.run(["nm", "-D", "--defined-only", api.path], capture_output=True, text=True, check=True).stdout
     exported = sorted(set(l.split()[-1] for l in out.splitlines() if l.split()[-1].startswith("h3s_")))
     assert exported == names, f"missing {set(names) - set(exported)}, extra {set(exported) - set(names)}"
@@ -48,6 +49,11 @@ def test_every_name_h3sys_resolves(api):
     assert set("h3s_" + n for n in H3SYS + ["create"]) == set(A.REFERENCE)
 
 
+def test_alloc_count_is_a_counter(api):
+    n = api.alloc_count()
+    assert isinstance(n, int) and n >= 0 and api.alloc_count() == n
+
+
 def test_no_context_is_an_error(api):
     assert api.rms_norm_mod(None, 16, 2, 4, 4096, 16, 1e-6, None, None, None, 16, 2) == -1
     assert "no context" in api.error()
@@ -57,6 +63,10 @@ def test_no_context_is_an_error(api):
 
 def test_arguments_are_checked_before_the_device(api):
     p = 1 << 20   # a 16-byte aligned address that is never dereferenced: every call below fails its checks first
+    assert api.int8_quantize(None, p, 2, 8, 256, 128, p, p) == -1
+    assert "group" in api.error()
+    assert api.int8_quantize(None, p + 8, 2, 8, 256, 64, p, p) == -1
+    assert "aligned" in api.error()
     assert api.int8_linear(None, p, 2, 8, 256, p, 8, p, 1, None, p, 2, 128) == -1
     assert "group" in api.error()
     assert api.int8_linear(None, p, 2, 8, 100, p, 8, p, 1, None, p, 2, 0) == -1

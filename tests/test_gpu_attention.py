@@ -244,13 +244,20 @@ def test_attention_refuses(dev):
                                                (300, 1, 130, 0, o.BF16)])
 def test_attention_head_sizes(dev_sage, dev_16, sage, S, H, D, pad, out_dt):
     """Heads of any size up to 256: 256 in its own kernel, the others zero-padded to 64, 128 or 256 features in the
-    preparation and stored at their own size (odd sizes one feature at a time)."""
+    preparation and stored at their own size (odd sizes one feature at a time). The int8 form is the reference's only
+    at 64 and 128 features (kernels/h3sycl.cpp:1706): on a context that asks for it at every length (dev_sage), these
+    head sizes still take the 16-bit form and match the 16-bit oracle."""
     stride = H * D + pad
     q, k, v = qkv(110 + D, S, H, D, o.BF16, stride)
-    want = o.attention(q, k, v, o.BF16, S, H, D, stride, out_dt=out_dt, sage=sage)
-    want = want[0] if sage else want
+    assert D not in (64, 128)
+    want = o.attention(q, k, v, o.BF16, S, H, D, stride, out_dt=out_dt, sage=False)
     got = run(dev_sage if sage else dev_16, q, k, v, o.BF16, S, H, D, stride, out_dt)
-    check(got, want, out_dt, f"{'int8' if sage else '16-bit'} S={S} H={H} D={D}")
+    check(got, want, out_dt, f"16-bit ({'a context asking for int8' if sage else 'default'}) S={S} H={H} D={D}")
+    if sage:
+        # and not the int8 form's result: its quantization moves the output far past the parity bar
+        int8 = o.attention(q, k, v, o.BF16, S, H, D, stride, out_dt=out_dt, sage=True)[0]
+        rel, _ = o.compare(o.from_dt(got, out_dt).astype(np.float32), o.from_dt(int8, out_dt).astype(np.float32))
+        assert rel > 1e-3, f"S={S} D={D}: the result is the int8 form's (relative L2 {rel:.2e} from it)"
 
 
 @pytest.mark.parametrize("dt", [o.BF16, o.F32])

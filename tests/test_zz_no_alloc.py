@@ -1,7 +1,8 @@
 """h3s_int8_linear_noalloc (the int8 linear that allocates nothing: its quantized rows go into the library's fixed
 device array) against h3s_int8_linear, bit for bit, through the C ABI: two calls in a row, the second smaller, so the
 second reuses the array the first filled. The first call is longer than one chunk of the array (64 MiB of codes is
-16384 rows of 4096 features), so the chunk loop runs. Neither call takes anything from the context's budget."""
+16384 rows of 4096 features), so the chunk loop runs. Neither call takes anything from the context's budget, nor
+makes any allocation, event, stream or handle (the library's own count of them, h3s_alloc_count)."""
 import numpy as np
 import pytest
 
@@ -40,9 +41,13 @@ def test_noalloc_matches_int8_linear(ctx, first, second):
         xt, wt, wst = up(dev, x, "BF16", [M, K]), up(dev, w, "I8", [N, K]), up(dev, ws, "F32", [ws.size])
         bt = up(dev, b, "F32", [N]) if bias else None
         got, want = new(dev, DTS[out_dt], [M, N]), new(dev, DTS[out_dt], [M, N])
-        used = dev.mem_used()
+        used, made = dev.mem_used(), dev.api.alloc_count()
         call(dev, dev.api.int8_linear_noalloc, xt, M, K, wt, N, wst, ws.size, bt, got, out_dt, group)
         dev.wait()
         assert dev.mem_used() == used, "the allocation-free entry point took device memory"
+        # no device or host allocation, event, stream or library handle was made on its path
+        assert dev.api.alloc_count() == made, "the allocation-free entry point allocated"
         call(dev, dev.api.int8_linear, xt, M, K, wt, N, wst, ws.size, bt, want, out_dt, group)
+        if i == 0:   # the counter sees allocations: the context's first int8 linear grows its scratch
+            assert dev.api.alloc_count() > made, "h3s_int8_linear's first call on a fresh context allocated nothing"
         assert_bits_equal(got.to_numpy(), want.to_numpy(), f"noalloc call {i}")
