@@ -38,6 +38,7 @@ from __future__ import annotations
 import argparse
 import collections
 import csv
+import fnmatch
 import json
 import math
 import os
@@ -80,10 +81,58 @@ def bytes_cfg():
         "attn_sage_16896x32x128": 4 * M2 * 4096 * 2,     # q, k, v read, out written (the products are the bound)
         "attn_sage_47104x32x128": 4 * M4 * 4096 * 2,
         "attn_f16_4096x32x128": 4 * 4096 * 4096 * 2,     # the 16-bit form (below 8192 tokens)
+        **dit_bytes(M2), **dit_bytes(M4),
         "copy_probe_1GiB": 2 << 30,
         # a plain copy moving config 1's bytes (half read, half written): the floor a launch of that size reaches
         "copy_probe_cfg1_bytes": 2 * CFG1_COPY_ELEMS * 2,
     }
+
+
+# The DiT block of the denoiser as the unchanged engine runs it (engine/h3-core/src/dit.rs:329-369): hidden 5376, 56
+# heads of 128 (q, k, v side by side in rows of 3 x 7168), an MLP of 5376 -> 2 x 14336 -> 5376 (docs/BASELINE.md:13),
+# rot_dim = 6 x 21 frequencies = 126 (dit.rs:71), float32 modulation tables [2, 5376] with the first 5 % of the
+# tokens on table row 1 (engine/h3d/src/jobs.rs:213), every activation bfloat16 (jobs.rs:217).
+DH, DHEADS, DHD, DFF, DROT = 5376, 56, 128, 14336, 126
+DQKV = 3 * DHEADS * DHD
+# the block's int8 linears: (name, K, N), dit.rs:341, 352, 359, 364
+DIT_LINEARS = (("qkv", DH, DQKV), ("out", DHEADS * DHD, DH), ("fc1", DH, 2 * DFF), ("fc2", DFF, DH))
+# the block's stages under the labels of the reference's harness (engine/h3d/src/jobs.rs:269-279), each the sum of
+# the workloads that run it, and the engine's published times per block (docs/PORT-PLAN.md:62-70, on its GPU)
+DIT_STAGES = (
+    ("norm + scale/shift", ("dit_rms_norm_mod", "dit_rms_norm_mod")),
+    ("linear: q, k, v", ("dit_int8_linear_qkv",)),
+    ("per-head norm + rotation (q, k)", ("dit_rms_rope_q_rot126", "dit_rms_rope_k_rot126")),
+    ("attention", ("dit_attention",)),
+    ("linear: attention out", ("dit_int8_linear_out",)),
+    ("gated add", ("dit_gate_add", "dit_gate_add")),
+    ("linear: MLP in", ("dit_int8_linear_fc1",)),
+    ("gated activation + linear: MLP out", ("dit_swiglu", "dit_int8_linear_fc2")),
+)
+DIT_PUBLISHED_MS = {"16.5k tokens": {"the four int8 linears (+ gated activation)": 67, "per-head norm + rotation": 6.2,
+                                     "norms, scale/shift, gated adds": 10.5, "attention": 96, "the block": 177},
+                    "47k tokens": {"the four int8 linears (+ gated activation)": 194, "per-head norm + rotation": 20.8,
+                                   "norms, scale/shift, gated adds": 28.1, "attention": 759, "the block": 998}}
+
+
+def dit_bytes(M: int) -> dict:
+    """Algorithmic bytes per launch of the DiT block's workloads at M tokens."""
+    cs126, cs96 = M * DROT // 2 * 2 * 4, M * 48 * 2 * 4
+    out = {
+        f"dit_rms_norm_mod_{M}": 2 * M * DH * 2 + M * 4,                  # x read, h written, the row table
+        f"dit_rms_rope_q_rot126_{M}": 2 * M * DHEADS * DHD * 2 + cs126,   # q read and written in place, cos/sin
+        f"dit_rms_rope_k_rot126_{M}": 2 * M * DHEADS * DHD * 2 + cs126,
+        f"dit_rms_rope_q_rot96_{M}": 2 * M * DHEADS * DHD * 2 + cs96,
+        f"dit_qk_rms_rope_rot126_{M}": 4 * M * DHEADS * DHD * 2 + cs126,  # the fused pair: cos/sin read once
+        f"dit_gate_add_{M}": 3 * M * DH * 2 + M * 4,                      # x read and written, the projection read
+        f"dit_swiglu_{M}": M * 2 * DFF * 2 + M * DFF * 2,
+        f"dit_norm_quant_g256_{M}": M * DH * 2 + M * DH + M * 4 + M * 4,  # x read, codes and scales, the row table
+        f"dit_swiglu_quant_g256_{M}": M * 2 * DFF * 2 + M * DFF + M * 4,
+        f"dit_attention_{M}": 4 * M * DHEADS * DHD * 2,
+    }
+    for name, K, N in DIT_LINEARS:
+        out[f"dit_quantize_g256_{name}_{M}"] = M * K * 2 + M * K + M * 4     # the int8 linear's first pass
+        out[f"dit_int8_linear_{name}_{M}"] = M * K * 2 + N * K + N * 4 + M * N * 2
+    return out
 
 
 def ring_size(nbytes: int) -> int:
@@ -150,7 +199,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--settle", type=float, default=0.15, help="seconds each kernel runs untimed before its warm-up")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of workload keys to time (default all)")
+    ap.add_argument("--only", default="", help="comma list of workload keys or shell-style patterns to time (default all)")
     ap.add_argument("--mark", action="store_true", help="bracket each timed region with a spin-kernel marker")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also time plain device copies of 1 GiB (the attainable HBM rate; the known-size kernel that "
@@ -182,6 +231,10 @@ def main() -> int:
     T = lambda t, dt=None: Tensor.from_torch(t, dt, dev)   # noqa: E731
     B = bytes_cfg()
     only = set(filter(None, args.only.split(",")))
+
+    def skip(key):
+        """not among --only's keys (shell-style patterns: dit_*rope* takes every key that matches)"""
+        return bool(only) and not any(fnmatch.fnmatchcase(key, k) for k in only)
     marked, steps_of = [], {}
 
     def bf16(*shape, scale=1.0):
@@ -224,11 +277,12 @@ def main() -> int:
 
     kernels, rings = {}, {}
 
-    def run(key, make, steps=20, warmup=3):
-        """times workload `key`: make() builds one buffer set and returns its launch; a ring of them when small"""
-        if only and key not in only:
+    def run(key, make, steps=20, warmup=3, ring=None):
+        """times workload `key`: make() builds one buffer set and returns its launch; a ring of them when small
+        (ring: a fixed count instead)"""
+        if skip(key):
             return
-        n = ring_size(B[key])
+        n = ring or ring_size(B[key])
         fns = [make() for _ in range(n)]
         kernels[key] = timed(key, cycle(fns), steps, warmup)
         rings[key] = n
@@ -252,7 +306,7 @@ def main() -> int:
     ms2 = timed(HEADLINE, cycle(ring2), args.steps, args.warmup)
     kernels[HEADLINE], rings[HEADLINE] = ms2, n2
     # the same launches back to back on one buffer set: part of the 415 MB stays in the Infinity Cache
-    if not only or HEADLINE + "_same_buffers" in only:
+    if not skip(HEADLINE + "_same_buffers"):
         kernels[HEADLINE + "_same_buffers"] = timed(HEADLINE + "_same_buffers", ring2[0], args.steps, args.warmup)
         rings[HEADLINE + "_same_buffers"] = 1
     del ring2
@@ -346,6 +400,87 @@ def main() -> int:
     run("cfg4_rmsnorm_wht128_quant_16896", make4(M2))
     run("cfg5a_rmsnorm_mod_quant_16896", make5a(M2))
 
+    # ---- the DiT block's bandwidth-bound calls, as the unchanged engine makes them (dit.rs:329-369), at 16896 and
+    # 47104 tokens; each takes buffers of its own call shape (cache-cold rings as above) ----
+    def dit_side(M):
+        g = torch.Generator(device="cpu").manual_seed(M)
+        rows = torch.zeros(M, dtype=torch.int32)
+        rows[: M // 20] = 1                                      # engine/h3d/src/jobs.rs:213
+        f32 = lambda *sh, sc=1.0, base=0.0: (base + sc * torch.randn(*sh, generator=g)).float().to(dev_t)   # noqa: E731
+        side = {"rows": rows.to(dev_t), "w": f32(DH, sc=0.1, base=1.0), "scale": f32(2, DH, sc=0.1),
+                "shift": f32(2, DH, sc=0.1), "gate": f32(2, DH, sc=0.5), "qn": f32(DHD, sc=0.1, base=1.0),
+                "kn": f32(DHD, sc=0.1, base=1.0)}
+        # (cos, sin) of the three position axes per token, 21 frequencies each (dit.rs:188-203)
+        pos = torch.randint(0, 64, (M, 3), generator=g).float()
+        inv = torch.pow(torch.tensor(10000.0), -torch.arange(21).float() / 21.0)
+        ang = (pos[:, :, None] * inv[None, None, :]).reshape(M, 63)
+        side["cs126"] = torch.stack([torch.cos(ang), torch.sin(ang)], -1).contiguous().to(dev_t)
+        side["cs96"] = side["cs126"][:, :48].contiguous()
+        return {k: T(v) for k, v in side.items()}
+
+    def dit_hbm(M):
+        sd = dit_side(M)
+        mod = ops.Mod(sd["rows"], sd["scale"], sd["shift"])
+
+        def norm():
+            x, h = bf16(M, DH), torch.empty(M, DH, dtype=torch.bfloat16, device=dev_t)
+            X, H = T(x), T(h)
+            return lambda: ops.rms_norm_mod(X, sd["w"], 1e-5, mod, H)
+        run(f"dit_rms_norm_mod_{M}", norm)
+
+        def rope(part, w, rot, cs, both=False):
+            def make():
+                qkv = bf16(M, DQKV)
+                QKV = T(qkv)
+                r = [ops.Rows(QKV, i * DHEADS * DHD, DQKV, M, DHEADS, DHD) for i in range(2)]
+                if both:
+                    return lambda: ops.qk_rms_rope(r[0], r[1], sd["qn"], sd["kn"], 1e-5, cs, rot)
+                return lambda: ops.rms_rope(r[part], w, 1e-5, cs, rot)
+            return make
+        run(f"dit_rms_rope_q_rot126_{M}", rope(0, sd["qn"], 126, sd["cs126"]))
+        run(f"dit_rms_rope_k_rot126_{M}", rope(1, sd["kn"], 126, sd["cs126"]))
+        run(f"dit_rms_rope_q_rot96_{M}", rope(0, sd["qn"], 96, sd["cs96"]))
+        run(f"dit_qk_rms_rope_rot126_{M}", rope(0, None, 126, sd["cs126"], both=True))
+
+        def gate_add():
+            x, pr = bf16(M, DH), bf16(M, DH)
+            X, PR = T(x), T(pr)
+            return lambda: ops.gate_add(X, PR, sd["rows"], sd["gate"])
+        run(f"dit_gate_add_{M}", gate_add)
+
+        def swiglu():
+            f1, act = bf16(M, 2 * DFF), torch.empty(M, DFF, dtype=torch.bfloat16, device=dev_t)
+            F1, ACT = T(f1), T(act)
+            return lambda: ops.swiglu(F1, ACT)
+        run(f"dit_swiglu_{M}", swiglu)
+
+        def quantize(K):
+            def make():
+                x = bf16(M, K)
+                X, Q, S = T(x), T(torch.empty(M, K, dtype=torch.int8, device=dev_t)), T(torch.empty(M, device=dev_t))
+                return lambda: ops.int8_quantize(X, Q, S, 256)
+            return make
+        for name, K, _ in DIT_LINEARS:
+            if name != "fc1":                                    # fc1 quantizes the same h as qkv
+                run(f"dit_quantize_g256_{name}_{M}", quantize(K))
+
+        # the fused forms of the pairs dit.rs:340-341 and 363-364
+        def norm_quant():
+            x = bf16(M, DH)
+            X, Q, S = T(x), T(torch.empty(M, DH, dtype=torch.int8, device=dev_t)), T(torch.empty(M, device=dev_t))
+            tb = ops.Tables(scale=sd["scale"], shift=sd["shift"], rows=sd["rows"])
+            return lambda: ops.norm_quant(X, sd["w"], 1e-5, tb, Q, S, rot=A.ROT_REGULAR, group=256)
+        run(f"dit_norm_quant_g256_{M}", norm_quant)
+
+        def swiglu_quant():
+            f1 = bf16(M, 2 * DFF)
+            F1, Q, S = T(f1), T(torch.empty(M, DFF, dtype=torch.int8, device=dev_t)), T(torch.empty(M, device=dev_t))
+            return lambda: ops.swiglu_quant(F1, Q, S, rot=A.ROT_REGULAR, group=256)
+        run(f"dit_swiglu_quant_g256_{M}", swiglu_quant)
+
+    dit_hbm(M2)
+    dit_hbm(M4)
+
     # ---- the compute-bound kernels, last: config 5b's int8 GEMM, then attention ----
     run("cfg5b_int8_gemm_silu_47104x16384", lambda: (lambda: ops.int8_gemm_dequant(Q5, S5, layer, A.ACT_SILU, O5)), 5)
 
@@ -361,6 +496,32 @@ def main() -> int:
     run("attn_sage_47104x32x128", make_attn(M4), 3)
     # the 16-bit form, which the reference takes below 8192 tokens: 4096 tokens x 32 heads x 128
     run("attn_f16_4096x32x128", make_attn(4096), 20)
+
+    # ---- the DiT block's int8 linears (group 256, a scale per output) and its attention, 56 heads of 128 ----
+    def dit_compute(M):
+        gen = torch.Generator(device="cpu").manual_seed(M + 1)
+        for name, K, N in DIT_LINEARS:
+            key = f"dit_int8_linear_{name}_{M}"
+            if skip(key):
+                continue
+            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, generator=gen).to(dev_t)
+            ws = (0.005 + 0.015 * torch.rand(N, generator=gen)).float().to(dev_t)
+            lin = ops.Int8Linear(T(w), T(ws), group=256)
+            x, out = bf16(M, K), torch.empty(M, N, dtype=torch.bfloat16, device=dev_t)
+            X, O = T(x), T(out)
+            run(key, lambda: (lambda: lin.forward(X, O)), 5, ring=1)
+            del w, x, out, X, O, lin
+            torch.cuda.empty_cache()
+
+        def attn():
+            qkv, o = bf16(M, DQKV), torch.empty(M, DHEADS * DHD, dtype=torch.bfloat16, device=dev_t)
+            QKV, O = T(qkv), T(o)
+            rows = [ops.Rows(QKV, i * DHEADS * DHD, DQKV, M, DHEADS, DHD) for i in range(3)]
+            return lambda: ops.attention(*rows, O)
+        run(f"dit_attention_{M}", attn, 5 if M < 30000 else 2, ring=1)
+
+    dit_compute(M2)
+    dit_compute(M4)
 
     if args.copy_probe:
         def make_copy():
@@ -383,6 +544,16 @@ def main() -> int:
         if k.startswith("cfg5b"):
             tops = 2 * M4 * C * 16384 / (ms * 1e-3) / 1e12
             e.update({"TOPS_i8": round(tops, 1), "frac_i8_peak": round(tops / PEAK_I8_TOPS, 4)})
+        if k.startswith("dit_int8_linear"):
+            Mk = int(k.rsplit("_", 1)[1])
+            K_, N_ = next((K, N) for name, K, N in DIT_LINEARS if k.startswith(f"dit_int8_linear_{name}_"))
+            tops = 2 * Mk * K_ * N_ / (ms * 1e-3) / 1e12
+            e.update({"TOPS_i8": round(tops, 1), "frac_i8_peak": round(tops / PEAK_I8_TOPS, 4)})
+        if k.startswith("dit_attention"):
+            Mk = int(k.rsplit("_", 1)[1])
+            half_ops = 2.0 * Mk * Mk * DHEADS * DHD
+            t_peak = half_ops / (PEAK_I8_TOPS * 1e12) + half_ops / (PEAK_F16_TFLOPS * 1e12)
+            e.update({"TOPS": round(2 * half_ops / (ms * 1e-3) / 1e12, 1), "frac_mfma_peak": round(t_peak / (ms * 1e-3), 4)})
         if k.startswith("attn"):
             # the int8 form: q k^T on the i8 cores (5 POPS) and P v on the f16 cores (2.5 PFLOP/s); the 16-bit form:
             # both on the f16 cores. The time both take at peak.
@@ -414,8 +585,12 @@ def main() -> int:
                      "frac": round(value / PEAK_GBS, 4), "traffic": measured_traffic(HEADLINE)},
         "kernels": per,
         "device": dev.name(),
+        "library": os.path.relpath(A.load().path, ROOT),
         "cus": torch.cuda.get_device_properties(0).multi_processor_count,
     }
+    dit = dit_block_table(kernels)
+    if dit:
+        line["dit_block"] = dit
     if args.mark:
         line["marked"] = marked
     if not args.no_cpu:
@@ -425,6 +600,42 @@ def main() -> int:
                                                           "q5": q5, "s5": s5, "w5": w5, "ws5": ws5})
     print(json.dumps(line), flush=True)
     return 0
+
+
+def dit_block_table(kernels: dict) -> dict:
+    """The DiT block's time per stage under the labels of the reference's harness (engine/h3d/src/jobs.rs:269-279),
+    each stage the sum of its calls' times (the norm and the gated add run twice a block), beside the engine's
+    published times per block (docs/PORT-PLAN.md:62-70, on its own GPU); and the three fused pairs against the two
+    calls each replaces."""
+    out = {}
+    for M in (M2, M4):
+        st = {}
+        for label, keys in DIT_STAGES:
+            ks = [f"{k}_{M}" for k in keys]
+            if all(k in kernels for k in ks):
+                st[label] = round(sum(kernels[k] for k in ks), 4)
+        if not st:
+            continue
+        e = {"stages_ms": st, "ms_per_block": round(sum(st.values()), 3) if len(st) == len(DIT_STAGES) else None}
+        pairs = {
+            "rms_norm_mod + int8_linear's quantizer (dit.rs:340-341) -> h3s_norm_quant":
+                (("dit_rms_norm_mod", "dit_quantize_g256_qkv"), "dit_norm_quant_g256"),
+            "swiglu + fc2's quantizer (dit.rs:363-364) -> h3s_swiglu_quant":
+                (("dit_swiglu", "dit_quantize_g256_fc2"), "dit_swiglu_quant_g256"),
+            "rms_rope of q + of k (dit.rs:347-348) -> h3s_qk_rms_rope": (("dit_rms_rope_q_rot126", "dit_rms_rope_k_rot126"),
+                                                                         "dit_qk_rms_rope_rot126"),
+        }
+        fused = {}
+        for label, (two, one) in pairs.items():
+            ks, k1 = [f"{k}_{M}" for k in two], f"{one}_{M}"
+            if all(k in kernels for k in ks) and k1 in kernels:
+                fused[label] = {"two_calls_ms": round(sum(kernels[k] for k in ks), 4), "fused_ms": round(kernels[k1], 4)}
+        if fused:
+            e["fused_pairs"] = fused
+        out[str(M)] = e
+    if out:
+        out["published_engine_ms_per_block"] = DIT_PUBLISHED_MS
+    return out
 
 
 def cpu_baseline(x2, r2, tab, t):

@@ -284,38 +284,27 @@ int h3o_layer_norm(const void* x, int x_dt, int64_t M, int64_t C, const float* w
 }
 
 /* ---- rms_rope: kernels/h3sycl.cpp:1276-1376 ----
- * Canonical per-head order. With V the elements of a 16-byte vector and half = rot_dim / 2, a head's features are
- * dealt to "slots": rotated slot p takes the pairs j in [pV, min(pV + V, half)) - its first features j, then their
- * partners half + j - and pass-through slot q the features [rot + qV, min(rot + qV + V, D)). So there are
- * ceil(half / V) rotated slots and ceil((D - rot) / V) pass-through ones; when half and D - rot are whole vectors,
- * a slot is one 16-byte chunk (a rotated slot the pair of chunks p, p + half / V). Slot s accumulates its squares
- * in that order; the P slot partials, padded with zeros to a power of two, are combined by the xor butterfly. */
+ * Canonical per-head order: the head's D features are D / V 16-byte chunks (V the elements of a vector), chunk l
+ * summed in order into partial l, the partials padded with zeros to CL = pow2ceil(D / V) and combined by the xor
+ * butterfly: h3o_canon_sum over CL lanes. Then each pair (j, half + j), half = rot_dim / 2, rotates by the token's
+ * (cos, sin) of j (h3sycl.cpp:1325-1331), and the features from rot_dim on are only normalized (h3sycl.cpp:1345). */
 static int pow2ceil(int n) { int p = 1; while (p < n) p *= 2; return p; }
 typedef struct {
     void* x; int x_dt; int64_t H, D, stride; const float* w; float eps; const float* cs; int rot;
 } rope_ctx;
 static void rope_rows(void* p, int64_t r0, int64_t r1) {
     const rope_ctx* c = (const rope_ctx*) p;
-    const int64_t D = c->D, half = c->rot / 2, npf = D - c->rot;
+    const int64_t D = c->D, half = c->rot / 2;
     const int V = vec_of(c->x_dt);
-    const int nrot = (int) ((half + V - 1) / V), npass = (int) ((npf + V - 1) / V), P = nrot + npass, P2 = pow2ceil(P);
+    /* the head's sum of squares: the canonical sum over pow2ceil(D / V) lanes, one 16-byte chunk of the head a lane
+     * (the reference's order, a sequential s += v * v, h3sycl.cpp:1296-1300, is left to its device: not restated) */
+    const int CL = pow2ceil((int) (D / V));
     float* v = (float*) malloc((size_t) D * sizeof(float));
     for (int64_t m = r0; m < r1; ++m)
         for (int64_t h = 0; h < c->H; ++h) {
             const int64_t base = m * c->stride + h * D;
             for (int64_t i = 0; i < D; ++i) v[i] = h3o_load(c->x, c->x_dt, base + i);
-            float part[64];
-            for (int s = 0; s < P2; ++s) part[s] = 0.0f;
-            for (int s = 0; s < nrot; ++s) {
-                const int64_t j0 = (int64_t) s * V, j1 = j0 + V < half ? j0 + V : half;
-                for (int64_t j = j0; j < j1; ++j) part[s] = fmaf(v[j], v[j], part[s]);
-                for (int64_t j = j0; j < j1; ++j) part[s] = fmaf(v[half + j], v[half + j], part[s]);
-            }
-            for (int q = 0; q < npass; ++q) {
-                const int64_t i0 = c->rot + (int64_t) q * V, i1 = i0 + V < D ? i0 + V : D;
-                for (int64_t i = i0; i < i1; ++i) part[nrot + q] = fmaf(v[i], v[i], part[nrot + q]);
-            }
-            const float inv = inv_root(butterfly(part, P2), D, c->eps);
+            const float inv = inv_root(h3o_canon_sum(v, D, V, CL, H3O_SUMSQ, 0.0f), D, c->eps);
             for (int64_t j = 0; j < half; ++j) {
                 const float a = v[j] * inv * c->w[j], b = v[half + j] * inv * c->w[half + j];
                 const int64_t t = m * half + j;
@@ -335,8 +324,7 @@ int h3o_rms_rope(void* x, int x_dt, int64_t M, int64_t H, int64_t D, int64_t str
     if (stride < H * D) return fail("rms_rope: the row stride is shorter than a row");
     if (!dt_ok(x_dt)) return fail("rms_rope: unknown element type");
     const int V = vec_of(x_dt);
-    if (pow2ceil((int) ((rot_dim / 2 + V - 1) / V + (D - rot_dim + V - 1) / V)) > 64)
-        return fail("rms_rope: a head of more than 64 slots");
+    if (D % V != 0 || D / V > 64) return fail("rms_rope: a head of whole 16-byte vectors, at most 64 of them");
     rope_ctx c = {x, x_dt, H, D, stride, weight, eps, cs, rot_dim};
     parallel_rows(M, rope_rows, &c);
     return 0;

@@ -388,3 +388,16 @@ def int8_gemm_dequant(q: Tensor, s: Tensor, layer: Int8Linear, act: int, out: Te
             layer.scale.ptr(), ns, bias, act, out.ptr(), out.dtype.kernel_code(),)
     dev = _dev(q)
     dev.check(dev.api.int8_gemm_dequant(dev.ctx, *args))
+
+
+def int8_quantize(x: Tensor, q: Tensor, s: Tensor, group: int = 0) -> None:
+    """The int8 linear's first pass on its own: x [M, K] rotated per `group` features by the regular Hadamard (0:
+    none), then per-row codes q int8 [M, K] and scales s float32 [M] (the quantizer of ops.rs:46-83's call)."""
+    if not x.shape:
+        raise Error("int8_quantize: x has no shape")
+    k = x.shape[-1]
+    m = x.elements() // max(k, 1)
+    if q.dtype != DType.I8 or q.elements() != m * k or s.dtype != DType.F32 or s.elements() != m:
+        raise Error(f"int8_quantize: q {q.dtype} {q.shape} / s {s.dtype} {s.shape} for x {x.shape}")
+    dev = _dev(x)
+    dev.check(dev.api.int8_quantize(dev.ctx, x.ptr(), x.dtype.kernel_code(), m, k, group, q.ptr(), s.ptr()))

@@ -629,6 +629,34 @@ def test_layer_norm_chain_is_a_composition(oracle, affine):
     assert not np.array_equal(bad, want.ravel())
 
 
+def test_rms_rope_norm_is_the_canonical_head_sum(oracle):
+    """A head's norm is the canonical sum over pow2ceil(D / V) lanes, one 16-byte chunk a lane. With rot_dim 0 and a
+    unit weight, feature 0 = 1 reads inv off the output. Planted (float32, V = 4, D = 128: 32 lanes): 1, 2^24, 1 in
+    chunks 0, 1, 2. The butterfly adds chunks 0 and 2 first (2), then 2^24 + 2 exactly; a sequential sum loses both
+    ones to ties (2^24 + 1 rounds to 2^24)."""
+    D = 128
+    inv = lambda s, n=D: np.float32(1.0) / np.sqrt(np.float32(np.float32(s) / np.float32(n)) + np.float32(1e-5))   # noqa: E731
+    x = np.zeros(D, dtype=np.float32)
+    x[0], x[4], x[8] = 1.0, 4096.0, 1.0
+    w = np.ones(D, dtype=np.float32)
+    y = oracle.rms_rope(x, oracle.F32, 1, 1, D, D, w, 1e-5, None, 0)
+    assert oracle.canon_sum(x, 4, 32, oracle.SUMSQ) == 2.0 ** 24 + 2
+    seq = np.float32(0.0)
+    for v in x:
+        seq = np.float32(seq + np.float32(v * v))
+    assert seq == 2.0 ** 24
+    assert y[0] == inv(2.0 ** 24 + 2) and y[0] != inv(seq)
+    # random heads: float32 of 128 (32 lanes) and bfloat16 of 80 features (10 chunks of 8, padded to 16 lanes)
+    xr = np.random.default_rng(3).standard_normal(D).astype(np.float32) * 3
+    xr[0] = 1.0
+    assert oracle.rms_rope(xr, oracle.F32, 1, 1, D, D, w, 1e-5, None, 0)[0] == inv(oracle.canon_sum(xr, 4, 32, oracle.SUMSQ))
+    xb = oracle.to_bf16(np.random.default_rng(4).standard_normal(80).astype(np.float32) * 3)
+    yb = oracle.rms_rope(xb, oracle.BF16, 1, 1, 80, 80, np.ones(80, np.float32), 1e-5, None, 0)
+    xf = oracle.from_bf16(xb)
+    inv_b = inv(oracle.canon_sum(xf, 8, 16, oracle.SUMSQ), 80)
+    assert np.array_equal(yb, oracle.to_bf16((xf * inv_b).astype(np.float32)))
+
+
 # ---- rotary with partial slots: rot_dim / 2 or D - rot_dim not a whole 16-byte vector ----
 @pytest.mark.parametrize("dt", [o.F32, o.BF16])
 @pytest.mark.parametrize("D,rot", [(128, 126), (128, 120), (128, 60), (128, 2), (64, 48), (128, 128)])
