@@ -374,9 +374,10 @@ int h3o_gate_add(void* x, int x_dt, int64_t M, int64_t C, const void* other, int
  * it: its work-item holds 16 consecutive features, so the digits of stride 1 and 4 are summed in registers left to
  * right, t = ((x0 + x1) + x2) + x3 (h3sycl.cpp:440), and the digits of stride 16 and 64 across the lanes, pairwise,
  * t = (x0 + x1) + (x2 + x3) (h3sycl.cpp:452-453). Then * 1/sqrt(g), a power of two (h3sycl.cpp:456). The smaller
- * groups (4, 16, 64) take the same rule by stride. The digit of stride 1 forms t - 2 x with one rounding,
- * fmaf(-2, x, t), as the GPU does: 2 x is exact for |x| < 2^127, so it is the value of the reference's t - 2.0f * x
- * (h3sycl.cpp:441); the two differ only where 2 x overflows.
+ * groups (4, 16, 64) take the same rule by stride. Every digit forms t - 2 x with one rounding, fmaf(-2, x, t): the
+ * reference's t - 2.0f * x (h3sycl.cpp:441, 454), which icpx -O3 contracts into that fma under its default
+ * floating-point model (container/build-inside.sh:12); 2 x is exact for |x| < 2^127, so the two agree unless 2 x
+ * overflows.
  * Sylvester: h = 1, 2, ..., g/2, (a, b) -> (a + b, a - b); then * fl(1/sqrt(g)). */
 void h3o_rotate_group(float* y, int g, int kind) {
     if (kind == H3O_ROT_REGULAR) {
@@ -385,17 +386,10 @@ void h3o_rotate_group(float* y, int g, int kind) {
                 if ((i / d) % 4 != 0) continue;
                 const float x0 = y[i], x1 = y[i + d], x2 = y[i + 2 * d], x3 = y[i + 3 * d];
                 const float t = d < 16 ? ((x0 + x1) + x2) + x3 : (x0 + x1) + (x2 + x3);
-                if (d == 1) {
-                    y[i] = fmaf(-2.0f, x3, t);
-                    y[i + d] = fmaf(-2.0f, x2, t);
-                    y[i + 2 * d] = fmaf(-2.0f, x1, t);
-                    y[i + 3 * d] = fmaf(-2.0f, x0, t);
-                } else {
-                    y[i] = t - 2.0f * x3;
-                    y[i + d] = t - 2.0f * x2;
-                    y[i + 2 * d] = t - 2.0f * x1;
-                    y[i + 3 * d] = t - 2.0f * x0;
-                }
+                y[i] = fmaf(-2.0f, x3, t);
+                y[i + d] = fmaf(-2.0f, x2, t);
+                y[i + 2 * d] = fmaf(-2.0f, x1, t);
+                y[i + 3 * d] = fmaf(-2.0f, x0, t);
             }
     } else if (kind == H3O_ROT_SYLVESTER) {
         for (int h = 1; h < g; h *= 2)

@@ -115,8 +115,12 @@ void release_blas(Ctx* c);
 // device must be current. 0, or -1 when the lookup failed (the entry point then reports why).
 int noalloc_setup(int device);
 
-// the quantizer of h3s_int8_linear (rownorm.hip): x [M, K] -> regular rotation per group (0: none) -> q, s
+// the quantizer of h3s_int8_linear (quant.hip): x [M, K] -> regular rotation per group (0: none) -> q, s
 int launch_quantize(Ctx* c, const void* x, int x_dt, int64_t M, int64_t K, int group, int8_t* q, float* s);
+// h3s_rms_norm_mod on the quantizer's one-wavefront-a-row layout (quant.hip), for the shapes it takes: 0 or -1 when
+// it ran, 1 when the shape is not one of them (the row chain kernel then runs it)
+int launch_norm_out(Ctx* c, const char* fn, const void* x, int x_dt, int64_t M, int64_t C, const float* w, float eps,
+                    const int32_t* rows, const float* scale, const float* shift, void* out, int out_dt);
 
 inline bool aligned16(const void* p) { return ((uintptr_t) p & 15) == 0; }
 inline int elem_size(int dt) { return dt == H3S_F32 ? 4 : 2; }

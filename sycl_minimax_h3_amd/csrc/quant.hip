@@ -39,6 +39,18 @@ int launch_quantize(Ctx* c, const void* x, int x_dt, int64_t M, int64_t K, int g
     return dispatch(c, fn, x_dt, A, QUANT_RAW, p);
 }
 
+// h3s_rms_norm_mod on the one-wavefront-a-row layout, for the shapes it takes (bfloat16 rows and out of the model's
+// hidden width, a weight, float32 tables or none): 0 or -1 when it ran, 1 when the shape is not one it takes.
+int launch_norm_out(Ctx* c, const char* fn, const void* x, int x_dt, int64_t M, int64_t C, const float* w, float eps,
+                    const int32_t* rows, const float* scale, const float* shift, void* out, int out_dt) {
+    if (x_dt != H3S_BF16 || out_dt != H3S_BF16 || !w || M < c->quant_wave_min) return 1;
+    QuantArgs A{x, M, C, w, eps, rows, scale, shift, H3S_F32, H3S_BF16, H3S_ROT_NONE, 0, 1.0f, nullptr, nullptr};
+    A.h = out;
+    const int f = ROW_W | (scale ? ROW_TAB | ROW_TAB32 : 0) | ROW_OUTH;
+    if (!quant_wave_model_takes(A, f)) return 1;
+    return quant_launch<H3S_BF16>(c, fn, A, QUANT_NORM_OUT, row_plan(C / 8));
+}
+
 }  // namespace h3
 
 using namespace h3;

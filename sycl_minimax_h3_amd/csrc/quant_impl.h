@@ -150,8 +150,8 @@ template <int V, bool SW = false> __device__ __forceinline__ void sylvester(floa
 template <int CTRL> __device__ __forceinline__ float quad(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
-// the digit of stride 1, inside a chunk; t - 2 x as one fma (2 x is exact below 2^127, so this is the value of
-// t - 2.0f * x; the digits across lanes keep the two instructions, whose partner values come through DPP)
+// the digit of stride 1, inside a chunk. Every digit forms t - 2 x as one fma, the oracle's (2 x is exact below
+// 2^127, so it is the value of t - 2.0f * x)
 template <int V> __device__ __forceinline__ void reg_in(float (&v)[V]) {
 #pragma unroll
     for (int e = 0; e < V; e += 4) {
@@ -170,8 +170,8 @@ __device__ __forceinline__ void reg_pair(float (&v)[8]) {
     for (int r = 0; r < 4; ++r) {
         const float lo = v[r], hi = v[r + 4];
         const float t = (quad<0xA0>(lo + hi) + quad<0xF5>(lo)) + quad<0xF5>(hi);
-        v[r] = t - 2.0f * quad<0xB1>(hi);
-        v[r + 4] = t - 2.0f * quad<0xB1>(lo);
+        v[r] = __builtin_fmaf(-2.0f, quad<0xB1>(hi), t);
+        v[r + 4] = __builtin_fmaf(-2.0f, quad<0xB1>(lo), t);
     }
 }
 // the digit of stride 4 with V = 4: x0..x3 in the four lanes of a quad, taken in order (quad_perm [a,a,a,a]); the
@@ -180,7 +180,7 @@ __device__ __forceinline__ void reg_quad(float (&v)[4]) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const float t = ((quad<0x00>(v[e]) + quad<0x55>(v[e])) + quad<0xAA>(v[e])) + quad<0xFF>(v[e]);
-        v[e] = t - 2.0f * quad<0x1B>(v[e]);
+        v[e] = __builtin_fmaf(-2.0f, quad<0x1B>(v[e]), t);
     }
 }
 // the digit whose four values sit in lanes S apart (a = (lane / S) % 4): the own pair x_a + x_(a^1), the other pair
@@ -190,7 +190,7 @@ template <int V, int S> __device__ __forceinline__ void reg_x(float (&v)[V]) {
     for (int e = 0; e < V; ++e) {
         const float pv = v[e] + lane_xor<S>(v[e]);
         const float t = pv + lane_xor<2 * S>(pv);
-        v[e] = t - 2.0f * lane_xor<3 * S>(v[e]);
+        v[e] = __builtin_fmaf(-2.0f, lane_xor<3 * S>(v[e]), t);
     }
 }
 template <int V> __device__ __forceinline__ void regular(float (&v)[V], int G) {
@@ -205,6 +205,75 @@ template <int V> __device__ __forceinline__ void regular(float (&v)[V], int G) {
         if (G > 64) reg_x<4, 16>(v);
     }
 }
+
+// ---- the regular rotation of a group of 256 with a lane's 16 consecutive features in registers: the reference's
+// work-item (kernels/h3sycl.cpp:408-456). The group's 16 lanes of a 16-lane DPP row hold its 16 runs of 16 features,
+// run P = swap3(lane) & 15 in lane `lane` (a = features 0-7, b = 8-15). The digits of stride 1 and 4 are inside
+// the lane, summed left to right; the digit of stride 16 pairs runs P ^ 1, P ^ 2, P ^ 3 = lanes ^ 1, ^ 2, ^ 3 (quad
+// permutes); the digit of stride 64 runs P ^ 4, P ^ 8, P ^ 12 = lanes ^ 7, ^ 8, ^ 15 (swap3 turns position bit 2
+// into lane xor 7: the half-row mirror, the row rotate by 8 and the row mirror), summed pairwise. Every partner
+// value comes through the DPP operand of the add or fma that uses it: three instructions a value a digit, no LDS.
+// pv = x + x[C1]; t = pv + pv[C2]; x = t - 2 x[C3] (one fma) for 8 values; s_nop 1: the two wait states a DPP read
+// needs after the VALU write of its register
+#define H3_DPP_ADD8(OUT, IN, CTRL)                                                                            \
+    asm volatile("s_nop 1\n"                                                                                  \
+                 "v_add_f32_dpp %0, %8, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"                             \
+                 "v_add_f32_dpp %1, %9, %9 " CTRL " row_mask:0xf bank_mask:0xf\n"                             \
+                 "v_add_f32_dpp %2, %10, %10 " CTRL " row_mask:0xf bank_mask:0xf\n"                           \
+                 "v_add_f32_dpp %3, %11, %11 " CTRL " row_mask:0xf bank_mask:0xf\n"                           \
+                 "v_add_f32_dpp %4, %12, %12 " CTRL " row_mask:0xf bank_mask:0xf\n"                           \
+                 "v_add_f32_dpp %5, %13, %13 " CTRL " row_mask:0xf bank_mask:0xf\n"                           \
+                 "v_add_f32_dpp %6, %14, %14 " CTRL " row_mask:0xf bank_mask:0xf\n"                           \
+                 "v_add_f32_dpp %7, %15, %15 " CTRL " row_mask:0xf bank_mask:0xf"                              \
+                 : "=&v"(OUT[0]), "=&v"(OUT[1]), "=&v"(OUT[2]), "=&v"(OUT[3]), "=&v"(OUT[4]), "=&v"(OUT[5]),     \
+                   "=&v"(OUT[6]), "=&v"(OUT[7])                                                               \
+                 : "v"(IN[0]), "v"(IN[1]), "v"(IN[2]), "v"(IN[3]), "v"(IN[4]), "v"(IN[5]), "v"(IN[6]), "v"(IN[7]))
+#define H3_DPP_FMAC8(ACC, IN, M2, CTRL)                                                                        \
+    asm volatile("s_nop 1\n"                                                                                  \
+                 "v_fmac_f32_dpp %0, %8, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                           \
+                 "v_fmac_f32_dpp %1, %9, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                           \
+                 "v_fmac_f32_dpp %2, %10, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                          \
+                 "v_fmac_f32_dpp %3, %11, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                          \
+                 "v_fmac_f32_dpp %4, %12, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                          \
+                 "v_fmac_f32_dpp %5, %13, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                          \
+                 "v_fmac_f32_dpp %6, %14, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                          \
+                 "v_fmac_f32_dpp %7, %15, %16 " CTRL " row_mask:0xf bank_mask:0xf"                             \
+                 : "+v"(ACC[0]), "+v"(ACC[1]), "+v"(ACC[2]), "+v"(ACC[3]), "+v"(ACC[4]), "+v"(ACC[5]),         \
+                   "+v"(ACC[6]), "+v"(ACC[7])                                                                 \
+                 : "v"(IN[0]), "v"(IN[1]), "v"(IN[2]), "v"(IN[3]), "v"(IN[4]), "v"(IN[5]), "v"(IN[6]), "v"(IN[7]), \
+                   "v"(M2))
+// one cross-lane digit on 8 values x (in place)
+#define H3_DIGIT8(X, C1, C2, C3)                                                                               \
+    {                                                                                                          \
+        float pv_[8], t_[8];                                                                                   \
+        H3_DPP_ADD8(pv_, X, C1);                                                                               \
+        H3_DPP_ADD8(t_, pv_, C2);                                                                              \
+        H3_DPP_FMAC8(t_, X, m2, C3);                                                                           \
+        _Pragma("unroll") for (int e_ = 0; e_ < 8; ++e_) X[e_] = t_[e_];                                       \
+    }
+__device__ __forceinline__ void regular256_pair(float (&a)[8], float (&b)[8]) {
+    // stride 1: inside each chunk's two quads
+    reg_in<8>(a);
+    reg_in<8>(b);
+    // stride 4: a[i], a[i + 4], b[i], b[i + 4]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float x0 = a[i], x1 = a[i + 4], x2 = b[i], x3 = b[i + 4];
+        const float t = ((x0 + x1) + x2) + x3;
+        a[i] = __builtin_fmaf(-2.0f, x3, t); a[i + 4] = __builtin_fmaf(-2.0f, x2, t);
+        b[i] = __builtin_fmaf(-2.0f, x1, t); b[i + 4] = __builtin_fmaf(-2.0f, x0, t);
+    }
+    const float m2 = -2.0f;
+    // stride 16: lanes ^ 1, ^ 2, ^ 3
+    H3_DIGIT8(a, "quad_perm:[1,0,3,2]", "quad_perm:[2,3,0,1]", "quad_perm:[3,2,1,0]")
+    H3_DIGIT8(b, "quad_perm:[1,0,3,2]", "quad_perm:[2,3,0,1]", "quad_perm:[3,2,1,0]")
+    // stride 64: lanes ^ 7, ^ 8, ^ 15
+    H3_DIGIT8(a, "row_half_mirror", "row_ror:8", "row_mirror")
+    H3_DIGIT8(b, "row_half_mirror", "row_ror:8", "row_mirror")
+}
+#undef H3_DIGIT8
+#undef H3_DPP_FMAC8
+#undef H3_DPP_ADD8
 
 // A kernel's ROT template value: the rotation kind (H3S_ROT_NONE, H3S_ROT_REGULAR or H3S_ROT_SYLVESTER) in the low
 // four bits, and above them a group size fixed at compile time (0: the group size of the call). A fixed group turns
@@ -229,6 +298,7 @@ struct QuantArgs {
     float cg;                // fl(1 / sqrt(group))
     int8_t* q;
     float* s;
+    void* h = nullptr;       // ROW_OUTH: the bfloat16 rows h [M, C] (then q and s are unused)
 };
 
 // ROT: the rotation kind (group size at run time); F: the side inputs (ROW_W, ROW_TAB, ROW_TAB32 or ROW_DYN, as in
@@ -433,18 +503,28 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
     }
 }
 
-// ---- one wavefront a row, for rows of exactly 64 CPL 16-byte chunks of a 16-bit type (2048 or 4096 features) ----
+// ---- one or more wavefronts a row, for rows of a 16-bit type whose chunk count the kernel fixes ----
 // The same arithmetic as quant_kernel, laid out so that the row's scalar work is done once: quant_kernel spreads
-// such a row over four wavefronts, each of which repeats the row's statistics (the butterflies, the LDS combine
-// and its barrier, the divisions and the square root). Here lane t of the wavefront holds chunks t + 64 j
-// (j < CPL), every one inside the row, and the row statistics keep the order of the 256-lane layout that the oracle restates: chunk slot j
-// belongs to canonical wavefront j % 4 (chunk t + 64 j is canonical lane (t + 64 j) % 256), so a lane keeps four
-// partial sums, each summed over the wavefront by the butterfly and then combined as (w0 + w2) + (w1 + w3).
+// a row of 256 or more chunks over four or eight wavefronts, each of which repeats the row's statistics (the
+// butterflies, the LDS combine and its barrier, the divisions and the square root). Here lane t of wavefront s of
+// the row's WPR holds chunks t + 64 (WPR j + s) (j < CPL); in the row's last slots only the lanes whose chunk is
+// below the row's NCH chunks hold one (5376 features, one wavefront a row: 10 whole slots and half of an eleventh),
+// the others load a copy of the row's last chunk and never use it. A rotation group is whole inside the valid lanes
+// (a group size divides C and 64 V), so it never mixes a copy with a chunk.
 //
-// Rows are dealt out grid-stride by wavefront: wavefront w of block b takes rows g, g + U, g + 2U, ... with
-// g = b NW + w and U = NW x the blocks, so the rows in flight across the device form one contiguous window (a
-// contiguous run per wavefront streams measurably slower), and at step k the block's wavefronts hold the
-// neighbouring rows b NW + k U + [0, NW). The next row's x is in registers while a row is computed.
+// Norm: the row statistics keep the order of the 256-lane layout that the oracle restates: chunk slot j belongs to
+// canonical wavefront j % 4 (chunk t + 64 j is canonical lane (t + 64 j) % 256), so a lane keeps four partial sums,
+// each summed over the wavefront by the butterfly and then combined as (w0 + w2) + (w1 + w3); with two wavefronts a
+// row each forms its own two (w0 + w2, w1 + w3) and they meet in LDS. With ROW_OUTH the kernel is h3s_rms_norm_mod:
+// it stores the bfloat16 row h itself and computes no codes.
+//
+// Several wavefronts a row: each wavefront's maximum goes to LDS, and after one barrier every wavefront of the row
+// takes the maximum of the row's. The block's side values (below) hold the table row of its first row; a row of
+// another table row reads its table values from memory.
+//
+// Rows are dealt out by wavefront (group): group w of block b takes row g = b R + w (R rows a block step) with ONE,
+// else rows g, g + U, g + 2U, ... (U = R x the blocks: the rows in flight across the device form one contiguous
+// window; a contiguous run per wavefront streams measurably slower).
 //
 // The side inputs every wavefront of the block shares live in LDS, laid out [j][half][lane][4 floats] so that a
 // wavefront's 16-byte reads are consecutive: the weight, and one decoded table row (1 + scale and shift), the
@@ -452,83 +532,108 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
 // but those a segment boundary of rows[] cuts) is one round. Otherwise the block takes one round per distinct table
 // row of the step, in the order of its rows: between two barriers it re-decodes the cached row when the round's
 // differs, and the wavefronts whose rows use it run them (every wavefront takes the same rounds and barriers).
-template <int CPL> constexpr size_t quant_wave_side_bytes(int f) {
-    return (size_t) ((f & ROW_W) ? 1 : 0) * CPL * 2048 + (size_t) ((f & ROW_TAB) ? 2 : 0) * CPL * 2048;
+template <int CPL, int WPR = 1> constexpr size_t quant_wave_side_bytes(int f) {
+    return ((size_t) ((f & ROW_W) ? 1 : 0) + (size_t) ((f & ROW_TAB) ? 2 : 0)) * WPR * CPL * 2048;
 }
-// wavefronts a block: 8 with tables (one LDS copy of the side values serves more rows), else 4
-constexpr int quant_wave_nw(int f) { return (f & ROW_TAB) ? 8 : 4; }
-// ONE: the grid has a wavefront for every row, so each takes one row (108 registers for config 4's kernel, four
-// wavefronts a SIMD); else the grid strides over the rows, with nothing prefetched either: four wavefronts a SIMD
-// hide the loads (the registers of a prefetched next row would leave room for three). With tables and no rotation
-// the kernel is held to four wavefronts a SIMD (120 registers, no spills).
-template <int XDT, int CPL, int ROT, int F, bool ONE>
+// wavefronts a block: 8 with tables (one LDS copy of the side values serves more rows) or two or four a row, a row's
+// own with more, else 4
+constexpr int quant_wave_nw(int f, int wpr) { return wpr > 4 ? wpr : (f & ROW_TAB) || wpr > 1 ? 8 : 4; }
+// ONE: the grid has a wavefront (group) for every row, so each takes one row (108 registers for config 4's kernel,
+// four wavefronts a SIMD); else the grid strides over the rows, with nothing prefetched either: four wavefronts a
+// SIMD hide the loads (the registers of a prefetched next row would leave room for three). With tables and no
+// rotation (and at most 8 slots) the kernel is held to four wavefronts a SIMD (120 registers, no spills).
+template <int XDT, int CPL, int ROT, int F, bool ONE, int NCH, int WPR = 1, bool PAIR = false>
 __global__ __launch_bounds__(512)
-__attribute__((amdgpu_waves_per_eu((F & ROW_TAB) && rot_kind(ROT) == H3S_ROT_NONE ? 4 : 1)))
+__attribute__((amdgpu_waves_per_eu((F & ROW_TAB) && rot_kind(ROT) == H3S_ROT_NONE && CPL <= 8 ? 4 : 1)))
 void quant_wave_kernel(QuantArgs A) {
-    static_assert(XDT != H3S_F32 && !(F & (ROW_DYN | ROW_SWIGLU)), "quant_wave_kernel: 16-bit x, exact side inputs");
+    static_assert(XDT != H3S_F32 && !(F & ROW_DYN), "quant_wave_kernel: 16-bit x, exact side inputs");
+    static_assert(PAIR ? NCH > 128 * WPR * (CPL / 2 - 1) && NCH <= 128 * WPR * (CPL / 2)
+                       : NCH > 64 * WPR * (CPL - 1) && NCH <= 64 * WPR * CPL, "quant_wave_kernel: NCH reaches the last slots");
+    static_assert(WPR == 1 || (ONE && ((F & (ROW_RAW | ROW_SWIGLU)) || WPR == 2)),
+                  "quant_wave_kernel: several wavefronts a row: the quantizer on x or swiglu(x), or the norm, two a row");
+    static_assert(!PAIR || (ROT == rot_with(H3S_ROT_REGULAR, 256) && CPL % 2 == 0), "quant_wave_kernel: pairs for regular 256");
     constexpr int V = 8;
     constexpr bool ROTATED = rot_kind(ROT) != H3S_ROT_NONE;
-    constexpr bool NORM = !(F & ROW_RAW);
+    constexpr bool SWI = F & ROW_SWIGLU;
+    constexpr bool NORM = !(F & (ROW_RAW | ROW_SWIGLU));
+    constexpr bool OUTH = NORM && (F & ROW_OUTH);
     constexpr bool HASW = F & ROW_W;
     constexpr bool TAB = F & ROW_TAB;
     constexpr int TDT = (F & ROW_TAB32) ? H3S_F32 : H3S_BF16;
-    constexpr int WOFF = 0, SOFF = HASW ? CPL * 512 : 0, HOFF = SOFF + CPL * 512;     // float offsets in side
+    constexpr int WOFF = 0, SOFF = HASW ? WPR * CPL * 512 : 0, HOFF = SOFF + WPR * CPL * 512;   // float offsets in side
+    constexpr int NW = quant_wave_nw(F, WPR), RPB = NW / WPR;
+    // NCH chunks a row; PAIR: slot pair p of wavefront s holds run pair k = WPR p + s (chunks 128 k + [0, 128))
+    static_assert(!NORM || (NCH >= 256 && NCH <= 1024), "quant_wave_kernel: the norm's canonical order of 256 lanes");
     extern __shared__ __align__(16) float side[];
-    constexpr int NW = quant_wave_nw(F);
+    __shared__ float wmax[NW];
+    __shared__ float wsum[NW][2];
     const int lane = (int) (threadIdx.x & 63);
     const int wave = (int) wave_uniform(threadIdx.x >> 6);
-    const int64_t C = 64 * CPL * V;                         // the launch checks A.C against this
-    const int64_t b0 = (int64_t) blockIdx.x * NW, U = (int64_t) gridDim.x * NW, M = A.M;
+    const int ws = wave % WPR, wr = wave / WPR;             // this wavefront's share of its row, and the row's group
+    const int64_t C = (int64_t) NCH * V;                     // the launch checks A.C against this
+    const int64_t b0 = (int64_t) blockIdx.x * RPB, U = (int64_t) gridDim.x * RPB, M = A.M;
     if (b0 >= M) return;                                    // the whole block
-    // chunk slot j: chunk 64 j + pos, pos = the lane (swap3 of the lane for the Sylvester rotation, whose stage 4
-    // chunks apart then pairs lanes 7 apart: one DPP operand instead of two)
-    constexpr bool SW = rot_kind(ROT) == H3S_ROT_SYLVESTER;
+    // chunk slot j: chunk 64 (WPR j + ws) + pos, pos = the lane (swap3 of the lane for the Sylvester rotation, whose
+    // stage 4 chunks apart then pairs lanes 7 apart: one DPP operand instead of two; and for pairs, whose digit of
+    // stride 64 features then pairs lanes 7, 8 and 15 apart)
+    constexpr bool SW = rot_kind(ROT) == H3S_ROT_SYLVESTER || PAIR;
     const int pos = SW ? swap3(lane) : lane;
-    int cc[CPL];
+    // slot j of the row's wavefront s: its chunk, and whether it is inside the row (the row's last slots may be
+    // partial or empty); chunk_of gives the row's last chunk for a lane past the row
+    auto raw_chunk = [&](int s_, int j) {
+        return PAIR ? 128 * (WPR * (j / 2) + s_) + 2 * pos + (j & 1) : pos + 64 * (WPR * j + s_);
+    };
+    auto valid_of = [&](int s_, int j) {
+        // whole slots are decided at compile time; only the row's last ones test the lane
+        if (PAIR ? 128 * (WPR * (j / 2) + WPR) <= NCH : 64 * (WPR * j + WPR) <= NCH) return true;
+        return raw_chunk(s_, j) < NCH;
+    };
+    auto chunk_of = [&](int s_, int j) { return valid_of(s_, j) ? raw_chunk(s_, j) : NCH - 1; };
+    auto valid = [&](int j) { return valid_of(ws, j); };
+    int cc[CPL];                                            // the chunks this wavefront loads
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) cc[j] = pos + 64 * j;
-    // the side values of chunk j: 8 floats at ((j * 2 + half) * 64 + lane) * 4 of an array
-    auto side_at = [&](int off, int j, int h) { return side + off + ((j * 2 + h) * 64 + lane) * 4; };
-    auto put8 = [&](int off, int j, const float* f) {
-        *reinterpret_cast<float4*>(side_at(off, j, 0)) = make_float4(f[0], f[1], f[2], f[3]);
-        *reinterpret_cast<float4*>(side_at(off, j, 1)) = make_float4(f[4], f[5], f[6], f[7]);
+    for (int j = 0; j < CPL; ++j) cc[j] = chunk_of(ws, j);
+    // the side values of slot j of the row's wavefront s: 8 floats at (((s CPL + j) * 2 + half) * 64 + lane) * 4 of an
+    // array (each of the row's wavefronts has its own slots)
+    auto side_at = [&](int off, int sj, int h) { return side + off + ((sj * 2 + h) * 64 + lane) * 4; };
+    auto put8 = [&](int off, int sj, const float* f) {
+        *reinterpret_cast<float4*>(side_at(off, sj, 0)) = make_float4(f[0], f[1], f[2], f[3]);
+        *reinterpret_cast<float4*>(side_at(off, sj, 1)) = make_float4(f[4], f[5], f[6], f[7]);
     };
     auto get8 = [&](int off, int j, float* f) {
-        const float4 a = *reinterpret_cast<const float4*>(side_at(off, j, 0));
-        const float4 b = *reinterpret_cast<const float4*>(side_at(off, j, 1));
+        const float4 a = *reinterpret_cast<const float4*>(side_at(off, ws * CPL + j, 0));
+        const float4 b = *reinterpret_cast<const float4*>(side_at(off, ws * CPL + j, 1));
         f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
     };
-    // one table row's 1 + scale and shift for chunk j, decoded from memory
-    auto table8 = [&](int64_t trow, int j, float* s1, float* sh) {
+    // one table row's 1 + scale and shift for chunk c, decoded from memory
+    auto table8 = [&](int64_t trow, int c, float* s1, float* sh) {
         Raw<V, TDT == H3S_F32> sr, hr;
-        fetch(sr, A.scale, TDT, trow * C + (int64_t) cc[j] * V);
-        fetch(hr, A.shift, TDT, trow * C + (int64_t) cc[j] * V);
+        fetch(sr, A.scale, TDT, trow * C + (int64_t) c * V);
+        fetch(hr, A.shift, TDT, trow * C + (int64_t) c * V);
         decode(sr, TDT, s1);
         decode(hr, TDT, sh);
 #pragma unroll
         for (int e = 0; e < V; ++e) s1[e] = 1.0f + s1[e];
     };
-    // the block's side values (the weight with W, the table row trow): wavefront w decodes chunk slots w, w + NW, ...
+    // the block's side values (the weight with W, the table row trow): wavefront w decodes slots w, w + NW, ... of
+    // the row's WPR CPL slots
     auto fill = [&](int64_t trow, bool with_w) {
-        for (int j = wave; j < CPL; j += NW) {
-#pragma unroll
-            for (int jj = 0; jj < CPL; ++jj) {
-                if (jj != j) continue;                       // a constant slot index for the register arrays
-                if constexpr (HASW) {
-                    if (with_w) {
-                        Raw<V, true> wr;
-                        fetch(wr, A.w, H3S_F32, (int64_t) cc[jj] * V);
-                        float f[V];
-                        decode(wr, H3S_F32, f);
-                        put8(WOFF, jj, f);
-                    }
+        for (int sj = wave; sj < WPR * CPL; sj += NW) {
+            const int c = chunk_of(sj / CPL, sj % CPL);
+            if constexpr (HASW) {
+                if (with_w) {
+                    Raw<V, true> wr;
+                    fetch(wr, A.w, H3S_F32, (int64_t) c * V);
+                    float f[V];
+                    decode(wr, H3S_F32, f);
+                    put8(WOFF, sj, f);
                 }
-                if constexpr (TAB) {
-                    float s1[V], sh[V];
-                    table8(trow, jj, s1, sh);
-                    put8(SOFF, jj, s1);
-                    put8(HOFF, jj, sh);
-                }
+            }
+            if constexpr (TAB) {
+                float s1[V], sh[V];
+                table8(trow, c, s1, sh);
+                put8(SOFF, sj, s1);
+                put8(HOFF, sj, sh);
             }
         }
     };
@@ -539,15 +644,18 @@ void quant_wave_kernel(QuantArgs A) {
     }
 
     const int G = rot_fixed(ROT) ? rot_fixed(ROT) : A.group;
-    const float cgs = SW ? A.cg * syl_sign<V>(pos, G) : A.cg;
+    const float cgs = rot_kind(ROT) == H3S_ROT_SYLVESTER ? A.cg * syl_sign<V>(pos, G) : A.cg;
     // a row's x: a base the whole wavefront shares (the row is the wavefront's) and a 32-bit unsigned byte offset
     // a lane, so the loads and stores take the scalar-base form and hold no 64-bit address registers (the row
     // passes through readfirstlane, which keeps the compiler from turning each chunk's address into an induction
-    // variable of its own across the grid-stride loop)
-    auto load_row = [&](uint4 (&xr)[CPL], int64_t row) {
-        const char* xp = reinterpret_cast<const char*>(A.x) + wave_uniform(row) * C * 2;
+    // variable of its own across the grid-stride loop). With SWIGLU the row is [gate | up], 2 C features.
+    auto load_row = [&](uint4 (&xr)[CPL], uint4 (&ur)[CPL], int64_t row) {
+        const char* xp = reinterpret_cast<const char*>(A.x) + wave_uniform(row) * C * 2 * (SWI ? 2 : 1);
 #pragma unroll
         for (int j = 0; j < CPL; ++j) xr[j] = ld_nt(xp + (uint32_t) (cc[j] * 16));
+        if constexpr (SWI)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) ur[j] = ld_nt(xp + (uint32_t) ((NCH + cc[j]) * 16));
     };
     // The table rows of each step's group of NW rows (rows g + [0, NW), g = b0 + k U, one a wavefront), 64 steps
     // at a time, one step a lane, taken out with readlane: the group's first row's (gix), this wavefront's (tix),
@@ -571,25 +679,63 @@ void quant_wave_kernel(QuantArgs A) {
             uni = __builtin_amdgcn_ballot_w64(same);
         }
     };
-    // One row, with the table row cached in LDS.
-    auto process = [&](int64_t row) {
-        uint4 x[CPL];
-        load_row(x, row);
+    // One row (its share), with the table row cached in LDS; live false: a row past the end (ONE with several
+    // wavefronts a row), computed on a copy for the barrier and not stored.
+    // tab_lds: the row's table row is the one cached in LDS (else its values are read from memory, chunk by chunk)
+    auto process = [&](int64_t row, bool live, bool tab_lds) {
+        uint4 x[CPL], u[CPL];
+        load_row(x, u, row);
         float v[CPL][V];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(x[j], v[j]);
 
         // ---- rms_norm_mod into bfloat16 (the reference's scratch h) ----
         if constexpr (NORM) {
+            // PAIR: chunk 128 k + 2 pos + h is canonical lane 2 (pos % 32) + h of canonical wavefront 2 (k % 2) +
+            // pos / 32, so a lane keeps a partial sum for each (k % 2, h); each is summed over its half wave (the
+            // canonical offsets 32 .. 2 are the position offsets 16 .. 1), the two h then added (offset 1), and the
+            // halves hold canonical wavefronts (0, 2) and (1, 3): (w0 + w2) + (w1 + w3) across them
             float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < CPL; ++j)
+                if (valid(j)) {
+                    // (two wavefronts a row: a wavefront's run pairs all have k % 2 = its share s; one chunk a lane,
+                    // slot j of wavefront s is canonical wavefront (2 j + s) % 4, its partial j % 2)
+                    const int q = PAIR ? (WPR == 2 ? (j & 1) : ((j / 2) % 2) * 2 + (j & 1)) : WPR == 2 ? j % 2 : j % 4;
 #pragma unroll
-                for (int e = 0; e < V; ++e) ss[j % 4] = __builtin_fmaf(v[j][e], v[j][e], ss[j % 4]);
-            float w4[4];
+                    for (int e = 0; e < V; ++e) ss[q] = __builtin_fmaf(v[j][e], v[j][e], ss[q]);
+                }
+            float tot;
+            if constexpr (PAIR && WPR == 2) {
+                // wavefront s holds the run pairs k = 2 p + s, so k % 2 = s: its halves hold canonical wavefronts 2 s
+                // and 2 s + 1 (its partials ss[0], ss[1] by h); the row's two wavefronts meet in LDS for
+                // (w0 + w2) + (w1 + w3)
+                const float w = wave_sum<32, SW>(ss[0]) + wave_sum<32, SW>(ss[1]);
+                if ((lane & 31) == 0) wsum[wave][lane >> 5] = w;
+                lds_barrier();
+                const int b = wr * 2;
+                tot = (wsum[b][0] + wsum[b + 1][0]) + (wsum[b][1] + wsum[b + 1][1]);
+            } else if constexpr (WPR == 2) {
+                // wavefront s holds canonical wavefronts s (ss[0]) and s + 2 (ss[1]): w0 + w2 in the first, w1 + w3
+                // in the second, met in LDS
+                const float w = wave_sum<64, SW>(ss[0]) + wave_sum<64, SW>(ss[1]);
+                if (lane == 0) wsum[wave][0] = w;
+                lds_barrier();
+                tot = wsum[wr * 2][0] + wsum[wr * 2 + 1][0];
+            } else if constexpr (PAIR) {
+                float w4[4];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) w4[g] = wave_sum<64, SW>(ss[g]);
-            const float inv = inv_root((w4[0] + w4[2]) + (w4[1] + w4[3]), (float) C, A.eps);
+                for (int g = 0; g < 4; ++g) w4[g] = wave_sum<32, SW>(ss[g]);
+                const float half = (w4[0] + w4[1]) + (w4[2] + w4[3]);
+                tot = half + xor_lane<32>(half);
+            } else {
+                float w4[4];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) w4[g] = wave_sum<64, SW>(ss[g]);
+                tot = (w4[0] + w4[2]) + (w4[1] + w4[3]);
+            }
+            const float inv = inv_root(tot, (float) C, A.eps);
+            uint16_t* hrow = OUTH ? reinterpret_cast<uint16_t*>(A.h) + wave_uniform(row) * C : nullptr;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 if constexpr (HASW) {
@@ -603,52 +749,99 @@ void quant_wave_kernel(QuantArgs A) {
                 }
                 if constexpr (TAB) {
                     float s1[V], sh[V];
-                    get8(SOFF, j, s1);
-                    get8(HOFF, j, sh);
+                    // (one wavefront a row takes rows[] grid-strided, with every table row through LDS)
+                    if (WPR == 1 || tab_lds) {
+                        get8(SOFF, j, s1);
+                        get8(HOFF, j, sh);
+                    } else {
+                        table8(A.rows[row], cc[j], s1, sh);
+                    }
 #pragma unroll
                     for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * s1[e] + sh[e];
                 }
+                uint32_t p[V / 2];
+#pragma unroll
+                for (int e = 0; e < V; e += 2) {
+                    p[e / 2] = pack_bf16(v[j][e], v[j][e + 1]);
+                    v[j][e] = bf16_lo(p[e / 2]);
+                    v[j][e + 1] = bf16_hi(p[e / 2]);
+                }
+                if constexpr (OUTH) {
+                    if (valid(j)) st_nt(hrow + (uint32_t) (cc[j] * 8), make_uint4(p[0], p[1], p[2], p[3]));
+                }
+                // with tables, one chunk's LDS reads at a time: the registers stay within four wavefronts a SIMD
+                if constexpr (TAB) __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (OUTH) return;
+        }
+        // ---- swiglu into bfloat16, as h3s_swiglu computes it (the MLP's scratch act) ----
+        if constexpr (SWI) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                float uu[V];
+                Vec<XDT>::unpack(u[j], uu);
+#pragma unroll
+                for (int e = 0; e < V; ++e) v[j][e] = act_silu(v[j][e]) * uu[e];
 #pragma unroll
                 for (int e = 0; e < V; e += 2) {
                     const uint32_t p = pack_bf16(v[j][e], v[j][e + 1]);
                     v[j][e] = bf16_lo(p);
                     v[j][e + 1] = bf16_hi(p);
                 }
-                // with tables, one chunk's LDS reads at a time: the registers stay within four wavefronts a SIMD
-                if constexpr (TAB) __builtin_amdgcn_sched_barrier(0);
             }
         }
 
         // ---- the block rotation, then the row's absolute maximum ----
         float m = 0.0f;
+        if constexpr (PAIR) {
+#pragma unroll
+            for (int j = 0; j < CPL; j += 2) regular256_pair(v[j], v[j + 1]);
+        }
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             if constexpr (ROTATED) {
-                if constexpr (SW) sylvester<V, true>(v[j], pos, G);
-                else regular<V>(v[j], G);
+                if constexpr (!PAIR) {
+                    if constexpr (SW) sylvester<V, true>(v[j], pos, G);
+                    else regular<V>(v[j], G);
+                }
 #pragma unroll
                 for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * cgs;
             }
+            if (valid(j))
 #pragma unroll
-            for (int e = 0; e < V; ++e) m = fmaxf(m, fabsf(v[j][e]));
+                for (int e = 0; e < V; ++e) m = fmaxf(m, fabsf(v[j][e]));
         }
         m = wave_max<64>(m);
+        if constexpr (WPR > 1) {
+            // the row's wavefronts meet once: every wavefront of the block reaches this barrier (ONE)
+            if (lane == 0) wmax[wave] = m;
+            lds_barrier();
+#pragma unroll
+            for (int s = 0; s < WPR; ++s) m = fmaxf(m, wmax[wr * WPR + s]);
+        }
         const float sc = fmaxf(m / 127.0f, 1e-30f), r = 1.0f / sc;
-        if (lane == 0) A.s[row] = sc;
+        if (!live) return;
+        if (lane == 0 && ws == 0) A.s[row] = sc;
 
         // ---- the codes, 8 bytes a chunk ----
         int8_t* qrow = A.q + wave_uniform(row) * C;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
+            if (!valid(j)) continue;
             const float* o = v[j];
             const uint32_t lo = bytes4(code_of(o[0], sc, r), code_of(o[1], sc, r), code_of(o[2], sc, r), code_of(o[3], sc, r));
             const uint32_t hi = bytes4(code_of(o[4], sc, r), code_of(o[5], sc, r), code_of(o[6], sc, r), code_of(o[7], sc, r));
             st_nt(qrow + (uint32_t) (cc[j] * 8), make_uint2(lo, hi));
         }
     };
-    int64_t row = b0 + wave;
+    int64_t row = b0 + wr;
     if constexpr (ONE) {
-        if (row < M) process(row);
+        // the block's side values hold the table row of its first row; a row of another table row (one a segment
+        // boundary of rows[] puts in the block) reads its table values from memory
+        const int64_t rc = row < M ? row : M - 1;
+        const bool tab_lds = !TAB || !A.rows || A.rows[rc] == tcache;
+        if constexpr (WPR > 1) process(rc, row < M, tab_lds);
+        else if (row < M) process(row, true, tab_lds);
         return;
     }
     for (int64_t k = 0, g = b0; g < M; row += U, g += U, ++k) {
@@ -682,10 +875,10 @@ void quant_wave_kernel(QuantArgs A) {
                     lds_barrier();
                     tcache = t;
                 }
-                if (row < M && own == t) process(row);
+                if (row < M && own == t) process(row, true, true);
             }
         } else {
-            if (row < M) process(row);
+            if (row < M) process(row, true, true);
         }
     }
 }
@@ -697,42 +890,100 @@ constexpr int kQuantNone = 0, kQuantW = ROW_W, kQuantWTab = ROW_W | ROW_TAB, kQu
               kQuantRaw = ROW_RAW, kQuantSwiglu = ROW_SWIGLU;
 
 // The launch of quant_wave_kernel: blocks of 4 wavefronts (8 with tables, so one LDS copy of the side values
-// serves more rows).
-template <int XDT, int CPL, int ROT, int F> int quant_wave_one(Ctx* c, const char* fn, const QuantArgs& A) {
-    const int threads = 64 * quant_wave_nw(F);
-    const size_t lds = quant_wave_side_bytes<CPL>(F);
-    const int64_t rows_blocks = (A.M + threads / 64 - 1) / (threads / 64);
+// serves more rows, or with several wavefronts a row).
+template <int XDT, int CPL, int ROT, int F, int NCH, int WPR, bool PAIR = false>
+int quant_wave_one(Ctx* c, const char* fn, const QuantArgs& A) {
+    constexpr int NW = quant_wave_nw(F, WPR), RPB = NW / WPR;
+    const int threads = 64 * NW;
+    const size_t lds = quant_wave_side_bytes<CPL, WPR>(F);
+    const int64_t rows_blocks = (A.M + RPB - 1) / RPB;
     // One row a wavefront, nothing prefetched (config 4 at 47104 rows: 106 us, against 119 us grid-strided with the
     // next row in flight): without tables, and with tables whose one row serves every token (rows NULL), each block
     // decoding its side values once. With a table row per token, as many blocks as the device holds, grid-strided,
     // each refilling its cached table row when the rows' table row changes.
-    if constexpr (F & ROW_TAB) {
+    if constexpr ((F & ROW_TAB) && WPR == 1) {
         if (A.rows) {
-            const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, false>;
+            const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, false, NCH, WPR, PAIR>;
             const int64_t blocks = std::min<int64_t>((int64_t) c->cus * blocks_per_cu(k, threads, lds), rows_blocks);
-            quant_wave_kernel<XDT, CPL, ROT, F, false><<<(unsigned) blocks, threads, lds, c->stream>>>(A);
+            quant_wave_kernel<XDT, CPL, ROT, F, false, NCH, WPR, PAIR><<<(unsigned) blocks, threads, lds, c->stream>>>(A);
             return launched(fn);
         }
     }
-    quant_wave_kernel<XDT, CPL, ROT, F, true><<<(unsigned) rows_blocks, threads, lds, c->stream>>>(A);
+    quant_wave_kernel<XDT, CPL, ROT, F, true, NCH, WPR, PAIR><<<(unsigned) rows_blocks, threads, lds, c->stream>>>(A);
     return launched(fn);
 }
+// rows of 2048 or 4096 features (CPL 4 or 8, every slot whole): the norm with its side inputs, or the quantizer on x
 template <int XDT, int CPL> int quant_wave_launch(Ctx* c, const char* fn, const QuantArgs& A, int f) {
-#define H3_QW(RR)                                                                          \
-    if (f == kQuantNone) return quant_wave_one<XDT, CPL, RR, kQuantNone>(c, fn, A);         \
-    if (f == kQuantW) return quant_wave_one<XDT, CPL, RR, kQuantW>(c, fn, A);               \
-    if (f == kQuantWTab) return quant_wave_one<XDT, CPL, RR, kQuantWTab>(c, fn, A);         \
-    if (f == kQuantWTab32) return quant_wave_one<XDT, CPL, RR, kQuantWTab32>(c, fn, A);     \
-    return quant_wave_one<XDT, CPL, RR, kQuantRaw>(c, fn, A);
+#define H3_QW(RR)                                                                                  \
+    if (f == kQuantNone) return quant_wave_one<XDT, CPL, RR, kQuantNone, 64 * CPL, 1>(c, fn, A);     \
+    if (f == kQuantW) return quant_wave_one<XDT, CPL, RR, kQuantW, 64 * CPL, 1>(c, fn, A);           \
+    if (f == kQuantWTab) return quant_wave_one<XDT, CPL, RR, kQuantWTab, 64 * CPL, 1>(c, fn, A);     \
+    if (f == kQuantWTab32) return quant_wave_one<XDT, CPL, RR, kQuantWTab32, 64 * CPL, 1>(c, fn, A); \
+    return quant_wave_one<XDT, CPL, RR, kQuantRaw, 64 * CPL, 1>(c, fn, A);
     if (A.rot == H3S_ROT_SYLVESTER && A.group == 128) { H3_QW(rot_with(H3S_ROT_SYLVESTER, 128)) }
     if (A.rot == H3S_ROT_SYLVESTER) { H3_QW(H3S_ROT_SYLVESTER) }
     if (A.rot == H3S_ROT_REGULAR) { H3_QW(H3S_ROT_REGULAR) }
     H3_QW(H3S_ROT_NONE)
 #undef H3_QW
 }
+// The model's own widths (docs/BASELINE.md:13), each with the layout measured fastest for it. With the checkpoints'
+// ConvRot group (regular 256), a lane holds 16 consecutive features of a group (two chunks, "pairs"), so every digit
+// of the rotation is inside the lane or one DPP operand away; without a rotation, one chunk a lane:
+//   5376 features (the hidden width):     the norm with a weight (and float32 tables: the DiT's AdaLN), or the
+//                                         quantizer on x: two wavefronts a row, 3 run pairs each, the row's last a
+//                                         quarter full (unrotated: the norm two wavefronts a row of 6 slots, the
+//                                         last of the second empty; the quantizer on x one wavefront a row, 11
+//                                         slots, the last half full); with ROW_OUTH h3s_rms_norm_mod itself
+//   7168 features (the attention's out):  the quantizer on x: seven wavefronts a row, one run pair each (two
+//                                         wavefronts of 7 slots unrotated)
+//   4096 features:                        the quantizer on x, rotated: two wavefronts a row, two run pairs each
+//   8192 features (the MLP's middle of    the quantizer on swiglu(x), rotated: four wavefronts a row, two run pairs
+//   the measured 47104 x 8192 workload):  each
+//   14336 features (the MLP's middle):    the quantizer on x or on swiglu(x): seven wavefronts a row, two run pairs
+//                                         each (four wavefronts of 7 slots unrotated)
+template <int XDT> int quant_wave_model(Ctx* c, const char* fn, const QuantArgs& A, int f) {
+    const bool reg256 = A.rot == H3S_ROT_REGULAR && A.group == 256, none = A.rot == H3S_ROT_NONE;
+    constexpr int R256 = rot_with(H3S_ROT_REGULAR, 256), R0 = H3S_ROT_NONE;
+    if (A.C == 5376) {
+        constexpr int N = 672;
+        if (f == (kQuantW | ROW_OUTH)) return quant_wave_one<XDT, 6, R0, kQuantW | ROW_OUTH, N, 2>(c, fn, A);
+        if (f == (kQuantWTab32 | ROW_OUTH)) return quant_wave_one<XDT, 6, R0, kQuantWTab32 | ROW_OUTH, N, 2>(c, fn, A);
+        if (f == kQuantWTab32 && reg256) return quant_wave_one<XDT, 6, R256, kQuantWTab32, N, 2, true>(c, fn, A);
+        if (f == kQuantWTab32 && none) return quant_wave_one<XDT, 6, R0, kQuantWTab32, N, 2>(c, fn, A);
+        if (f == kQuantW && reg256) return quant_wave_one<XDT, 6, R256, kQuantW, N, 2, true>(c, fn, A);
+        if (f == kQuantW && none) return quant_wave_one<XDT, 6, R0, kQuantW, N, 2>(c, fn, A);
+        if (f == kQuantRaw && reg256) return quant_wave_one<XDT, 6, R256, kQuantRaw, N, 2, true>(c, fn, A);
+        if (f == kQuantRaw && none) return quant_wave_one<XDT, 11, R0, kQuantRaw, N, 1>(c, fn, A);
+    }
+    if (A.C == 7168 && f == kQuantRaw) {
+        if (reg256) return quant_wave_one<XDT, 2, R256, kQuantRaw, 896, 7, true>(c, fn, A);
+        if (none) return quant_wave_one<XDT, 7, R0, kQuantRaw, 896, 2>(c, fn, A);
+    }
+    if (A.C == 4096 && f == kQuantRaw && reg256) return quant_wave_one<XDT, 4, R256, kQuantRaw, 512, 2, true>(c, fn, A);
+    if (A.C == 8192 && f == kQuantSwiglu && reg256) return quant_wave_one<XDT, 4, R256, kQuantSwiglu, 1024, 4, true>(c, fn, A);
+    if (A.C == 14336) {
+        if (f == kQuantRaw && reg256) return quant_wave_one<XDT, 4, R256, kQuantRaw, 1792, 7, true>(c, fn, A);
+        if (f == kQuantRaw && none) return quant_wave_one<XDT, 7, R0, kQuantRaw, 1792, 4>(c, fn, A);
+        if (f == kQuantSwiglu && reg256) return quant_wave_one<XDT, 4, R256, kQuantSwiglu, 1792, 7, true>(c, fn, A);
+        if (f == kQuantSwiglu && none) return quant_wave_one<XDT, 7, R0, kQuantSwiglu, 1792, 4>(c, fn, A);
+    }
+    return 1;   // not a shape of this set
+}
+// whether quant_wave_model takes this call
+inline bool quant_wave_model_takes(const QuantArgs& A, int f) {
+    const bool reg256 = A.rot == H3S_ROT_REGULAR && A.group == 256, none = A.rot == H3S_ROT_NONE;
+    if (f & ROW_OUTH) return A.C == 5376 && none && (f == (kQuantW | ROW_OUTH) || f == (kQuantWTab32 | ROW_OUTH));
+    if (!reg256 && !none) return false;
+    if (A.C == 5376) return f == kQuantWTab32 || f == kQuantW || f == kQuantRaw;
+    if (A.C == 7168) return f == kQuantRaw;
+    if (A.C == 4096) return f == kQuantRaw && reg256;
+    if (A.C == 8192) return f == kQuantSwiglu && reg256;
+    if (A.C == 14336) return f == kQuantRaw || f == kQuantSwiglu;
+    return false;
+}
 
-// what the quantizer runs on: rms_norm_mod of x, x itself, or swiglu of x
-enum QuantMode { QUANT_NORM, QUANT_RAW, QUANT_SWIGLU };
+// what the quantizer runs on: rms_norm_mod of x, x itself, or swiglu of x; or rms_norm_mod's h itself as the result
+enum QuantMode { QUANT_NORM, QUANT_RAW, QUANT_SWIGLU, QUANT_NORM_OUT };
 
 // Launches the kernel for one input type; the plan comes from row_plan.
 template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, int mode, RowPlan p) {
@@ -741,6 +992,15 @@ template <int XDT> int quant_launch(Ctx* c, const char* fn, const QuantArgs& A, 
         f = ROW_DYN;
     if (mode == QUANT_RAW) f = kQuantRaw;
     if (mode == QUANT_SWIGLU) f = XDT == H3S_F32 || A.h_dt != H3S_BF16 ? (ROW_SWIGLU | ROW_DYN) : kQuantSwiglu;
+    if (mode == QUANT_NORM_OUT) f |= ROW_OUTH;
+    // the model's widths, one or two wavefronts a row
+    if constexpr (XDT != H3S_F32) {
+        if (quant_wave_model_takes(A, f) && (A.M >= c->quant_wave_min || (f & ROW_OUTH))) {
+            const int r = quant_wave_model<XDT>(c, fn, A, f);
+            if (r != 1) return r;
+        }
+    }
+    if (f & ROW_OUTH) return fail(std::string(fn) + ": no kernel stores h for this row shape");
 #define H3_QUANT_F(CC, RR, FF)                                                                      \
     {                                                                                                \
         const PersistentLaunch R = persistent_launch(c, (const void*) quant_kernel<XDT, CC, RR, FF>, A.M, p, A.scale != nullptr); \

@@ -183,6 +183,7 @@ enum : int {
     ROW_LN = 512,       // the row chain: layer norm (else RMS norm)
     ROW_ACT1 = 1024,    // the row chain's activation, 2 bits: H3S_ACT_NONE, H3S_ACT_GELU_TANH or H3S_ACT_SILU
     ROW_SWIGLU = 4096,  // the quantizer on silu(gate) * up of a [gate | up] row, with no norm (h3s_swiglu_quant)
+    ROW_OUTH = 8192,    // the norm's bfloat16 row h stored as the result, no rotation or codes (h3s_rms_norm_mod)
 };
 constexpr int row_act(int f) { return (f / ROW_ACT1) & 3; }
 

@@ -51,6 +51,11 @@ H3S_EXPORT int h3s_rms_norm_mod(void* ctx, const void* x, int x_dt, int64_t M, i
     if (!weight) return fail(std::string(fn) + ": the weight is required");
     Ctx* c = ctx_of(ctx, fn);
     if (!c) return -1;
+    // the model's hidden width: one wavefront a row (the same arithmetic and order; the chain's four wavefronts a
+    // row leave three eighths of their last chunk slot idle at 5376 features)
+    const int r = launch_norm_out(c, fn, x, x_dt, M, C, weight, eps, A.rows, A.scale ? (const float*) A.scale : nullptr,
+                                  A.shift ? (const float*) A.shift : nullptr, out, out_dt);
+    if (r != 1) return r;
     return chain_dispatch(c, fn, x_dt, A, p);
 } catch (const std::exception& e) { return fail(e.what()); }
 

@@ -71,9 +71,39 @@ def test_int8_quantize_dit_widths(request, layout, K, group):
     codes_close(q.to_numpy(), want_q, "codes")
 
 
+# ---- the two-chunks-a-lane (16 features) layout of the regular-256 rotation at the other widths it serves ----
+@pytest.mark.parametrize("layout", ["four", "wave"])
+def test_int8_quantize_4096_pairs(request, layout):
+    dev = request.getfixturevalue("dev" if layout == "four" else "dev_wave")
+    M, K = 1025, 4096
+    x = bf16_rows(90, M, K)
+    want_q, want_s = o.quantize_act(x, o.BF16, M, K, o.ROT_REGULAR, 256)
+    q, s = new(dev, "I8", [M, K]), new(dev, "F32", [M])
+    ops.int8_quantize(up(dev, x, "BF16", [M, K]), q, s, 256)
+    assert_bits_equal(s.to_numpy(), want_s, "scales")
+    codes_close(q.to_numpy(), want_q, "codes")
+
+
+@pytest.mark.parametrize("layout", ["four", "wave"])
+def test_swiglu_quant_8192_pairs(request, layout):
+    dev = request.getfixturevalue("dev" if layout == "four" else "dev_wave")
+    M, C = 301, 8192
+    x = bf16_rows(91, M, 2 * C, 4.0, heavy=False)
+    xt = up(dev, x, "BF16", [M, 2 * C])
+    q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+    ops.swiglu_quant(xt, q, s, rot=o.ROT_REGULAR, group=256)
+    act = new(dev, "BF16", [M, C])
+    ops.swiglu(xt, act)
+    want_q, want_s = o.quantize_act(act.to_numpy().ravel(), o.BF16, M, C, o.ROT_REGULAR, 256)
+    assert_bits_equal(s.to_numpy(), want_s, "scales")
+    codes_close(q.to_numpy(), want_q, "codes")
+
+
 # ---- h3s_swiglu_quant at fc2's width: 14336 features, 1792 16-byte chunks a row ----
 @pytest.mark.parametrize("M,rot,group", [(9, o.ROT_REGULAR, 256), (2500, o.ROT_REGULAR, 256), (33, o.ROT_NONE, 0)])
-def test_swiglu_quant_fc2_width(dev, M, rot, group):
+@pytest.mark.parametrize("layout", ["four", "wave"])
+def test_swiglu_quant_fc2_width(request, layout, M, rot, group):
+    dev = request.getfixturevalue("dev" if layout == "four" else "dev_wave")
     C = DFF
     x = bf16_rows(M + 41, M, 2 * C, 4.0, heavy=False)
     xt = up(dev, x, "BF16", [M, 2 * C])
@@ -122,6 +152,27 @@ def test_norm_quant_dit_width(request, layout, rot, group):
         ops.int8_quantize(h, q2, s2, group)
         assert_bits_equal(s2.to_numpy(), want_s, "two-call scales")
         codes_close(q2.to_numpy(), want_q, "two-call codes")
+
+
+# ---- h3s_rms_norm_mod at the hidden width in both layouts (the one-wavefront form stores h itself) ----
+@pytest.mark.parametrize("mod", [True, False])
+@pytest.mark.parametrize("M", [1, 37, 300])
+@pytest.mark.parametrize("layout", ["four", "wave"])
+def test_rms_norm_mod_dit_width(request, layout, mod, M):
+    dev = request.getfixturevalue("dev" if layout == "four" else "dev_wave")
+    C = DH
+    x = bf16_rows(80 + M, M, C)
+    rng = np.random.default_rng(81)
+    w = (1.0 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    R = 3
+    rows = (np.arange(M) * 7 % R).astype(np.int32) if mod else None
+    sc = (0.3 * rng.standard_normal(R * C)).astype(np.float32) if mod else None
+    sh = (0.3 * rng.standard_normal(R * C)).astype(np.float32) if mod else None
+    want = o.rms_norm_mod(x, o.BF16, M, C, w, 1e-5, rows, sc, sh, o.BF16)
+    h = new(dev, "BF16", [M, C])
+    m = ops.Mod(up(dev, rows, "I32", [M]), up(dev, sc, "F32", [R, C]), up(dev, sh, "F32", [R, C])) if mod else None
+    ops.rms_norm_mod(up(dev, x, "BF16", [M, C]), up(dev, w, "F32", [C]), 1e-5, m, h)
+    assert_bits_equal(h.to_numpy(), want, f"rms_norm_mod M={M}")
 
 
 # ---- h3s_gate_add and h3s_swiglu at the block's shapes, many rows ----
