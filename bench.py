@@ -7,7 +7,7 @@
 A step is one launch of the headline kernel over the whole batch: the AdaLN chain (LayerNorm without affine, then
 x * (1 + scale) + shift, GELU-tanh, out = res + gate * y) on X, res [16896 x 4096] bf16, token grid T16 x H24 x W44.
 ``value`` is its achieved HBM bandwidth: algorithmic bytes (X and res read once, out written once) divided by the
-mean launch time.
+median launch time (each launch timed between HIP events; the mean over the window is reported beside it).
 
 Cache-cold timing: MI355X's 256 MB Infinity Cache would hold part of a 415 MB working set launched back to back on
 the same buffers. Every workload of less than 1 GiB per launch is therefore timed over a ring of independent buffer
@@ -256,15 +256,18 @@ def main() -> int:
         if args.mark:
             torch.cuda._sleep(1)
             marked.append(key)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(steps):
+        # an event before every launch and one after the last: each launch's time, and the window's
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        for i in range(steps):
+            ev[i].record()
             fn()
-        e1.record()
+        ev[steps].record()
         if args.mark:
             torch.cuda._sleep(1)
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / steps   # ms per launch
+        each = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+        means[key] = ev[0].elapsed_time(ev[steps]) / steps
+        return each[steps // 2] if steps % 2 else 0.5 * (each[steps // 2 - 1] + each[steps // 2])   # median ms
 
     def cycle(fns):
         """one launch of the next buffer set of a ring"""
@@ -275,7 +278,7 @@ def main() -> int:
             state[0] += 1
         return f
 
-    kernels, rings = {}, {}
+    kernels, rings, means = {}, {}, {}
 
     def run(key, make, steps=20, warmup=3, ring=None):
         """times workload `key`: make() builds one buffer set and returns its launch; a ring of them when small
@@ -539,8 +542,8 @@ def main() -> int:
     per = {}
     for k, ms in kernels.items():
         gbs = B[k] / (ms * 1e-3) / 1e9
-        e = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_GBS, 4), "bytes": B[k],
-             "ring": rings[k], "steps": steps_of[k]}
+        e = {"ms": round(ms, 5), "ms_mean": round(means[k], 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_GBS, 4),
+             "bytes": B[k], "ring": rings[k], "steps": steps_of[k]}
         if k.startswith("cfg5b"):
             tops = 2 * M4 * C * 16384 / (ms * 1e-3) / 1e12
             e.update({"TOPS_i8": round(tops, 1), "frac_i8_peak": round(tops / PEAK_I8_TOPS, 4)})
@@ -573,6 +576,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms2, 5),
+        "ms_per_step_mean": round(means[HEADLINE], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -675,7 +679,8 @@ def cpu_baseline(x2, r2, tab, t):
     out = {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
            "sample": f"the full 16896 x 4096 workload, median of {n} runs ({med * 1e3:.1f} ms each), {threads} threads "
                      f"on {share['model']} (nproc {share['nproc']}, affinity {share['affinity']}, cgroup quota "
-                     f"{share['cgroup_quota']})",
+                     f"{share['cgroup_quota']}; at most 16 threads: the CPU share a one-GPU job has on these hosts, "
+                     f"whatever nproc shows)",
            "host": share}
 
     per = {}

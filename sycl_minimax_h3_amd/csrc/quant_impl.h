@@ -537,20 +537,22 @@ template <int CPL, int WPR = 1> constexpr size_t quant_wave_side_bytes(int f) {
 }
 // wavefronts a block: 8 with tables (one LDS copy of the side values serves more rows) or two or four a row, a row's
 // own with more, else 4
-constexpr int quant_wave_nw(int f, int wpr) { return wpr > 4 ? wpr : (f & ROW_TAB) || wpr > 1 ? 8 : 4; }
+constexpr int quant_wave_nw(int f, int wpr) { return wpr > 4 || wpr == 3 ? wpr * (8 / wpr > 0 ? 8 / wpr : 1) : (f & ROW_TAB) || wpr > 1 ? 8 : 4; }
 // ONE: the grid has a wavefront (group) for every row, so each takes one row (108 registers for config 4's kernel,
 // four wavefronts a SIMD); else the grid strides over the rows, with nothing prefetched either: four wavefronts a
 // SIMD hide the loads (the registers of a prefetched next row would leave room for three). With tables and no
 // rotation (and at most 8 slots) the kernel is held to four wavefronts a SIMD (120 registers, no spills).
-template <int XDT, int CPL, int ROT, int F, bool ONE, int NCH, int WPR = 1, bool PAIR = false>
-__global__ __launch_bounds__(512)
-__attribute__((amdgpu_waves_per_eu((F & ROW_TAB) && rot_kind(ROT) == H3S_ROT_NONE && CPL <= 8 ? 4 : 1)))
-void quant_wave_kernel(QuantArgs A) {
+// The body of quant_wave_kernel for the blocks [blk0, ...) of one layout: block blk takes rows row0 + blk R ... (R rows
+// a block step); NW wavefronts a block.
+template <int XDT, int CPL, int ROT, int F, bool ONE, int NCH, int WPR, bool PAIR, int NW>
+__device__ __forceinline__ void quant_wave_body(const QuantArgs& A, int64_t blk, int64_t row0) {
     static_assert(XDT != H3S_F32 && !(F & ROW_DYN), "quant_wave_kernel: 16-bit x, exact side inputs");
     static_assert(PAIR ? NCH > 128 * WPR * (CPL / 2 - 1) && NCH <= 128 * WPR * (CPL / 2)
                        : NCH > 64 * WPR * (CPL - 1) && NCH <= 64 * WPR * CPL, "quant_wave_kernel: NCH reaches the last slots");
-    static_assert(WPR == 1 || (ONE && ((F & (ROW_RAW | ROW_SWIGLU)) || WPR == 2)),
-                  "quant_wave_kernel: several wavefronts a row: the quantizer on x or swiglu(x), or the norm, two a row");
+    static_assert(WPR == 1 || (ONE && ((F & (ROW_RAW | ROW_SWIGLU)) || WPR == 2 || (WPR == 4 && !PAIR))),
+                  "quant_wave_kernel: several wavefronts a row: the quantizer on x or swiglu(x), or the norm, two a row "
+                  "(four a row one chunk a lane)");
+    static_assert(NW % WPR == 0, "quant_wave_kernel: whole rows a block");
     static_assert(!PAIR || (ROT == rot_with(H3S_ROT_REGULAR, 256) && CPL % 2 == 0), "quant_wave_kernel: pairs for regular 256");
     constexpr int V = 8;
     constexpr bool ROTATED = rot_kind(ROT) != H3S_ROT_NONE;
@@ -561,7 +563,7 @@ void quant_wave_kernel(QuantArgs A) {
     constexpr bool TAB = F & ROW_TAB;
     constexpr int TDT = (F & ROW_TAB32) ? H3S_F32 : H3S_BF16;
     constexpr int WOFF = 0, SOFF = HASW ? WPR * CPL * 512 : 0, HOFF = SOFF + WPR * CPL * 512;   // float offsets in side
-    constexpr int NW = quant_wave_nw(F, WPR), RPB = NW / WPR;
+    constexpr int RPB = NW / WPR;
     // NCH chunks a row; PAIR: slot pair p of wavefront s holds run pair k = WPR p + s (chunks 128 k + [0, 128))
     static_assert(!NORM || (NCH >= 256 && NCH <= 1024), "quant_wave_kernel: the norm's canonical order of 256 lanes");
     extern __shared__ __align__(16) float side[];
@@ -571,7 +573,7 @@ void quant_wave_kernel(QuantArgs A) {
     const int wave = (int) wave_uniform(threadIdx.x >> 6);
     const int ws = wave % WPR, wr = wave / WPR;             // this wavefront's share of its row, and the row's group
     const int64_t C = (int64_t) NCH * V;                     // the launch checks A.C against this
-    const int64_t b0 = (int64_t) blockIdx.x * RPB, U = (int64_t) gridDim.x * RPB, M = A.M;
+    const int64_t b0 = row0 + blk * RPB, U = (int64_t) gridDim.x * RPB, M = A.M;   // (U: grid-strided, row0 0)
     if (b0 >= M) return;                                    // the whole block
     // chunk slot j: chunk 64 (WPR j + ws) + pos, pos = the lane (swap3 of the lane for the Sylvester rotation, whose
     // stage 4 chunks apart then pairs lanes 7 apart: one DPP operand instead of two; and for pairs, whose digit of
@@ -701,7 +703,7 @@ void quant_wave_kernel(QuantArgs A) {
                 if (valid(j)) {
                     // (two wavefronts a row: a wavefront's run pairs all have k % 2 = its share s; one chunk a lane,
                     // slot j of wavefront s is canonical wavefront (2 j + s) % 4, its partial j % 2)
-                    const int q = PAIR ? (WPR == 2 ? (j & 1) : ((j / 2) % 2) * 2 + (j & 1)) : WPR == 2 ? j % 2 : j % 4;
+                    const int q = PAIR ? (WPR == 2 ? (j & 1) : ((j / 2) % 2) * 2 + (j & 1)) : WPR == 4 ? 0 : WPR == 2 ? j % 2 : j % 4;
 #pragma unroll
                     for (int e = 0; e < V; ++e) ss[q] = __builtin_fmaf(v[j][e], v[j][e], ss[q]);
                 }
@@ -715,6 +717,14 @@ void quant_wave_kernel(QuantArgs A) {
                 lds_barrier();
                 const int b = wr * 2;
                 tot = (wsum[b][0] + wsum[b + 1][0]) + (wsum[b][1] + wsum[b + 1][1]);
+            } else if constexpr (WPR == 4) {
+                // wavefront s holds canonical wavefront s (its slots j are chunks 64 (4 j + s) + pos): they meet in
+                // LDS for (w0 + w2) + (w1 + w3)
+                const float w = wave_sum<64, SW>(ss[0]);
+                if (lane == 0) wsum[wave][0] = w;
+                lds_barrier();
+                const int b = wr * 4;
+                tot = (wsum[b][0] + wsum[b + 2][0]) + (wsum[b + 1][0] + wsum[b + 3][0]);
             } else if constexpr (WPR == 2) {
                 // wavefront s holds canonical wavefronts s (ss[0]) and s + 2 (ss[1]): w0 + w2 in the first, w1 + w3
                 // in the second, met in LDS
@@ -883,6 +893,24 @@ void quant_wave_kernel(QuantArgs A) {
     }
 }
 
+// TAIL > 1: the blocks from tail_blk0 on take the rows from tail_row0 on with TAIL wavefronts a row (CPL / TAIL
+// slots each, the same chunks and the same arithmetic and order), so the launch's last rows, which run on a
+// partly idle device, end sooner.
+template <int XDT, int CPL, int ROT, int F, bool ONE, int NCH, int WPR = 1, bool PAIR = false, int TAIL = 1>
+__global__ __launch_bounds__(512)
+__attribute__((amdgpu_waves_per_eu((F & ROW_TAB) && rot_kind(ROT) == H3S_ROT_NONE && CPL <= 8 ? 4 : 1)))
+void quant_wave_kernel(QuantArgs A, int64_t tail_blk0, int64_t tail_row0) {
+    constexpr int NW = quant_wave_nw(F, WPR);
+    if constexpr (TAIL > 1) {
+        static_assert(ONE && WPR == 1 && !PAIR && CPL % TAIL == 0, "quant_wave_kernel: a tail of one-wavefront rows");
+        if ((int64_t) blockIdx.x >= tail_blk0) {
+            quant_wave_body<XDT, CPL / TAIL, ROT, F, true, NCH, TAIL, PAIR, NW>(A, (int64_t) blockIdx.x - tail_blk0, tail_row0);
+            return;
+        }
+    }
+    quant_wave_body<XDT, CPL, ROT, F, ONE, NCH, WPR, PAIR, NW>(A, blockIdx.x, 0);
+}
+
 // The side-input masks compiled exactly for 16-bit inputs: none (h3s_int8_linear's quantizer), the weight
 // (configs 1 and 4), the weight with 16-bit or float32 tables (config 5's front pass, the DiT's AdaLN). Every other
 // call shape runs the ROW_DYN instantiation.
@@ -891,7 +919,7 @@ constexpr int kQuantNone = 0, kQuantW = ROW_W, kQuantWTab = ROW_W | ROW_TAB, kQu
 
 // The launch of quant_wave_kernel: blocks of 4 wavefronts (8 with tables, so one LDS copy of the side values
 // serves more rows, or with several wavefronts a row).
-template <int XDT, int CPL, int ROT, int F, int NCH, int WPR, bool PAIR = false>
+template <int XDT, int CPL, int ROT, int F, int NCH, int WPR, bool PAIR = false, int TAIL = 1>
 int quant_wave_one(Ctx* c, const char* fn, const QuantArgs& A) {
     constexpr int NW = quant_wave_nw(F, WPR), RPB = NW / WPR;
     const int threads = 64 * NW;
@@ -905,19 +933,35 @@ int quant_wave_one(Ctx* c, const char* fn, const QuantArgs& A) {
         if (A.rows) {
             const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, false, NCH, WPR, PAIR>;
             const int64_t blocks = std::min<int64_t>((int64_t) c->cus * blocks_per_cu(k, threads, lds), rows_blocks);
-            quant_wave_kernel<XDT, CPL, ROT, F, false, NCH, WPR, PAIR><<<(unsigned) blocks, threads, lds, c->stream>>>(A);
+            quant_wave_kernel<XDT, CPL, ROT, F, false, NCH, WPR, PAIR><<<(unsigned) blocks, threads, lds, c->stream>>>(A, blocks, A.M);
             return launched(fn);
         }
     }
-    quant_wave_kernel<XDT, CPL, ROT, F, true, NCH, WPR, PAIR><<<(unsigned) rows_blocks, threads, lds, c->stream>>>(A);
+    // With a tail form: the blocks that fill whole rounds of the device take one row a wavefront, and the rows of
+    // a last round at most a quarter full TAIL wavefronts a row (config 4 at 16896 rows, 0.125 of a round: 43.4
+    // against 44.3 us, config 5a 41.2 against 42.1; at 47104 rows, half a round, the tail form measured 4 % slower)
+    int64_t main_blocks = rows_blocks, tail_blocks = 0;
+    if constexpr (TAIL > 1) {
+        const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, true, NCH, WPR, PAIR, TAIL>;
+        const int64_t round = (int64_t) c->cus * blocks_per_cu(k, threads, lds);
+        const int64_t full = rows_blocks / round * round;
+        if (full > 0 && full < rows_blocks && 4 * (rows_blocks - full) <= round) {
+            main_blocks = full;
+            tail_blocks = (A.M - full * RPB + (NW / TAIL) - 1) / (NW / TAIL);
+        }
+    }
+    quant_wave_kernel<XDT, CPL, ROT, F, true, NCH, WPR, PAIR, TAIL>
+        <<<(unsigned) (main_blocks + tail_blocks), threads, lds, c->stream>>>(A, main_blocks, main_blocks * RPB);
     return launched(fn);
 }
-// rows of 2048 or 4096 features (CPL 4 or 8, every slot whole): the norm with its side inputs, or the quantizer on x
+// rows of 2048 or 4096 features (CPL 4 or 8, every slot whole): the norm with its side inputs, or the quantizer on x;
+// at 4096 features the norm's launches end with the last partial round four wavefronts a row
 template <int XDT, int CPL> int quant_wave_launch(Ctx* c, const char* fn, const QuantArgs& A, int f) {
+    constexpr int TL = CPL == 8 ? 4 : 1;
 #define H3_QW(RR)                                                                                  \
     if (f == kQuantNone) return quant_wave_one<XDT, CPL, RR, kQuantNone, 64 * CPL, 1>(c, fn, A);     \
-    if (f == kQuantW) return quant_wave_one<XDT, CPL, RR, kQuantW, 64 * CPL, 1>(c, fn, A);           \
-    if (f == kQuantWTab) return quant_wave_one<XDT, CPL, RR, kQuantWTab, 64 * CPL, 1>(c, fn, A);     \
+    if (f == kQuantW) return quant_wave_one<XDT, CPL, RR, kQuantW, 64 * CPL, 1, false, TL>(c, fn, A);     \
+    if (f == kQuantWTab) return quant_wave_one<XDT, CPL, RR, kQuantWTab, 64 * CPL, 1, false, TL>(c, fn, A); \
     if (f == kQuantWTab32) return quant_wave_one<XDT, CPL, RR, kQuantWTab32, 64 * CPL, 1>(c, fn, A); \
     return quant_wave_one<XDT, CPL, RR, kQuantRaw, 64 * CPL, 1>(c, fn, A);
     if (A.rot == H3S_ROT_SYLVESTER && A.group == 128) { H3_QW(rot_with(H3S_ROT_SYLVESTER, 128)) }

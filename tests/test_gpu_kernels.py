@@ -407,6 +407,48 @@ def test_norm_quant_full_size(dev, config):
     codes_close(gq[rows], want_q, "codes")
 
 
+@pytest.mark.parametrize("config", ["4", "5a"])
+@pytest.mark.parametrize("M", [100, 96, 8])
+def test_norm_quant_tail_rows(config, M):
+    """Configs 4 and 5a end their launch with a last round at most a quarter full four wavefronts a row: on a
+    context that sizes its grids for 2 compute units (H3S_CUS=2) the one-wavefront layout takes M = 100 rows as 96
+    in whole rounds and 4 in the tail form (96: whole rounds only; 8: less than a round, one form), each bit for bit
+    the oracle's."""
+    import os
+    from sycl_minimax_h3_amd import Device
+
+    old = {k: os.environ.get(k) for k in ("H3S_CUS", "H3S_QUANT_WAVE_MIN_ROWS")}
+    os.environ.update({"H3S_CUS": "2", "H3S_QUANT_WAVE_MIN_ROWS": "0"})
+    try:
+        dev = Device.open()
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+    try:
+        C = 4096
+        rng = np.random.default_rng(74 + M)
+        heavy = np.where(rng.random(C) < 0.01, 20.0, 1.0).astype(np.float32) if config == "4" else np.ones(C, np.float32)
+        x = o.to_bf16(rng.standard_normal((M, C), dtype=np.float32) * heavy).ravel()
+        w = weight(75, C)
+        if config == "4":
+            tb, sc, sh, rot, group = None, None, None, o.ROT_SYLVESTER, 128
+        else:
+            sc = o.to_bf16((0.5 * rng.standard_normal(C)).astype(np.float32))
+            sh = o.to_bf16((0.5 * rng.standard_normal(C)).astype(np.float32))
+            tb, rot, group = ops.Tables(scale=up(dev, sc, "BF16", [1, C]), shift=up(dev, sh, "BF16", [1, C])), o.ROT_NONE, 0
+        q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+        ops.norm_quant(up(dev, x, "BF16", [M, C]), up(dev, w, "F32", [C]), 1e-6, tb, q, s, rot=rot, group=group,
+                       h_dtype=DType.BF16)
+        want_q, want_s = o.norm_quant(x, o.BF16, M, C, w, 1e-6, None, sc, sh, o.BF16, o.BF16, rot=rot, group=group)
+        assert_bits_equal(s.to_numpy(), want_s, "scales")
+        codes_close(q.to_numpy(), want_q, "codes")
+    finally:
+        dev.close()
+
+
 # ---- h3s_swiglu_quant: swiglu -> the MLP's act scratch -> fc2's quantizer, in one pass ----
 @pytest.mark.parametrize("rot,group", [(o.ROT_NONE, 0), (o.ROT_REGULAR, 256), (o.ROT_REGULAR, 16), (o.ROT_SYLVESTER, 128)])
 @pytest.mark.parametrize("x_dt,h_dt", [(o.BF16, o.BF16), (o.F16, o.F16), (o.F32, o.F32), (o.F32, o.BF16), (o.BF16, o.F32)])
