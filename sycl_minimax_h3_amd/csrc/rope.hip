@@ -26,7 +26,9 @@ namespace h3 {
 constexpr int kRopeKU = 8;       // most units a wavefront takes (their loads in flight together)
 constexpr int kRopeArea = 512;   // floats of a wavefront's partner area: HPW heads of D <= CL V features
 
-template <int XDT, int CL, bool VX>
+// PURE: every wavefront's share lies inside one tensor (the launch checks it), so a wavefront holds one tensor's
+// weights and its units' addresses are one tensor's
+template <int XDT, int CL, bool VX, bool PURE>
 __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M, int H, int D, int64_t stride,
                                                    const float* __restrict__ w0, const float* __restrict__ w1, float eps,
                                                    const float* __restrict__ cs, int rot, int pshift) {
@@ -36,7 +38,7 @@ __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M
     static_assert(HPW * CL == kWave, "rope_kernel: CL divides 64");
     __shared__ __align__(16) float part_all[4][2][kRopeArea];   // each wavefront's partner areas, by unit parity
     __shared__ __align__(16) float cs_all[4][kRopeArea];        // each wavefront's (cos, sin) row
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wv = (int) wave_uniform(threadIdx.x >> 6);
     const int64_t wid = (int64_t) blockIdx.x * 4 + wv, tok = wid >> pshift;
     if (tok >= M) return;                       // whole wavefronts: nothing below synchronizes the block
     const int part = (int) (wid & ((1 << pshift) - 1));
@@ -45,14 +47,23 @@ __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M
     const bool chunk = c < DC;
     const int f0 = c * V;                       // the lane's first feature inside its head
 
+    // ---- this wavefront's share of the token's units (tensor, group of HPW heads), all uniform ----
+    const int ngroups = (H + HPW - 1) / HPW, nunits = (x1 ? 2 : 1) * ngroups;
+    const int ubeg = (part * nunits) >> pshift, per = (((part + 1) * nunits) >> pshift) - ubeg;
+    const int t0 = ubeg / ngroups, g0 = ubeg - t0 * ngroups;
+
     // ---- the token's (cos, sin) pairs into LDS, then each element's: cos, and sin signed for its side ----
     float* csl = cs_all[wv];
     const float* ct = cs + tok * (int64_t) rot;               // [half] pairs: rot floats, 8-byte aligned
     for (int i = lane; i < half; i += kWave) *reinterpret_cast<float2*>(csl + 2 * i) = *reinterpret_cast<const float2*>(ct + 2 * i);
-    // the weights of both tensors for this lane's features (pass-through and idle lanes: unused)
+    // the weights for this lane's features (pass-through and idle lanes: unused): the share's tensor's, or both
     float wa[2][V];
-    load_f32x(w0 + (chunk ? f0 : 0), wa[0], V);
-    if (x1) load_f32x(w1 + (chunk ? f0 : 0), wa[1], V);
+    if constexpr (PURE) {
+        load_f32x((t0 ? w1 : w0) + (chunk ? f0 : 0), wa[0], V);
+    } else {
+        load_f32x(w0 + (chunk ? f0 : 0), wa[0], V);
+        if (x1) load_f32x(w1 + (chunk ? f0 : 0), wa[1], V);
+    }
     int pofs[V];                                // the partner's feature (its own for a pass-through element)
     bool pass[V];
 #pragma unroll
@@ -76,35 +87,44 @@ __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M
         }
     }
 
-    // ---- this wavefront's units, every load in flight before the first is used ----
-    const int ngroups = (H + HPW - 1) / HPW, nunits = (x1 ? 2 : 1) * ngroups;
-    const int ubeg = (part * nunits) >> pshift, per = (((part + 1) * nunits) >> pshift) - ubeg;
+    // ---- the units, every load in flight before the first is used. Unit k of the share: tensor tk, group gk (the
+    // groups counted on from g0, wrapping into the next tensor); its heads start at a wave-uniform address, and a lane
+    // adds its own 32-bit offset. Units past the share read the share's last unit again, and lanes past the heads
+    // or the head's chunks read the unit's first chunk: every load is to a valid place and none is branched around;
+    // their values are never stored. ----
+    const uint32_t lofs = (uint32_t) ((hh * D + f0) * ES);
+    auto unit = [&](int k, int& t, int& g) {
+        g = g0 + k;
+        t = t0;
+        if (g >= ngroups) { g -= ngroups; ++t; }
+    };
+    auto unit_base = [&](int t, int g) {
+        return (char*) (t ? x1 : x0) + (tok * stride + (int64_t) g * HPW * D) * ES;
+    };
     uint4 raw[kRopeKU];
 #pragma unroll
     for (int k = 0; k < kRopeKU; ++k) {
-        // units past the share read the share's last unit again, and lanes past the heads read head 0: every load
-        // is to a valid place and none is branched around; their values are never stored
-        const int u = ubeg + (k < per ? k : per - 1), t = u / ngroups, h0 = (u % ngroups) * HPW + hh;
-        const int head = chunk && h0 < H ? h0 : 0;
-        const char* base = (const char*) (t ? x1 : x0) + (tok * stride + (int64_t) head * D) * ES;
-        raw[k] = ld_nt(base + (chunk ? f0 : 0) * ES);
+        int t, g;
+        unit(k < per ? k : per - 1, t, g);
+        const bool ok = chunk && g * HPW + hh < H;
+        raw[k] = ld_nt(unit_base(t, g) + (ok ? lofs : 0u));
     }
 #pragma unroll
     for (int k = 0; k < kRopeKU; ++k) {
         if (k >= per) break;                    // uniform across the wavefront
-        const int u = ubeg + k, t = u / ngroups, head = (u % ngroups) * HPW + hh;
-        const bool ok = chunk && head < H;
+        int t, g;
+        unit(k, t, g);
+        const bool ok = chunk && g * HPW + hh < H;
         float a[V];
         Vec<XDT>::unpack(raw[k], a);
         float s = 0.0f;
-        if (ok)
 #pragma unroll
-            for (int e = 0; e < V; ++e) s = __builtin_fmaf(a[e], a[e], s);
-        s = wave_sum<CL>(s);
+        for (int e = 0; e < V; ++e) s = __builtin_fmaf(a[e], a[e], s);
+        s = wave_sum<CL>(ok ? s : 0.0f);
         const float inv = inv_root(s, (float) D, eps);
         float n[V], o[V];
 #pragma unroll
-        for (int e = 0; e < V; ++e) n[e] = a[e] * inv * (t ? wa[1][e] : wa[0][e]);
+        for (int e = 0; e < V; ++e) n[e] = a[e] * inv * (PURE || !t ? wa[0][e] : wa[1][e]);
         if (rot > 0) {
             float* area = part_all[wv][k & 1] + hh * D;
             if (chunk)
@@ -130,10 +150,7 @@ __global__ __launch_bounds__(256) void rope_kernel(void* x0, void* x1, int64_t M
 #pragma unroll
             for (int e = 0; e < V; ++e) o[e] = n[e];
         }
-        if (ok) {
-            char* base = (char*) (t ? x1 : x0) + (tok * stride + (int64_t) head * D) * ES;
-            st_nt(base + f0 * ES, Vec<XDT>::pack(o));
-        }
+        if (ok) st_nt(unit_base(t, g) + lofs, Vec<XDT>::pack(o));
     }
 }
 
@@ -167,11 +184,16 @@ static int rope_launch(const char* fn, void* ctx, void* x0, void* x1, int x_dt, 
     while ((nunits + (1 << pshift) - 1) >> pshift > kRopeKU) ++pshift;
     if (pshift > 10 || M > (((int64_t) 1 << 31) >> pshift)) return fail(std::string(fn) + ": too many heads a token");
     const bool vx = half % 4 == 0;
+    // every wavefront's share inside one tensor: one tensor, or the shares divide each tensor's groups
+    const int64_t ngroups = (H + kWave / CL - 1) / (kWave / CL);
+    const bool pure = !x1 || (nunits % ((int64_t) 1 << pshift) == 0 && ngroups % (nunits >> pshift) == 0);
     const unsigned grid = (unsigned) (((M << pshift) + 3) / 4);
 #define LPV(XDT, CC)                                                                                              \
     {                                                                                                              \
-        if (vx) rope_kernel<XDT, CC, true><<<grid, 256, 0, c->stream>>>(x0, x1, M, (int) H, (int) D, stride, w0, w1, eps, cs, rot_dim, pshift); \
-        else rope_kernel<XDT, CC, false><<<grid, 256, 0, c->stream>>>(x0, x1, M, (int) H, (int) D, stride, w0, w1, eps, cs, rot_dim, pshift); \
+        if (vx && pure) rope_kernel<XDT, CC, true, true><<<grid, 256, 0, c->stream>>>(x0, x1, M, (int) H, (int) D, stride, w0, w1, eps, cs, rot_dim, pshift); \
+        else if (vx) rope_kernel<XDT, CC, true, false><<<grid, 256, 0, c->stream>>>(x0, x1, M, (int) H, (int) D, stride, w0, w1, eps, cs, rot_dim, pshift); \
+        else if (pure) rope_kernel<XDT, CC, false, true><<<grid, 256, 0, c->stream>>>(x0, x1, M, (int) H, (int) D, stride, w0, w1, eps, cs, rot_dim, pshift); \
+        else rope_kernel<XDT, CC, false, false><<<grid, 256, 0, c->stream>>>(x0, x1, M, (int) H, (int) D, stride, w0, w1, eps, cs, rot_dim, pshift); \
     }
 #define LD(XDT)                          \
     switch (CL) {                        \
