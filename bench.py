@@ -7,7 +7,8 @@
 A step is one launch of the headline kernel over the whole batch: the AdaLN chain (LayerNorm without affine, then
 x * (1 + scale) + shift, GELU-tanh, out = res + gate * y) on X, res [16896 x 4096] bf16, token grid T16 x H24 x W44.
 ``value`` is its achieved HBM bandwidth: algorithmic bytes (X and res read once, out written once) divided by the
-median launch time (each launch timed between HIP events; the mean over the window is reported beside it).
+median launch time (the timed launches run back to back in up to 5 equal windows between HIP events: the median of the
+windows' times per launch; the mean over all of them is reported beside it).
 
 Cache-cold timing: MI355X's 256 MB Infinity Cache would hold part of a 415 MB working set launched back to back on
 the same buffers. Every workload of less than 1 GiB per launch is therefore timed over a ring of independent buffer
@@ -256,18 +257,23 @@ def main() -> int:
         if args.mark:
             torch.cuda._sleep(1)
             marked.append(key)
-        # an event before every launch and one after the last: each launch's time, and the window's
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-        for i in range(steps):
-            ev[i].record()
-            fn()
-        ev[steps].record()
+        # The launches back to back in up to 5 windows of equal length, an event at each window's edge: the median of
+        # the windows' times per launch, and the mean over all of them. (An event between every two launches puts its
+        # own gap, about 3 us, into every launch's time.)
+        nw = max(1, min(5, steps // 4))
+        edges = [round(i * steps / nw) for i in range(nw + 1)]
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(nw + 1)]
+        ev[0].record()
+        for w in range(nw):
+            for _ in range(edges[w + 1] - edges[w]):
+                fn()
+            ev[w + 1].record()
         if args.mark:
             torch.cuda._sleep(1)
         torch.cuda.synchronize()
-        each = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
-        means[key] = ev[0].elapsed_time(ev[steps]) / steps
-        return each[steps // 2] if steps % 2 else 0.5 * (each[steps // 2 - 1] + each[steps // 2])   # median ms
+        each = sorted(ev[w].elapsed_time(ev[w + 1]) / (edges[w + 1] - edges[w]) for w in range(nw))
+        means[key] = ev[0].elapsed_time(ev[nw]) / steps
+        return each[nw // 2] if nw % 2 else 0.5 * (each[nw // 2 - 1] + each[nw // 2])   # median ms a launch
 
     def cycle(fns):
         """one launch of the next buffer set of a ring"""
