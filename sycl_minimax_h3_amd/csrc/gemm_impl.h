@@ -127,6 +127,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
                 rw, (__attribute__((address_space(3))) void*) (st + kGemmBM * kGemmBK + (kGemmLoads * wave + q) * 1024), 16, vo[q], 0, 0, 0);
     };
 
+    // the epilogue's row and column scales, loaded now (three registers through the K steps) so that their latency
+    // is not waited for at the end
+    float sv = 0.0f, wv = 0.0f, bv = 0.0f;
+    if (tid < kGemmBM) {
+        const int64_t m = m0 + tid < P.M ? m0 + tid : P.M - 1, n = n0 + tid < P.N ? n0 + tid : P.N - 1;
+        sv = P.sA[m];
+        if constexpr (PER_N) wv = P.ws[n];
+        if (P.bias) bv = P.bias[n];
+    }
+
     v16i acc[kGemmWI][kGemmWJ];
 #pragma unroll
     for (int i = 0; i < kGemmWI; ++i)
@@ -239,10 +249,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
     float* wcol = srow + kGemmBM;                           // wscale[n] of its 256 columns
     float* bcol = wcol + kGemmBN;                           // bias[n]
     if (tid < kGemmBM) {
-        const int64_t m = m0 + tid < P.M ? m0 + tid : P.M - 1, n = n0 + tid < P.N ? n0 + tid : P.N - 1;
-        srow[tid] = P.sA[m];
-        wcol[tid] = PER_N ? P.ws[n] : 0.0f;
-        bcol[tid] = P.bias ? P.bias[n] : 0.0f;
+        srow[tid] = sv;
+        wcol[tid] = wv;
+        bcol[tid] = bv;
     }
     __syncthreads();
     auto epilogue = [&](auto out_tag, auto bias_tag) {
