@@ -63,11 +63,11 @@ struct GemmArgs {
 
 __device__ __forceinline__ int gemm_unit(int r, int c) { return (r << 3) | (c ^ ((r >> 1) & 7)); }
 
-// the tile of block b: XCD-contiguous renumbering, then 8-high groups of tiles
+// the tile of block b: XCD-contiguous renumbering (the blocks b % 8 = x, which XCD x runs, take the consecutive ids
+// x q + min(x, r) + b / 8, q = total / 8, r = total % 8: the first r XCDs one id more), then 8-high groups of tiles
 __device__ __forceinline__ void gemm_tile(int b, int tm, int tn, int* im, int* in) {
-    const int total = tm * tn;
-    int id = b;
-    if (total % 8 == 0) id = (b % 8) * (total / 8) + b / 8;
+    const int total = tm * tn, q = total / 8, r = total % 8, x = b % 8;
+    const int id = x * q + (x < r ? x : r) + b / 8;
     const int group = 8 * tn;
     const int first = (id / group) * 8;
     const int rows = tm - first < 8 ? tm - first : 8;
