@@ -537,19 +537,33 @@ template <int CPL, int WPR = 1> constexpr size_t quant_wave_side_bytes(int f) {
 }
 // wavefronts a block: 8 with tables (one LDS copy of the side values serves more rows) or two or four a row, a row's
 // own with more, else 4
-constexpr int quant_wave_nw(int f, int wpr) { return wpr > 4 || wpr == 3 ? wpr * (8 / wpr > 0 ? 8 / wpr : 1) : (f & ROW_TAB) || wpr > 1 ? 8 : 4; }
-// ONE: the grid has a wavefront (group) for every row, so each takes one row (108 registers for config 4's kernel,
-// four wavefronts a SIMD); else the grid strides over the rows, with nothing prefetched either: four wavefronts a
-// SIMD hide the loads (the registers of a prefetched next row would leave room for three). With tables and no
-// rotation (and at most 8 slots) the kernel is held to four wavefronts a SIMD (120 registers, no spills).
+enum : int { QW_ROUNDS = 0, QW_ONE = 1, QW_STREAM = 2 };
+constexpr int quant_wave_nw(int f, int wpr, int mode) {
+    // several wavefronts a row with no side values to share: a block is one row, so the blocks resident on a CU follow
+    // the registers (the 5376-feature quantizer, two wavefronts a row: 54.7 against 57.4 us at 16896 rows in blocks of
+    // four rows)
+    if (!(f & (ROW_W | ROW_TAB)) && wpr > 1 && mode == QW_ONE) return wpr;
+    return wpr > 4 || wpr == 3 ? wpr * (8 / wpr > 0 ? 8 / wpr : 1) : (f & ROW_TAB) || wpr > 1 ? 8 : 4;
+}
+// How a launch deals out its rows:
+//   QW_ONE     the grid has a wavefront (group) for every row, so each takes one row (108 registers for config 4's
+//              kernel, four wavefronts a SIMD);
+//   QW_ROUNDS  one wavefront a row, the grid strided over the rows with nothing prefetched (four wavefronts a SIMD
+//              hide the loads), a table row per token cached in LDS and refilled in rounds (below). With tables and no
+//              rotation (and at most 8 slots) the kernel is held to four wavefronts a SIMD (120 registers, no spills);
+//   QW_STREAM  as many blocks as the device holds, grid-strided, each group of wavefronts taking rows g, g + U, ...
+//              with nothing prefetched; the block's side values (the weight, one table row) are decoded into LDS once
+//              and refilled only when the table row of a step's first row changes (the norm at the hidden width: each
+//              block of four rows had decoded 63 KiB of float32 weight and tables).
 // The body of quant_wave_kernel for the blocks [blk0, ...) of one layout: block blk takes rows row0 + blk R ... (R rows
 // a block step); NW wavefronts a block.
-template <int XDT, int CPL, int ROT, int F, bool ONE, int NCH, int WPR, bool PAIR, int NW>
+template <int XDT, int CPL, int ROT, int F, int MODE, int NCH, int WPR, bool PAIR, int NW>
 __device__ __forceinline__ void quant_wave_body(const QuantArgs& A, int64_t blk, int64_t row0) {
+    constexpr bool ONE = MODE == QW_ONE;
     static_assert(XDT != H3S_F32 && !(F & ROW_DYN), "quant_wave_kernel: 16-bit x, exact side inputs");
     static_assert(PAIR ? NCH > 128 * WPR * (CPL / 2 - 1) && NCH <= 128 * WPR * (CPL / 2)
                        : NCH > 64 * WPR * (CPL - 1) && NCH <= 64 * WPR * CPL, "quant_wave_kernel: NCH reaches the last slots");
-    static_assert(WPR == 1 || (ONE && ((F & (ROW_RAW | ROW_SWIGLU)) || WPR == 2 || (WPR == 4 && !PAIR))),
+    static_assert(WPR == 1 || (MODE != QW_ROUNDS && ((F & (ROW_RAW | ROW_SWIGLU)) || WPR == 2 || (WPR == 4 && !PAIR))),
                   "quant_wave_kernel: several wavefronts a row: the quantizer on x or swiglu(x), or the norm, two a row "
                   "(four a row one chunk a lane)");
     static_assert(NW % WPR == 0, "quant_wave_kernel: whole rows a block");
@@ -639,12 +653,6 @@ __device__ __forceinline__ void quant_wave_body(const QuantArgs& A, int64_t blk,
             }
         }
     };
-    int64_t tcache = TAB && A.rows ? A.rows[b0] : 0;
-    if constexpr (HASW || TAB) {
-        fill(tcache, true);
-        lds_barrier();
-    }
-
     const int G = rot_fixed(ROT) ? rot_fixed(ROT) : A.group;
     const float cgs = rot_kind(ROT) == H3S_ROT_SYLVESTER ? A.cg * syl_sign<V>(pos, G) : A.cg;
     // a row's x: a base the whole wavefront shares (the row is the wavefront's) and a 32-bit unsigned byte offset
@@ -659,6 +667,12 @@ __device__ __forceinline__ void quant_wave_body(const QuantArgs& A, int64_t blk,
 #pragma unroll
             for (int j = 0; j < CPL; ++j) ur[j] = ld_nt(xp + (uint32_t) ((NCH + cc[j]) * 16));
     };
+    const int64_t M1 = M - 1;
+    int64_t tcache = TAB && A.rows ? A.rows[b0] : 0;
+    if constexpr (HASW || TAB) {
+        fill(tcache, true);
+        lds_barrier();
+    }
     // The table rows of each step's group of NW rows (rows g + [0, NW), g = b0 + k U, one a wavefront), 64 steps
     // at a time, one step a lane, taken out with readlane: the group's first row's (gix), this wavefront's (tix),
     // and a bit of uni set when the whole group shares one table row. rows[] is read once per 64 steps.
@@ -684,9 +698,7 @@ __device__ __forceinline__ void quant_wave_body(const QuantArgs& A, int64_t blk,
     // One row (its share), with the table row cached in LDS; live false: a row past the end (ONE with several
     // wavefronts a row), computed on a copy for the barrier and not stored.
     // tab_lds: the row's table row is the one cached in LDS (else its values are read from memory, chunk by chunk)
-    auto process = [&](int64_t row, bool live, bool tab_lds) {
-        uint4 x[CPL], u[CPL];
-        load_row(x, u, row);
+    auto compute = [&](const uint4 (&x)[CPL], const uint4 (&u)[CPL], int64_t row, bool live, bool tab_lds) {
         float v[CPL][V];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) Vec<XDT>::unpack(x[j], v[j]);
@@ -777,7 +789,7 @@ __device__ __forceinline__ void quant_wave_body(const QuantArgs& A, int64_t blk,
                     v[j][e + 1] = bf16_hi(p[e / 2]);
                 }
                 if constexpr (OUTH) {
-                    if (valid(j)) st_nt(hrow + (uint32_t) (cc[j] * 8), make_uint4(p[0], p[1], p[2], p[3]));
+                    if (live && valid(j)) st_nt(hrow + (uint32_t) (cc[j] * 8), make_uint4(p[0], p[1], p[2], p[3]));
                 }
                 // with tables, one chunk's LDS reads at a time: the registers stay within four wavefronts a SIMD
                 if constexpr (TAB) __builtin_amdgcn_sched_barrier(0);
@@ -802,6 +814,12 @@ __device__ __forceinline__ void quant_wave_body(const QuantArgs& A, int64_t blk,
         }
 
         // ---- the block rotation, then the row's absolute maximum ----
+        // P2: the regular rotation of a fixed group of 256, whose fl(1 / sqrt(256)) = 2^-4 is a power of two. The
+        // values are then left unscaled: y = v 2^-4 exactly, so y / s = v / (16 s) exactly, and code_of(v, 16 s,
+        // fl(1 / s) / 16) forms every intermediate 16 times that of code_of(y, s, fl(1 / s)) - the same roundings,
+        // the same bits - as long as no intermediate is subnormal. A row whose unscaled maximum is below 2^-60 (its
+        // codes' residuals could be) takes the scaled values as written.
+        constexpr bool P2 = rot_kind(ROT) == H3S_ROT_REGULAR && rot_fixed(ROT) == 256;
         float m = 0.0f;
         if constexpr (PAIR) {
 #pragma unroll
@@ -814,8 +832,9 @@ __device__ __forceinline__ void quant_wave_body(const QuantArgs& A, int64_t blk,
                     if constexpr (SW) sylvester<V, true>(v[j], pos, G);
                     else regular<V>(v[j], G);
                 }
+                if constexpr (!P2)
 #pragma unroll
-                for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * cgs;
+                    for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * cgs;
             }
             if (valid(j))
 #pragma unroll
@@ -829,22 +848,73 @@ __device__ __forceinline__ void quant_wave_body(const QuantArgs& A, int64_t blk,
 #pragma unroll
             for (int s = 0; s < WPR; ++s) m = fmaxf(m, wmax[wr * WPR + s]);
         }
+        bool unscaled = false;
+        if constexpr (P2) {
+            // the maximum of the scaled values, fl(max |v| 2^-4) (rounding is monotonic)
+            unscaled = m >= 0x1p-60f;
+            if (!unscaled) {
+#pragma unroll
+                for (int j = 0; j < CPL; ++j)
+#pragma unroll
+                    for (int e = 0; e < V; ++e) v[j][e] = v[j][e] * cgs;
+            }
+            m = m * cgs;
+        }
         const float sc = fmaxf(m / 127.0f, 1e-30f), r = 1.0f / sc;
         if (!live) return;
         if (lane == 0 && ws == 0) A.s[row] = sc;
+        const float sq = unscaled ? sc * 16.0f : sc, rq = unscaled ? r * 0.0625f : r;   // the codes' divisor
 
-        // ---- the codes, 8 bytes a chunk ----
+        // ---- the codes, 8 bytes a chunk; a lane's run pair (two consecutive chunks) as one 16-byte store, so each
+        // store instruction writes whole lines (two 8-byte halves 16 bytes apart wrote up to 17 % more bytes) ----
         int8_t* qrow = A.q + wave_uniform(row) * C;
+        auto codes8 = [&](const float* o) {
+            return make_uint2(bytes4(code_of(o[0], sq, rq), code_of(o[1], sq, rq), code_of(o[2], sq, rq), code_of(o[3], sq, rq)),
+                              bytes4(code_of(o[4], sq, rq), code_of(o[5], sq, rq), code_of(o[6], sq, rq), code_of(o[7], sq, rq)));
+        };
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            if (!valid(j)) continue;
-            const float* o = v[j];
-            const uint32_t lo = bytes4(code_of(o[0], sc, r), code_of(o[1], sc, r), code_of(o[2], sc, r), code_of(o[3], sc, r));
-            const uint32_t hi = bytes4(code_of(o[4], sc, r), code_of(o[5], sc, r), code_of(o[6], sc, r), code_of(o[7], sc, r));
-            st_nt(qrow + (uint32_t) (cc[j] * 8), make_uint2(lo, hi));
+        for (int j = 0; j < CPL; j += PAIR ? 2 : 1) {
+            if (!valid(j)) continue;                      // (a pair's two chunks are inside the row or past it together)
+            const uint2 a = codes8(v[j]);
+            if constexpr (PAIR) {
+                const uint2 b = codes8(v[j + 1]);
+                st_nt(qrow + (uint32_t) (cc[j] * 8), make_uint4(a.x, a.y, b.x, b.y));
+            } else {
+                st_nt(qrow + (uint32_t) (cc[j] * 8), a);
+            }
         }
     };
+    auto process = [&](int64_t row, bool live, bool tab_lds) {
+        uint4 x[CPL], u[CPL];
+        load_row(x, u, row);
+        compute(x, u, row, live, tab_lds);
+    };
     int64_t row = b0 + wr;
+    if constexpr (MODE == QW_STREAM) {
+        // Steps g = b0, b0 + U, ...: this group's row g + wr. Every wavefront of the block takes every step (a row past
+        // the end is computed on a copy and not stored), so the row barriers and the refills below match. The block's
+        // cached table row is that of the step's first row (a uniform value): a step whose first row has another one
+        // refills the cache between two barriers; a row whose table row differs from the cached one (a segment
+        // boundary of rows[] inside the step) reads its table values from memory.
+        for (int64_t g = b0; g < M; g += U) {
+            const int64_t rc = g + wr < M ? g + wr : M1;
+            bool tab_lds = true;
+            if constexpr (TAB) {
+                if (A.rows) {
+                    const int64_t tg = A.rows[g];
+                    if (tg != tcache) {
+                        lds_barrier();                    // every wavefront is done with the cached row
+                        fill(tg, false);
+                        lds_barrier();
+                        tcache = tg;
+                    }
+                    tab_lds = A.rows[rc] == tcache;
+                }
+            }
+            process(rc, g + wr < M, tab_lds);
+        }
+        return;
+    }
     if constexpr (ONE) {
         // the block's side values hold the table row of its first row; a row of another table row (one a segment
         // boundary of rows[] puts in the block) reads its table values from memory
@@ -896,19 +966,20 @@ __device__ __forceinline__ void quant_wave_body(const QuantArgs& A, int64_t blk,
 // TAIL > 1: the blocks from tail_blk0 on take the rows from tail_row0 on with TAIL wavefronts a row (CPL / TAIL
 // slots each, the same chunks and the same arithmetic and order), so the launch's last rows, which run on a
 // partly idle device, end sooner.
-template <int XDT, int CPL, int ROT, int F, bool ONE, int NCH, int WPR = 1, bool PAIR = false, int TAIL = 1>
+template <int XDT, int CPL, int ROT, int F, int MODE, int NCH, int WPR = 1, bool PAIR = false, int TAIL = 1>
 __global__ __launch_bounds__(512)
-__attribute__((amdgpu_waves_per_eu((F & ROW_TAB) && rot_kind(ROT) == H3S_ROT_NONE && CPL <= 8 ? 4 : 1)))
+__attribute__((amdgpu_waves_per_eu((F & ROW_TAB) && rot_kind(ROT) == H3S_ROT_NONE && CPL <= 8 && MODE == QW_ROUNDS ? 4 : 1)))
 void quant_wave_kernel(QuantArgs A, int64_t tail_blk0, int64_t tail_row0) {
-    constexpr int NW = quant_wave_nw(F, WPR);
+    constexpr int NW = quant_wave_nw(F, WPR, MODE);
+    static_assert(NW * 64 <= 512, "quant_wave_kernel: a block within the launch bound");
     if constexpr (TAIL > 1) {
-        static_assert(ONE && WPR == 1 && !PAIR && CPL % TAIL == 0, "quant_wave_kernel: a tail of one-wavefront rows");
+        static_assert(MODE == QW_ONE && WPR == 1 && !PAIR && CPL % TAIL == 0, "quant_wave_kernel: a tail of one-wavefront rows");
         if ((int64_t) blockIdx.x >= tail_blk0) {
-            quant_wave_body<XDT, CPL / TAIL, ROT, F, true, NCH, TAIL, PAIR, NW>(A, (int64_t) blockIdx.x - tail_blk0, tail_row0);
+            quant_wave_body<XDT, CPL / TAIL, ROT, F, QW_ONE, NCH, TAIL, PAIR, NW>(A, (int64_t) blockIdx.x - tail_blk0, tail_row0);
             return;
         }
     }
-    quant_wave_body<XDT, CPL, ROT, F, ONE, NCH, WPR, PAIR, NW>(A, blockIdx.x, 0);
+    quant_wave_body<XDT, CPL, ROT, F, MODE, NCH, WPR, PAIR, NW>(A, blockIdx.x, 0);
 }
 
 // The side-input masks compiled exactly for 16-bit inputs: none (h3s_int8_linear's quantizer), the weight
@@ -919,21 +990,28 @@ constexpr int kQuantNone = 0, kQuantW = ROW_W, kQuantWTab = ROW_W | ROW_TAB, kQu
 
 // The launch of quant_wave_kernel: blocks of 4 wavefronts (8 with tables, so one LDS copy of the side values
 // serves more rows, or with several wavefronts a row).
-template <int XDT, int CPL, int ROT, int F, int NCH, int WPR, bool PAIR = false, int TAIL = 1>
+template <int XDT, int CPL, int ROT, int F, int NCH, int WPR, bool PAIR = false, int TAIL = 1, int MODE = QW_ONE>
 int quant_wave_one(Ctx* c, const char* fn, const QuantArgs& A) {
-    constexpr int NW = quant_wave_nw(F, WPR), RPB = NW / WPR;
+    constexpr int NW = quant_wave_nw(F, WPR, MODE), RPB = NW / WPR;
     const int threads = 64 * NW;
     const size_t lds = quant_wave_side_bytes<CPL, WPR>(F);
     const int64_t rows_blocks = (A.M + RPB - 1) / RPB;
+    if constexpr (MODE == QW_STREAM) {
+        const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, MODE, NCH, WPR, PAIR>;
+        const int64_t blocks = std::min<int64_t>((int64_t) c->cus * blocks_per_cu(k, threads, lds), rows_blocks);
+        if (blocks < 1) return fail(std::string(fn) + ": the streamed row kernel fits no compute unit");
+        quant_wave_kernel<XDT, CPL, ROT, F, MODE, NCH, WPR, PAIR><<<(unsigned) blocks, threads, lds, c->stream>>>(A, blocks, A.M);
+        return launched(fn);
+    } else {
     // One row a wavefront, nothing prefetched (config 4 at 47104 rows: 106 us, against 119 us grid-strided with the
     // next row in flight): without tables, and with tables whose one row serves every token (rows NULL), each block
     // decoding its side values once. With a table row per token, as many blocks as the device holds, grid-strided,
     // each refilling its cached table row when the rows' table row changes.
     if constexpr ((F & ROW_TAB) && WPR == 1) {
         if (A.rows) {
-            const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, false, NCH, WPR, PAIR>;
+            const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, QW_ROUNDS, NCH, WPR, PAIR>;
             const int64_t blocks = std::min<int64_t>((int64_t) c->cus * blocks_per_cu(k, threads, lds), rows_blocks);
-            quant_wave_kernel<XDT, CPL, ROT, F, false, NCH, WPR, PAIR><<<(unsigned) blocks, threads, lds, c->stream>>>(A, blocks, A.M);
+            quant_wave_kernel<XDT, CPL, ROT, F, QW_ROUNDS, NCH, WPR, PAIR><<<(unsigned) blocks, threads, lds, c->stream>>>(A, blocks, A.M);
             return launched(fn);
         }
     }
@@ -942,7 +1020,7 @@ int quant_wave_one(Ctx* c, const char* fn, const QuantArgs& A) {
     // against 44.3 us, config 5a 41.2 against 42.1; at 47104 rows, half a round, the tail form measured 4 % slower)
     int64_t main_blocks = rows_blocks, tail_blocks = 0;
     if constexpr (TAIL > 1) {
-        const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, true, NCH, WPR, PAIR, TAIL>;
+        const void* k = (const void*) quant_wave_kernel<XDT, CPL, ROT, F, QW_ONE, NCH, WPR, PAIR, TAIL>;
         const int64_t round = (int64_t) c->cus * blocks_per_cu(k, threads, lds);
         const int64_t full = rows_blocks / round * round;
         if (full > 0 && full < rows_blocks && 4 * (rows_blocks - full) <= round) {
@@ -950,9 +1028,10 @@ int quant_wave_one(Ctx* c, const char* fn, const QuantArgs& A) {
             tail_blocks = (A.M - full * RPB + (NW / TAIL) - 1) / (NW / TAIL);
         }
     }
-    quant_wave_kernel<XDT, CPL, ROT, F, true, NCH, WPR, PAIR, TAIL>
+    quant_wave_kernel<XDT, CPL, ROT, F, QW_ONE, NCH, WPR, PAIR, TAIL>
         <<<(unsigned) (main_blocks + tail_blocks), threads, lds, c->stream>>>(A, main_blocks, main_blocks * RPB);
     return launched(fn);
+    }
 }
 // rows of 2048 or 4096 features (CPL 4 or 8, every slot whole): the norm with its side inputs, or the quantizer on x;
 // at 4096 features the norm's launches end with the last partial round four wavefronts a row
@@ -988,28 +1067,30 @@ template <int XDT, int CPL> int quant_wave_launch(Ctx* c, const char* fn, const 
 template <int XDT> int quant_wave_model(Ctx* c, const char* fn, const QuantArgs& A, int f) {
     const bool reg256 = A.rot == H3S_ROT_REGULAR && A.group == 256, none = A.rot == H3S_ROT_NONE;
     constexpr int R256 = rot_with(H3S_ROT_REGULAR, 256), R0 = H3S_ROT_NONE;
+    // the norm (with its side values in LDS) streamed; the quantizers on x or swiglu(x) one row a group
+    constexpr int MN = QW_STREAM, MR = QW_ONE;
     if (A.C == 5376) {
         constexpr int N = 672;
-        if (f == (kQuantW | ROW_OUTH)) return quant_wave_one<XDT, 6, R0, kQuantW | ROW_OUTH, N, 2>(c, fn, A);
-        if (f == (kQuantWTab32 | ROW_OUTH)) return quant_wave_one<XDT, 6, R0, kQuantWTab32 | ROW_OUTH, N, 2>(c, fn, A);
-        if (f == kQuantWTab32 && reg256) return quant_wave_one<XDT, 6, R256, kQuantWTab32, N, 2, true>(c, fn, A);
-        if (f == kQuantWTab32 && none) return quant_wave_one<XDT, 6, R0, kQuantWTab32, N, 2>(c, fn, A);
-        if (f == kQuantW && reg256) return quant_wave_one<XDT, 6, R256, kQuantW, N, 2, true>(c, fn, A);
-        if (f == kQuantW && none) return quant_wave_one<XDT, 6, R0, kQuantW, N, 2>(c, fn, A);
-        if (f == kQuantRaw && reg256) return quant_wave_one<XDT, 6, R256, kQuantRaw, N, 2, true>(c, fn, A);
-        if (f == kQuantRaw && none) return quant_wave_one<XDT, 11, R0, kQuantRaw, N, 1>(c, fn, A);
+        if (f == (kQuantW | ROW_OUTH)) return quant_wave_one<XDT, 6, R0, kQuantW | ROW_OUTH, N, 2, false, 1, MN>(c, fn, A);
+        if (f == (kQuantWTab32 | ROW_OUTH)) return quant_wave_one<XDT, 6, R0, kQuantWTab32 | ROW_OUTH, N, 2, false, 1, MN>(c, fn, A);
+        if (f == kQuantWTab32 && reg256) return quant_wave_one<XDT, 6, R256, kQuantWTab32, N, 2, true, 1, MN>(c, fn, A);
+        if (f == kQuantWTab32 && none) return quant_wave_one<XDT, 6, R0, kQuantWTab32, N, 2, false, 1, MN>(c, fn, A);
+        if (f == kQuantW && reg256) return quant_wave_one<XDT, 6, R256, kQuantW, N, 2, true, 1, MN>(c, fn, A);
+        if (f == kQuantW && none) return quant_wave_one<XDT, 6, R0, kQuantW, N, 2, false, 1, MN>(c, fn, A);
+        if (f == kQuantRaw && reg256) return quant_wave_one<XDT, 6, R256, kQuantRaw, N, 2, true, 1, MR>(c, fn, A);
+        if (f == kQuantRaw && none) return quant_wave_one<XDT, 11, R0, kQuantRaw, N, 1, false, 1, MR>(c, fn, A);
     }
     if (A.C == 7168 && f == kQuantRaw) {
-        if (reg256) return quant_wave_one<XDT, 2, R256, kQuantRaw, 896, 7, true>(c, fn, A);
-        if (none) return quant_wave_one<XDT, 7, R0, kQuantRaw, 896, 2>(c, fn, A);
+        if (reg256) return quant_wave_one<XDT, 2, R256, kQuantRaw, 896, 7, true, 1, MR>(c, fn, A);
+        if (none) return quant_wave_one<XDT, 7, R0, kQuantRaw, 896, 2, false, 1, MR>(c, fn, A);
     }
-    if (A.C == 4096 && f == kQuantRaw && reg256) return quant_wave_one<XDT, 4, R256, kQuantRaw, 512, 2, true>(c, fn, A);
-    if (A.C == 8192 && f == kQuantSwiglu && reg256) return quant_wave_one<XDT, 4, R256, kQuantSwiglu, 1024, 4, true>(c, fn, A);
+    if (A.C == 4096 && f == kQuantRaw && reg256) return quant_wave_one<XDT, 4, R256, kQuantRaw, 512, 2, true, 1, MR>(c, fn, A);
+    if (A.C == 8192 && f == kQuantSwiglu && reg256) return quant_wave_one<XDT, 4, R256, kQuantSwiglu, 1024, 4, true, 1, MR>(c, fn, A);
     if (A.C == 14336) {
-        if (f == kQuantRaw && reg256) return quant_wave_one<XDT, 4, R256, kQuantRaw, 1792, 7, true>(c, fn, A);
-        if (f == kQuantRaw && none) return quant_wave_one<XDT, 7, R0, kQuantRaw, 1792, 4>(c, fn, A);
-        if (f == kQuantSwiglu && reg256) return quant_wave_one<XDT, 4, R256, kQuantSwiglu, 1792, 7, true>(c, fn, A);
-        if (f == kQuantSwiglu && none) return quant_wave_one<XDT, 7, R0, kQuantSwiglu, 1792, 4>(c, fn, A);
+        if (f == kQuantRaw && reg256) return quant_wave_one<XDT, 4, R256, kQuantRaw, 1792, 7, true, 1, MR>(c, fn, A);
+        if (f == kQuantRaw && none) return quant_wave_one<XDT, 7, R0, kQuantRaw, 1792, 4, false, 1, MR>(c, fn, A);
+        if (f == kQuantSwiglu && reg256) return quant_wave_one<XDT, 4, R256, kQuantSwiglu, 1792, 7, true, 1, MR>(c, fn, A);
+        if (f == kQuantSwiglu && none) return quant_wave_one<XDT, 7, R0, kQuantSwiglu, 1792, 4, false, 1, MR>(c, fn, A);
     }
     return 1;   // not a shape of this set
 }

@@ -123,6 +123,64 @@ def test_swiglu_quant_fc2_width(request, layout, M, rot, group):
         codes_close(q2.to_numpy(), want_q, "two-call codes")
 
 
+# ---- the regular-256 quantizers leave the rotated values unscaled (fl(1/sqrt(256)) = 2^-4) and fold the power of
+# two into the codes' divisor, except in rows whose unscaled maximum is below 2^-60: rows of every magnitude from 1
+# down to 2^-115 and zero rows, on both sides of that threshold, bit for bit against the oracle's scaled arithmetic ----
+def tiny_rows(seed, C, heavy=True):
+    shifts = [0, -50, -56, -58, -60, -62, -64, -66, -68, -70, -80, -100, -115]
+    blocks = [bf16_rows(seed + i, 8, C, 2.0 ** k, heavy=heavy) for i, k in enumerate(shifts)]
+    blocks.append(np.zeros(4 * C, dtype=np.uint16))
+    return np.concatenate(blocks), 8 * len(shifts) + 4
+
+
+@pytest.mark.parametrize("K", [DH, DHEADS * DHD, DFF, 4096])
+@pytest.mark.parametrize("layout", ["four", "wave"])
+def test_int8_quantize_tiny_rows(request, layout, K):
+    dev = request.getfixturevalue("dev" if layout == "four" else "dev_wave")
+    x, M = tiny_rows(K, K)
+    want_q, want_s = o.quantize_act(x, o.BF16, M, K, o.ROT_REGULAR, 256)
+    q, s = new(dev, "I8", [M, K]), new(dev, "F32", [M])
+    ops.int8_quantize(up(dev, x, "BF16", [M, K]), q, s, 256)
+    assert_bits_equal(s.to_numpy(), want_s, "scales")
+    codes_close(q.to_numpy(), want_q, "codes")
+
+
+@pytest.mark.parametrize("C", [DFF, 8192])
+@pytest.mark.parametrize("layout", ["four", "wave"])
+def test_swiglu_quant_tiny_rows(request, layout, C):
+    dev = request.getfixturevalue("dev" if layout == "four" else "dev_wave")
+    x, M = tiny_rows(C + 7, 2 * C, heavy=False)
+    xt = up(dev, x, "BF16", [M, 2 * C])
+    q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+    ops.swiglu_quant(xt, q, s, rot=o.ROT_REGULAR, group=256)
+    act = new(dev, "BF16", [M, C])
+    ops.swiglu(xt, act)
+    want_q, want_s = o.quantize_act(act.to_numpy().ravel(), o.BF16, M, C, o.ROT_REGULAR, 256)
+    assert_bits_equal(s.to_numpy(), want_s, "scales")
+    codes_close(q.to_numpy(), want_q, "codes")
+
+
+@pytest.mark.parametrize("layout", ["four", "wave"])
+def test_norm_quant_tiny_weight(request, layout):
+    """the norm's rows are O(|w|) whatever x is: weights of 2^-62 .. 2^-75 put the rotated rows on both sides of the
+    threshold"""
+    dev = request.getfixturevalue("dev" if layout == "four" else "dev_wave")
+    M, C = 96, DH
+    x = bf16_rows(53, M, C)
+    rng = np.random.default_rng(54)
+    for k in (-62, -66, -70, -75):
+        w = (2.0 ** k * (1.0 + 0.1 * rng.standard_normal(C))).astype(np.float32)
+        sc = (0.3 * rng.standard_normal(2 * C)).astype(np.float32) * np.float32(2.0 ** k)
+        sh = (0.3 * rng.standard_normal(2 * C)).astype(np.float32) * np.float32(2.0 ** k)
+        rows = dit_rows(M)
+        want_q, want_s = o.norm_quant(x, o.BF16, M, C, w, 1e-5, rows, sc, sh, o.F32, o.BF16, o.ROT_REGULAR, 256)
+        q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+        tb = ops.Tables(scale=up(dev, sc, "F32", [2, C]), shift=up(dev, sh, "F32", [2, C]), rows=up(dev, rows, "I32", [M]))
+        ops.norm_quant(up(dev, x, "BF16", [M, C]), up(dev, w, "F32", [C]), 1e-5, tb, q, s, rot=o.ROT_REGULAR, group=256)
+        assert_bits_equal(s.to_numpy(), want_s, f"scales (w ~ 2^{k})")
+        codes_close(q.to_numpy(), want_q, f"codes (w ~ 2^{k})")
+
+
 # ---- h3s_norm_quant at the hidden width with float32 tables and a row table, 16896 rows ----
 @pytest.mark.parametrize("rot,group", [(o.ROT_REGULAR, 256), (o.ROT_NONE, 0)])
 @pytest.mark.parametrize("layout", ["four", "wave"])
@@ -152,6 +210,75 @@ def test_norm_quant_dit_width(request, layout, rot, group):
         ops.int8_quantize(h, q2, s2, group)
         assert_bits_equal(s2.to_numpy(), want_s, "two-call scales")
         codes_close(q2.to_numpy(), want_q, "two-call codes")
+
+
+# ---- the hidden width's norm kernels stream their rows over the resident blocks, each block keeping the weight and
+# one decoded table row in LDS: on a context sized for 2 compute units (H3S_CUS=2) every block takes many steps; the
+# row table has segments of three table rows whose boundaries fall inside steps (a step's rows then read table rows
+# other than the block's cached one from memory) and between them (the cache is refilled) ----
+@pytest.fixture(scope="module")
+def dev_cus2():
+    import os
+    from sycl_minimax_h3_amd import Device
+
+    old = {k: os.environ.get(k) for k in ("H3S_CUS", "H3S_QUANT_WAVE_MIN_ROWS")}
+    os.environ.update({"H3S_CUS": "2", "H3S_QUANT_WAVE_MIN_ROWS": "0"})
+    try:
+        d = Device.open()
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+    yield d
+    d.close()
+
+
+def segment_rows(M):
+    r = np.zeros(M, dtype=np.int32)
+    r[:37] = 1
+    r[37:41] = 2
+    r[41:90] = 0
+    r[90:91] = 1
+    r[91:300] = 2
+    r[300:] = 0
+    return r
+
+
+@pytest.mark.parametrize("M", [401, 130])
+@pytest.mark.parametrize("rot,group", [(o.ROT_REGULAR, 256), (o.ROT_NONE, 0)])
+def test_norm_quant_streamed_steps(dev_cus2, M, rot, group):
+    dev, C = dev_cus2, DH
+    x = bf16_rows(61 + M, M, C)
+    rng = np.random.default_rng(62)
+    w = (1.0 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    sc = (0.3 * rng.standard_normal(3 * C)).astype(np.float32)
+    sh = (0.3 * rng.standard_normal(3 * C)).astype(np.float32)
+    rows = segment_rows(M)
+    want_q, want_s = o.norm_quant(x, o.BF16, M, C, w, 1e-5, rows, sc, sh, o.F32, o.BF16, rot, group)
+    q, s = new(dev, "I8", [M, C]), new(dev, "F32", [M])
+    tb = ops.Tables(scale=up(dev, sc, "F32", [3, C]), shift=up(dev, sh, "F32", [3, C]), rows=up(dev, rows, "I32", [M]))
+    ops.norm_quant(up(dev, x, "BF16", [M, C]), up(dev, w, "F32", [C]), 1e-5, tb, q, s, rot=rot, group=group)
+    assert_bits_equal(s.to_numpy(), want_s, "scales")
+    codes_close(q.to_numpy(), want_q, "codes")
+
+
+@pytest.mark.parametrize("M", [401, 130])
+@pytest.mark.parametrize("mod", [True, False])
+def test_rms_norm_mod_streamed_steps(dev_cus2, M, mod):
+    dev, C = dev_cus2, DH
+    x = bf16_rows(63 + M, M, C)
+    rng = np.random.default_rng(64)
+    w = (1.0 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    sc = (0.3 * rng.standard_normal(3 * C)).astype(np.float32) if mod else None
+    sh = (0.3 * rng.standard_normal(3 * C)).astype(np.float32) if mod else None
+    rows = segment_rows(M) if mod else None
+    want = o.rms_norm_mod(x, o.BF16, M, C, w, 1e-5, rows, sc, sh, o.BF16)
+    h = new(dev, "BF16", [M, C])
+    m = ops.Mod(up(dev, rows, "I32", [M]), up(dev, sc, "F32", [3, C]), up(dev, sh, "F32", [3, C])) if mod else None
+    ops.rms_norm_mod(up(dev, x, "BF16", [M, C]), up(dev, w, "F32", [C]), 1e-5, m, h)
+    assert_bits_equal(h.to_numpy(), want, "h")
 
 
 # ---- h3s_rms_norm_mod at the hidden width in both layouts (the one-wavefront form stores h itself) ----
