@@ -86,6 +86,13 @@ def bytes_cfg():
         "copy_probe_1GiB": 2 << 30,
         # a plain copy moving config 1's bytes (half read, half written): the floor a launch of that size reaches
         "copy_probe_cfg1_bytes": 2 * CFG1_COPY_ELEMS * 2,
+        # torch's own elementwise kernels with the traffic of the fused kernels, the rate this device streams such a
+        # shape at: out = x + res (the AdaLN chain's two reads and one write), the two halves of each row of x added
+        # into a row half as long (the quantizers' 2 bytes read and 1 written a feature; torch's bfloat16 -> int8
+        # cast of the same bytes runs at 17 % of 8 TB/s), q of the qkv rows scaled in place (the DiT's rope)
+        **{f"probe_add_bf16_{M}x{C}": 3 * M * C * 2 for M in (M2, M4)},
+        **{f"probe_halfadd_bf16_{M}x{C}": M * C * 3 for M in (M2, M4)},
+        **{f"probe_inplace_bf16_{M}x7168_of_21504": 2 * M * 7168 * 2 for M in (M2, M4)},
     }
 
 
@@ -490,6 +497,26 @@ def main() -> int:
     dit_hbm(M2)
     dit_hbm(M4)
 
+    # torch's elementwise kernels with the fused kernels' traffic shapes (every run, before the compute-bound
+    # kernels: the rate attainable for each shape)
+    for M in (M2, M4):
+        def make_add(M=M):
+            x, r, o = bf16(M, C), bf16(M, C), torch.empty(M, C, dtype=torch.bfloat16, device=dev_t)
+            return lambda: torch.add(x, r, out=o)
+        run(f"probe_add_bf16_{M}x{C}", make_add)
+
+        def make_halfadd(M=M):
+            x, o = bf16(M, C), torch.empty(M, C // 2, dtype=torch.bfloat16, device=dev_t)
+            a, b = x[:, : C // 2], x[:, C // 2:]
+            return lambda: torch.add(a, b, out=o)
+        run(f"probe_halfadd_bf16_{M}x{C}", make_halfadd)
+
+        def make_inplace(M=M):
+            qkv = bf16(M, 3 * 7168)
+            q = qkv[:, :7168]
+            return lambda: q.mul_(1.0)
+        run(f"probe_inplace_bf16_{M}x7168_of_21504", make_inplace)
+
     # ---- the compute-bound kernels, last: config 5b's int8 GEMM, then attention ----
     run("cfg5b_int8_gemm_silu_47104x16384", lambda: (lambda: ops.int8_gemm_dequant(Q5, S5, layer, A.ACT_SILU, O5)), 5)
 
@@ -544,6 +571,7 @@ def main() -> int:
             dst = torch.empty_like(src)
             return lambda: dst.copy_(src)
         run("copy_probe_cfg1_bytes", make_copy1, 200)
+
 
     per = {}
     for k, ms in kernels.items():
