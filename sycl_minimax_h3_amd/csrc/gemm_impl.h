@@ -23,7 +23,8 @@
 // its unit holds: eight lanes cover one row's 128 bytes.
 //
 // Tile order: the 8 XCDs take blocks round robin; blocks are renumbered so that each XCD works on a contiguous
-// run of tiles, grouped 8 tiles high so that the resident blocks of an XCD share A and W panels in its L2.
+// run of tiles, grouped 8 tiles high (4 for K of 12288 or more) so that the resident blocks of an XCD share A and W
+// panels in its L2.
 // Epilogue: per 32-row slice of a wavefront's region, dequant + activation in registers, the slice through LDS,
 // then 16-byte row-contiguous stores.
 #pragma once
@@ -59,18 +60,21 @@ struct GemmArgs {
     void* out;                // [M, N]
     int out_dt;
     int tm, tn;               // tiles along M and N
+    int gh;                   // the height of a group of tiles an XCD walks (gemm_tile)
 };
 
 __device__ __forceinline__ int gemm_unit(int r, int c) { return (r << 3) | (c ^ ((r >> 1) & 7)); }
 
 // the tile of block b: XCD-contiguous renumbering (the blocks b % 8 = x, which XCD x runs, take the consecutive ids
-// x q + min(x, r) + b / 8, q = total / 8, r = total % 8: the first r XCDs one id more), then 8-high groups of tiles
-__device__ __forceinline__ void gemm_tile(int b, int tm, int tn, int* im, int* in) {
+// x q + min(x, r) + b / 8, q = total / 8, r = total % 8: the first r XCDs one id more), then GH-high groups of tiles
+// (GemmArgs::gh: 8, or 4 for the long-K products, whose A and W panels of 256 rows are larger: fc2's K = 14336 at
+// 47104 x 5376 took 3.50 against 3.64-3.66 ms with 4, config 5b's K = 4096 2.82 against 2.76-2.80 ms)
+__device__ __forceinline__ void gemm_tile(int b, int tm, int tn, int GH, int* im, int* in) {
     const int total = tm * tn, q = total / 8, r = total % 8, x = b % 8;
     const int id = x * q + (x < r ? x : r) + b / 8;
-    const int group = 8 * tn;
-    const int first = (id / group) * 8;
-    const int rows = tm - first < 8 ? tm - first : 8;
+    const int group = GH * tn;
+    const int first = (id / group) * GH;
+    const int rows = tm - first < GH ? tm - first : GH;
     *im = first + (id % group) % rows;
     *in = (id % group) / rows;
 }
@@ -94,7 +98,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / (kGemmBN / kGemmWN), wn = wave % (kGemmBN / kGemmWN);
     int im, in;
-    gemm_tile((int) blockIdx.x, P.tm, P.tn, &im, &in);
+    gemm_tile((int) blockIdx.x, P.tm, P.tn, P.gh, &im, &in);
     const int64_t m0 = (int64_t) im * kGemmBM, n0 = (int64_t) in * kGemmBN, K = P.K;
 
     // K steps of 128 bytes, the last one 64 when K is an odd multiple of 64 (its two slices only)

@@ -49,7 +49,7 @@ int launch_gemm(Ctx* c, const char* fn, const int8_t* q, const float* s, int64_t
                 const float* wscale, int64_t n_wscale, const float* bias, int act_, void* out, int out_dt) {
     const int64_t tm = (M + kGemmBM - 1) / kGemmBM, tn = (N + kGemmBN - 1) / kGemmBN;
     if (tm * tn > 0x7fffffff || tm > 0x7fffffff || tn > 0x7fffffff) return fail(std::string(fn) + ": too many tiles");
-    const GemmArgs P{q, s, M, K, w, N, wscale, bias, out, out_dt, (int) tm, (int) tn};
+    const GemmArgs P{q, s, M, K, w, N, wscale, bias, out, out_dt, (int) tm, (int) tn, K >= 12288 ? 4 : 8};
     const unsigned grid = (unsigned) (tm * tn);
     const bool per_n = n_wscale > 1;
 #define LG(ACT, PN) gemm_i8_kernel<ACT, PN><<<grid, kGemmThreads, 0, c->stream>>>(P)
