@@ -40,8 +40,10 @@ struct ChainArgs {
 // its rows, reloading the table rows only for a row whose table row differs. The weights and tables are read from
 // L2 by every block. At 16896 x 4096 with the AdaLN's three tables, two rows a block took the chain from 74.2 to
 // 70.8 us (cache-cold); three or four rows were slower (more registers, fewer wavefronts a SIMD).
-template <int XDT, int CPL, int F, int R = 1>
-__global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift) {
+// The rows of one unit: with first < 0 (R == 1) the row_pos layout (one row a block of L >= 256 lanes, or several
+// rows of 64 lanes a block); else the block's rows first .. first + R - 1 (rows of 256 or 512 lanes).
+template <int XDT, int CPL, int F, int R>
+__device__ __forceinline__ void row_chain_rows(const ChainArgs& A, int lshift, int64_t first) {
     constexpr int V = Vec<XDT>::V;
     constexpr bool DYN = F & ROW_DYN;
     constexpr bool TW = DYN || (F & ROW_TAB32), RW = DYN || (F & ROW_RES32);   // wide storage of tables, residual
@@ -63,7 +65,7 @@ __global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift)
     int t, W;
     int64_t rowk[R];
     bool livek[R];
-    if constexpr (R == 1) {
+    if (R == 1 && first < 0) {
         const RowPos P = row_pos(lshift, A.M);
         t = P.t;
         W = P.W;
@@ -74,7 +76,7 @@ __global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift)
         W = L >> 6;
 #pragma unroll
         for (int k = 0; k < R; ++k) {
-            const int64_t r = (int64_t) blockIdx.x * R + k;
+            const int64_t r = first + k;
             livek[k] = r < A.M;
             rowk[k] = livek[k] ? r : A.M - 1;
         }
@@ -221,6 +223,22 @@ __global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift)
     }
 }
 
+// R rows a block (R > 1: rows of 256 or 512 lanes). TAIL: the blocks from tail_blk0 on take one row each, the rows
+// from tail_row0 on: a launch of two-row blocks whose last round would fill at most half the device (16896 rows of
+// 4096 features: 5.5 rounds of the resident blocks) ends instead with a round of one-row blocks, twice as many and
+// half as long.
+template <int XDT, int CPL, int F, int R = 1, bool TAIL = false>
+__global__ __launch_bounds__(512) void row_chain_kernel(ChainArgs A, int lshift, int64_t tail_blk0, int64_t tail_row0) {
+    if constexpr (TAIL) {
+        static_assert(R > 1, "row_chain_kernel: a tail of one-row blocks after blocks of several rows");
+        if ((int64_t) blockIdx.x >= tail_blk0) {
+            row_chain_rows<XDT, CPL, F, 1>(A, lshift, tail_row0 + ((int64_t) blockIdx.x - tail_blk0));
+            return;
+        }
+    }
+    row_chain_rows<XDT, CPL, F, R>(A, lshift, R == 1 ? -1 : (int64_t) blockIdx.x * R);
+}
+
 // The call shapes compiled exactly (bfloat16 rows, 16-bit tensors all bfloat16): h3s_rms_norm_mod without and with
 // its float32 tables, h3s_layer_norm without and with weight and bias, and the AdaLN chain (16-bit tables, gate and
 // residual) for each norm and activation. Every other call shape runs the ROW_DYN instantiation.
@@ -246,18 +264,36 @@ template <int XDT> int chain_launch(Ctx* c, const char* fn, const ChainArgs& A, 
     // with side inputs the rows share, and rows enough that half as many blocks still fill the device many times
     const bool pair = XDT == H3S_BF16 && f != ROW_DYN && p.L >= 256 && p.cpl <= 2 &&
                       (f & (ROW_W | ROW_B | ROW_TAB | ROW_GATE)) && A.M >= (int64_t) c->cus * 16;
-    const unsigned grid2 = (unsigned) ((A.M + 1) / 2);
+    const int64_t pairs = (A.M + 1) / 2;
+#ifndef H3_CHAIN_TAIL
+#define H3_CHAIN_TAIL 1
+#endif
+    // the pairs that fill whole rounds of the device, and the rows of a last round at most half full as one-row
+    // blocks (H3_CHAIN_TAIL)
+    auto tail_split = [&](const void* k, int64_t& main_blocks, int64_t& tail_blocks) {
+        main_blocks = pairs;
+        tail_blocks = 0;
+        if (!H3_CHAIN_TAIL) return;
+        const int64_t round = (int64_t) c->cus * blocks_per_cu(k, (int) R.threads);
+        const int64_t full = pairs / round * round;
+        if (full > 0 && full < pairs && 2 * (pairs - full) <= round) {
+            main_blocks = full;
+            tail_blocks = A.M - 2 * full;
+        }
+    };
 #define H3_CHAIN_F(CC, FF)                                                                                            \
     {                                                                                                                 \
         if constexpr (CC <= 2) {                                                                                      \
             if (pair) {                                                                                               \
-                row_chain_kernel<XDT, CC, FF, 2><<<grid2, R.threads, 0, c->stream>>>(A, R.lshift);                   \
+                int64_t mb, tb;                                                                                       \
+                tail_split((const void*) row_chain_kernel<XDT, CC, FF, 2, true>, mb, tb);                             \
+                row_chain_kernel<XDT, CC, FF, 2, true><<<(unsigned) (mb + tb), R.threads, 0, c->stream>>>(A, R.lshift, mb, 2 * mb); \
                 return launched(fn);                                                                                  \
             }                                                                                                         \
         }                                                                                                             \
-        row_chain_kernel<XDT, CC, FF, 1><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift);                          \
+        row_chain_kernel<XDT, CC, FF, 1><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift, 0, 0);                    \
     }
-#define H3_CHAIN_D(CC) row_chain_kernel<XDT, CC, ROW_DYN, 1><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift)
+#define H3_CHAIN_D(CC) row_chain_kernel<XDT, CC, ROW_DYN, 1><<<R.grid, R.threads, 0, c->stream>>>(A, R.lshift, 0, 0)
 #define H3_CHAIN_ADA(CC, NORM)                                                                                        \
     if (f == (kChainAda | NORM)) { H3_CHAIN_F(CC, kChainAda | NORM); return launched(fn); }                          \
     if (f == (kChainAda | NORM | H3S_ACT_GELU_TANH * ROW_ACT1)) { H3_CHAIN_F(CC, kChainAda | NORM | H3S_ACT_GELU_TANH * ROW_ACT1); return launched(fn); } \

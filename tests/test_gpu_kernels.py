@@ -525,13 +525,16 @@ def segment_rows(seed, M, R):
     return np.repeat(np.arange(M) % R, lens)[:M].astype(np.int32)
 
 
+@pytest.mark.parametrize("M", [5001, 4401, 5201])
 @pytest.mark.parametrize("C", [2048, 4096])
 @pytest.mark.parametrize("kind", ["ada_ln_gelu", "ada_rms_silu", "ada_ln", "rms_mod_f32", "layer_norm_affine"])
-def test_chain_two_rows_a_block(dev, kind, C):
+def test_chain_two_rows_a_block(dev, kind, C, M):
     """Enough rows (an odd count) that rows of 256 lanes go two to a block: the weights and table rows are loaded
     once for both, and reloaded for the second row where its table row differs; the last block's second row is
-    past the end."""
-    M, R = 5001, 5          # at least 16 rows a compute unit of the 256
+    past the end. Where the pairs leave a last round of the resident blocks at most half full, the launch ends with
+    one-row blocks instead: 4401 rows (2201 pairs) do so for rounds of 1536 to 2048 blocks, 5201 rows for 1280,
+    1792 and 2048, 5001 rows for 1792 and 2048 (and take two-row blocks to the end for 1280 and 1536)."""
+    R = 5                   # at least 16 rows a compute unit of the 256
     x = inputs(40, M * C, o.BF16, 2.0)
     res = inputs(41, M * C, o.BF16)
     rows = segment_rows(42, M, R)
