@@ -82,7 +82,7 @@ def bytes_cfg():
         "attn_sage_16896x32x128": 4 * M2 * 4096 * 2,     # q, k, v read, out written (the products are the bound)
         "attn_sage_47104x32x128": 4 * M4 * 4096 * 2,
         "attn_f16_4096x32x128": 4 * 4096 * 4096 * 2,     # the 16-bit form (below 8192 tokens)
-        **dit_bytes(M2), **dit_bytes(M4),
+        **dit_bytes(M2), **dit_bytes(M4), **float_linear_bytes(M2),
         "copy_probe_1GiB": 2 << 30,
         # a plain copy moving config 1's bytes (half read, half written): the floor a launch of that size reaches
         "copy_probe_cfg1_bytes": 2 * CFG1_COPY_ELEMS * 2,
@@ -140,6 +140,22 @@ def dit_bytes(M: int) -> dict:
     for name, K, N in DIT_LINEARS:
         out[f"dit_quantize_g256_{name}_{M}"] = M * K * 2 + M * K + M * 4     # the int8 linear's first pass
         out[f"dit_int8_linear_{name}_{M}"] = M * K * 2 + N * K + N * 4 + M * N * 2
+    return out
+
+
+# The float linear (h3s_linear / h3s_linear_acc) at the DiT's hidden width, bfloat16 activations: a linear of the
+# width (with a bias) and a LoRA's two products at rank 64 (engine/h3-core/src/ops.rs:146-160: tmp = A x, then
+# out += B tmp); and torch's bfloat16 matmul of the square shape (the vendor library's rate, no bias)
+LORA_RANK = 64
+FLOAT_LINEARS = (("linear_bf16", DH, DH, True, False), ("lora_a_bf16", DH, LORA_RANK, False, False),
+                 ("lora_b_acc_bf16", LORA_RANK, DH, False, True))
+
+
+def float_linear_bytes(M: int) -> dict:
+    out = {}
+    for name, K, N, bias, acc in FLOAT_LINEARS:
+        out[f"{name}_{M}x{K}x{N}"] = M * K * 2 + N * K * 2 + (N * 4 if bias else 0) + M * N * 2 * (2 if acc else 1)
+    out[f"probe_matmul_bf16_{M}x{DH}x{DH}"] = M * DH * 2 + DH * DH * 2 + M * DH * 2
     return out
 
 
@@ -559,6 +575,29 @@ def main() -> int:
     dit_compute(M2)
     dit_compute(M4)
 
+    # ---- the float linear on bfloat16 activations (h3s_linear, h3s_linear_acc) ----
+    gen = torch.Generator(device="cpu").manual_seed(7)
+    for name, K, N, has_bias, acc in FLOAT_LINEARS:
+        key = f"{name}_{M2}x{K}x{N}"
+        if skip(key):
+            continue
+        w = (torch.randn(N, K, generator=gen) / K ** 0.5).to(torch.bfloat16).to(dev_t)
+        bias = (0.1 * torch.randn(N, generator=gen)).float().to(dev_t)
+        lin = ops.Linear(T(w), T(bias) if has_bias else None)
+        x, out = bf16(M2, K), bf16(M2, N)
+        X, O = T(x), T(out)
+        run(key, lambda: ((lambda: lin.forward_acc(X, O)) if acc else (lambda: lin.forward(X, O))), 10, ring=1)
+        del w, bias, lin, x, out, X, O
+        torch.cuda.empty_cache()
+    key = f"probe_matmul_bf16_{M2}x{DH}x{DH}"
+    if not skip(key):
+        w = (torch.randn(DH, DH, generator=gen) / DH ** 0.5).to(torch.bfloat16).to(dev_t)
+        x, out = bf16(M2, DH), torch.empty(M2, DH, dtype=torch.bfloat16, device=dev_t)
+        wt = w.t()
+        run(key, lambda: (lambda: torch.matmul(x, wt, out=out)), 10, ring=1)
+        del w, wt, x, out
+        torch.cuda.empty_cache()
+
     if args.copy_probe:
         def make_copy():
             src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev_t).fill_(1.0)
@@ -586,6 +625,11 @@ def main() -> int:
             K_, N_ = next((K, N) for name, K, N in DIT_LINEARS if k.startswith(f"dit_int8_linear_{name}_"))
             tops = 2 * Mk * K_ * N_ / (ms * 1e-3) / 1e12
             e.update({"TOPS_i8": round(tops, 1), "frac_i8_peak": round(tops / PEAK_I8_TOPS, 4)})
+        m_fl = re.match(r"(linear_bf16|lora_a_bf16|lora_b_acc_bf16|probe_matmul_bf16)_(\d+)x(\d+)x(\d+)$", k)
+        if m_fl:
+            Mk, K_, N_ = (int(v) for v in m_fl.groups()[1:])
+            tf = 2 * Mk * K_ * N_ / (ms * 1e-3) / 1e12
+            e.update({"TFLOPS_bf16": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_F16_TFLOPS, 4)})
         if k.startswith("dit_attention"):
             Mk = int(k.rsplit("_", 1)[1])
             half_ops = 2.0 * Mk * Mk * DHEADS * DHD

@@ -1,10 +1,16 @@
 // gemm_impl.h - the int8 GEMM with the dequant epilogue on gfx950's i8 matrix cores (kernels/h3sycl.cpp:576-631,
-// engine/h3-core/src/reference.rs:72-76), used by h3s_int8_linear and h3s_int8_gemm_dequant (int8_gemm.hip).
+// engine/h3-core/src/reference.rs:72-76), used by h3s_int8_linear and h3s_int8_gemm_dequant (int8_gemm.hip); and the
+// same pipeline on the bf16 / f16 matrix cores for the float linear (h3s_linear, h3s_linear_acc, linear.hip).
 //
 //   acc[m, n] = sum_k A[m, k] W[n, k]                    exact int32 (|acc| <= K 128 128 = 2^26 at K = 4096)
 //   one weight scale:  v = acc * fl(s[m] * wscale[0])     (the row factor the reference folds first, h3sycl.cpp:576)
 //   N weight scales:   v = (acc * s[m]) * wscale[n]       (the post-op order of h3sycl.cpp:588-602)
 //   then + bias[n], then the activation, rounded once to out's type.
+// 16-bit operands (gemm_f16_kernel): acc in float32 (v_mfma_f32_32x32x16_bf16 / _f16), v = acc [+ bias[n]]
+// [+ out[m, n], the old output of h3s_linear_acc], rounded once to out's type (kernels/h3sycl.cpp:656-720). A 32-deep
+// int8 slice and a 16-deep 16-bit slice are both 32 bytes of each row, with the same lane layout (lane l: row l % 32,
+// bytes 16 (l / 32) .. + 15 of the slice) and the same 32 x 32 accumulator layout, so the operand path below works
+// in bytes and serves both: GemmArgs::K is the bytes of a row.
 //
 // Block: 512 threads (eight wavefronts, 2 x 4, two a SIMD), a 256 x 256 tile of out; each wavefront 128 x 64 as
 // 4 x 2 v_mfma_i32_32x32x32_i8 accumulators (128 registers): while one wavefront of a SIMD waits (its fragment reads,
@@ -48,14 +54,20 @@ constexpr int kGemmLds = kGemmStages * kGemmStageBytes > kGemmEpiBytes ? kGemmSt
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf_g __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h_g __attribute__((ext_vector_type(8)));
+
+// the operands' element type: int8 codes (the dequant epilogue) or 16-bit floats (the float epilogue)
+enum : int { GEMM_I8 = 0, GEMM_BF16 = 1, GEMM_F16 = 2 };
 
 struct GemmArgs {
-    const int8_t* A;          // [M, K] quantized activations
-    const float* sA;          // [M] their scales
-    int64_t M, K;
+    const int8_t* A;          // [M, K] quantized activations (16-bit operands: their bytes)
+    const float* sA;          // [M] their scales (NULL for 16-bit operands)
+    int64_t M, K;             // K: the bytes of a row (the features for int8, twice them for 16-bit operands)
     const int8_t* W;          // [N, K]
     int64_t N;
-    const float* ws;          // [N] or [1]
+    const float* ws;          // [N] or [1] (NULL for 16-bit operands)
     const float* bias;        // [N] or NULL
     void* out;                // [M, N]
     int out_dt;
@@ -92,8 +104,43 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const int8_t* base, 
 __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 
-template <int ACT, bool PER_N>
-__global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
+// the float32 values of out[m, n .. n + 3] (the old output h3s_linear_acc adds): one vector load where the tile lies
+// inside out and its rows start on 16-byte boundaries (n is a multiple of 4), else element by element inside out
+template <int OUT>
+__device__ __forceinline__ void gemm_old4(const void* out, int64_t m, int64_t n, int64_t M, int64_t N, bool full, float (&o)[4]) {
+    if (full) {
+        if constexpr (OUT == H3S_F32) {
+            const float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(out) + m * N + n);
+            o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+        } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(out) + m * N + n);
+            const uint32_t h[2] = {v.x, v.y};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t b = (h[q / 2] >> (16 * (q & 1))) & 0xFFFFu;
+                o[q] = OUT == H3S_BF16 ? bf16_lo(b) : f16_lo(b);
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        o[q] = 0.0f;
+        if (m < M && n + q < N) {
+            const int64_t i = m * N + n + q;
+            if constexpr (OUT == H3S_F32) o[q] = reinterpret_cast<const float*>(out)[i];
+            else if constexpr (OUT == H3S_BF16) o[q] = bf16_lo(reinterpret_cast<const uint16_t*>(out)[i]);
+            else o[q] = f16_lo(reinterpret_cast<const uint16_t*>(out)[i]);
+        }
+    }
+}
+
+// The kernel body for the operand type OP; ACC (16-bit operands only): out += the product.
+template <int OP, int ACT, bool PER_N, bool ACC>
+__device__ __forceinline__ void gemm_body(const GemmArgs& P) {
+    static_assert(OP == GEMM_I8 || (ACT == H3S_ACT_NONE && !PER_N), "gemm_body: the float epilogue has no scales or activation");
+    static_assert(!ACC || OP != GEMM_I8, "gemm_body: accumulation into out is the float linear's");
+    using Acc = std::conditional_t<OP == GEMM_I8, v16i, v16f>;
     __shared__ __attribute__((aligned(16))) int8_t lds[kGemmLds];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / (kGemmBN / kGemmWN), wn = wave % (kGemmBN / kGemmWN);
@@ -136,16 +183,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
     float sv = 0.0f, wv = 0.0f, bv = 0.0f;
     if (tid < kGemmBM) {
         const int64_t m = m0 + tid < P.M ? m0 + tid : P.M - 1, n = n0 + tid < P.N ? n0 + tid : P.N - 1;
-        sv = P.sA[m];
+        if constexpr (OP == GEMM_I8) sv = P.sA[m];
         if constexpr (PER_N) wv = P.ws[n];
         if (P.bias) bv = P.bias[n];
     }
 
-    v16i acc[kGemmWI][kGemmWJ];
+    Acc acc[kGemmWI][kGemmWJ];
 #pragma unroll
     for (int i = 0; i < kGemmWI; ++i)
 #pragma unroll
-        for (int j = 0; j < kGemmWJ; ++j) acc[i][j] = (v16i) 0;
+        for (int j = 0; j < kGemmWJ; ++j) acc[i][j] = (Acc) 0;
 
     // fragment bases (bytes in a stage) of slice kk: row l % 32 of the wavefront's first 32-row tile, chunk
     // 2 kk + l / 32; tile i is 4096 i further (32 rows of 128 bytes, the swizzle the same for every tile)
@@ -170,7 +217,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
     // out) from A tile i, so each lane ends with four consecutive output columns of one output row per register group
     auto mfma = [&](const v4i (&a)[kGemmWI], const v4i (&b)[kGemmWJ], int p) {
         const int i = p / kGemmWJ, j = p % kGemmWJ;
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[j], a[i], acc[i][j], 0, 0, 0);
+        if constexpr (OP == GEMM_I8) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[j], a[i], acc[i][j], 0, 0, 0);
+        else if constexpr (OP == GEMM_BF16)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf_g, b[j]), __builtin_bit_cast(v8bf_g, a[i]),
+                                                                acc[i][j], 0, 0, 0);
+        else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_g, b[j]), __builtin_bit_cast(v8h_g, a[i]),
+                                                               acc[i][j], 0, 0, 0);
     };
     int issued = 0;
     for (; issued < kGemmStages && issued < nk; ++issued) issue(issued);
@@ -264,7 +317,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
         constexpr int esz = OUT == H3S_F32 ? 4 : 2;
         constexpr int pitch = kGemmWN * esz + 16;           // bytes a slice row (16 bytes of pad: distinct banks)
         int8_t* slice = lds + 3 * 1024 + wave * (32 * pitch);
-        const float ws0 = PER_N ? 0.0f : P.ws[0];
+        const float ws0 = OP == GEMM_I8 && !PER_N ? P.ws[0] : 0.0f;
         // rows of out start on 16-byte boundaries and the block's tile lies inside out: plain 16-byte stores
         const bool full = (P.N * esz) % 16 == 0 && m0 + kGemmBM <= P.M && n0 + kGemmBN <= P.N;
         constexpr int per_row = kGemmWN * esz / 16, epc = 16 / esz;
@@ -278,7 +331,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
                 for (int g = 0; g < 4; ++g) {
                     const int cl = wn * kGemmWN + j * 32 + 8 * g + 4 * (lane >> 5);    // first of the four columns
                     float v[4];
-                    if constexpr (PER_N) {
+                    if constexpr (OP != GEMM_I8) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) v[q] = acc[i][j][4 * g + q];
+                    } else if constexpr (PER_N) {
                         const float4 w4 = *reinterpret_cast<const float4*>(wcol + cl);
                         const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
@@ -290,6 +346,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
                     if constexpr (BIAS) {
                         const float4 b4 = *reinterpret_cast<const float4*>(bcol + cl);
                         v[0] = v[0] + b4.x; v[1] = v[1] + b4.y; v[2] = v[2] + b4.z; v[3] = v[3] + b4.w;
+                    }
+                    if constexpr (ACC) {
+                        float o4[4];
+                        gemm_old4<OUT>(P.out, m0 + wm * kGemmWM + i * 32 + (lane & 31), n0 + cl, P.M, P.N, full, o4);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) v[q] = v[q] + o4[q];
                     }
 #pragma unroll
                     for (int q = 0; q < 4; ++q) v[q] = act<ACT>(v[q]);
@@ -328,6 +390,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
     if (P.out_dt == H3S_BF16) { if (P.bias) epilogue(bf16_t{}, yes{}); else epilogue(bf16_t{}, no{}); }
     else if (P.out_dt == H3S_F16) { if (P.bias) epilogue(f16_t{}, yes{}); else epilogue(f16_t{}, no{}); }
     else { if (P.bias) epilogue(f32_t{}, yes{}); else epilogue(f32_t{}, no{}); }
+}
+
+template <int ACT, bool PER_N>
+__global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
+    gemm_body<GEMM_I8, ACT, PER_N, false>(P);
+}
+// the float linear: 16-bit operands (OP GEMM_BF16 or GEMM_F16), out = x w^T [+ bias] (ACC: out += x w^T [+ bias])
+template <int OP, bool ACC>
+__global__ __launch_bounds__(kGemmThreads, 1) void gemm_f16_kernel(GemmArgs P) {
+    gemm_body<OP, H3S_ACT_NONE, false, ACC>(P);
 }
 
 }  // namespace h3

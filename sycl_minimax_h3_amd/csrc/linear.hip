@@ -1,11 +1,14 @@
 // linear.hip - the plain (float) linear layers of kernels/h3sycl.h:87-93: h3s_linear (out = x w^T + bias),
 // h3s_linear_acc (out += x w^T + bias, a LoRA's second factor) and h3s_scale_rows (kernels/h3sycl.cpp:656-739).
-// The products run on rocBLAS (a plain library GEMM, float32 accumulation, on the context's stream) into a float32
-// scratch, a chunk of rows at a time; the epilogue kernel adds the bias (and the old output) in float32 and rounds
-// once to the output type, as the reference's matmul post-ops do.
+// bfloat16 and half operands with K a multiple of 32 and more than 128 outputs a row run on the matrix cores in
+// gemm_impl.h's pipeline (gemm_f16_kernel): float32 accumulation, and the epilogue adds the bias (and the old output)
+// in float32 and rounds once to the output type, as the reference's matmul post-ops do, with no intermediate in
+// memory. Every other call (float32 operands, other K, narrow outputs, unaligned rows) runs on rocBLAS (a plain
+// library GEMM, float32 accumulation, on the context's stream) into a float32 scratch, a chunk of rows at a time, and
+// the same epilogue as a kernel of its own.
 #include <rocblas/rocblas.h>
 
-#include "common.h"
+#include "gemm_impl.h"
 
 namespace h3 {
 
@@ -80,10 +83,37 @@ static int launch_epilogue(Ctx* c, const float* acc, int64_t M, int64_t N, const
     return 0;
 }
 
-// the product x [M, K] . w^T (w [N, K]), both in dt, into out (or out +=) a chunk of rows at a time
+// whether gemm_f16_kernel takes the product: 16-bit operands whose rows are whole 64-byte units (the pipeline's
+// half K step) and start on 16-byte boundaries (out too), K * 2 below 2^24 bytes, tile counts within 32 bits, and
+// more than 128 outputs a row. A narrower product (a LoRA's first factor, rank 64: 16896 x 5376 -> 64 took 104 us
+// on the 256 x 256 tiles, three quarters of their products wasted, against rocBLAS's 63) stays on rocBLAS.
+static bool mfma_takes(int dt, const void* x, const void* w, const void* out, int64_t M, int64_t K, int64_t N) {
+    const int64_t tm = (M + kGemmBM - 1) / kGemmBM, tn = (N + kGemmBN - 1) / kGemmBN;
+    return (dt == H3S_BF16 || dt == H3S_F16) && K % 32 == 0 && 2 * K < ((int64_t) 1 << 24) && N > 128 &&
+           aligned16(x) && aligned16(w) && aligned16(out) && tm * tn <= 0x7fffffff;
+}
+static int linear_mfma(Ctx* c, const char* fn, const void* x, int dt, int64_t M, int64_t K, const void* w, int64_t N,
+                       const float* bias, void* out, int out_dt, bool acc) {
+    const int64_t tm = (M + kGemmBM - 1) / kGemmBM, tn = (N + kGemmBN - 1) / kGemmBN, kb = 2 * K;
+    const GemmArgs P{(const int8_t*) x, nullptr, M, kb, (const int8_t*) w, N, nullptr, bias, out, out_dt, (int) tm, (int) tn,
+                     kb >= 12288 ? 4 : 8};
+    const unsigned grid = (unsigned) (tm * tn);
+    if (dt == H3S_BF16) {
+        if (acc) gemm_f16_kernel<GEMM_BF16, true><<<grid, kGemmThreads, 0, c->stream>>>(P);
+        else gemm_f16_kernel<GEMM_BF16, false><<<grid, kGemmThreads, 0, c->stream>>>(P);
+    } else {
+        if (acc) gemm_f16_kernel<GEMM_F16, true><<<grid, kGemmThreads, 0, c->stream>>>(P);
+        else gemm_f16_kernel<GEMM_F16, false><<<grid, kGemmThreads, 0, c->stream>>>(P);
+    }
+    return launched(fn);
+}
+
+// the product x [M, K] . w^T (w [N, K]), both in dt, into out (or out +=): on the matrix cores, or on rocBLAS a
+// chunk of rows at a time
 static int linear(Ctx* c, const char* fn, const void* x, int dt, int64_t M, int64_t K, const void* w, int64_t N,
                   const float* bias, void* out, int out_dt, bool acc) {
     if (K > 0x7fffffff || N > 0x7fffffff) return fail(std::string(fn) + ": K and N must be below 2^31");
+    if (mfma_takes(dt, x, w, out, M, K, N)) return linear_mfma(c, fn, x, dt, M, K, w, N, bias, out, out_dt, acc);
     rocblas_handle h = blas_of(c);
     if (!h) return -1;
     // rows a chunk: the float32 product of a chunk takes at most 256 MiB (and at most 8192 rows, as the reference)

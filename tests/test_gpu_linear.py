@@ -1,6 +1,10 @@
 """GPU parity of the plain linear layers (kernels/h3sycl.cpp:656-739) through the C ABI against the oracle's float64
 products: h3s_linear, h3s_linear_acc (row chunks included) and h3s_scale_rows. The reference's products are oneDNN's,
-whose accumulation order is not restated: the parity tolerance (relative L2 < 1e-3, one ulp of the output type)."""
+whose accumulation order is not restated: the parity tolerance (relative L2 < 1e-3, one ulp of the output type).
+bfloat16 and half operands with K a multiple of 32 and N above 128 run on the matrix-core kernel (256 x 256 tiles:
+partial tiles at every edge, K steps of 64 elements with a last half step where K is an odd multiple of 32, the
+long-K tile order from K = 6144); K = 200, N of 128 or less and float32 operands run on rocBLAS with the separate
+epilogue."""
 import numpy as np
 import pytest
 
@@ -31,7 +35,8 @@ def close(got, want, dt, what):
 
 
 @pytest.mark.parametrize("dt,out_dt", [(o.BF16, o.BF16), (o.BF16, o.F32), (o.F16, o.F16), (o.F32, o.F32), (o.F32, o.BF16)])
-@pytest.mark.parametrize("M,K,N", [(37, 256, 130), (300, 1024, 520), (8200, 64, 48)])
+@pytest.mark.parametrize("M,K,N", [(37, 256, 130), (300, 1024, 520), (8200, 64, 48), (1000, 2048, 700), (513, 6144, 300),
+                                   (600, 200, 90), (257, 96, 256)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_linear(dev, dt, out_dt, M, K, N, bias):
     x, w, b = mats(100 + K, M, K, N, dt)
@@ -42,9 +47,9 @@ def test_linear(dev, dt, out_dt, M, K, N, bias):
     close(out.to_numpy(), want, out_dt, "linear")
 
 
+@pytest.mark.parametrize("M,K,N", [(8300, 128, 64), (700, 1024, 600), (300, 96, 260), (130, 200, 70)])
 @pytest.mark.parametrize("dt", [o.BF16, o.F16, o.F32])
-def test_linear_acc(dev, dt):
-    M, K, N = 8300, 128, 64
+def test_linear_acc(dev, dt, M, K, N):
     x, w, b = mats(110, M, K, N, dt)
     prev = o.to_dt(np.random.default_rng(111).standard_normal(M * N).astype(np.float32), dt)
     want = o.linear(x, dt, M, K, w, N, b, out_dt=dt, acc_into=prev)
