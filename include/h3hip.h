@@ -90,8 +90,9 @@ int h3s_int8_linear(void* ctx, const void* x, int x_dt, int64_t M, int64_t K, co
                     const float* wscale, int64_t n_wscale, const float* bias, void* out, int out_dt, int group);
 
 /* Float linear layers (kernels/h3sycl.h:89-95): h3s_linear out = x w^T + bias, h3s_linear_acc out += x w^T + bias,
- * h3s_scale_rows x[r] *= s[r]. The products run on rocBLAS (float32 accumulation, the context's stream); the bias and
- * the old output are added in float32 and rounded once to the output type. */
+ * h3s_scale_rows x[r] *= s[r]. Float32 accumulation on the context's stream: bfloat16 and half operands with K a
+ * multiple of 32, more than 128 outputs a row and 16-byte aligned rows on the library's own matrix-core kernel, every
+ * other call on rocBLAS; the bias and the old output are added in float32 and rounded once to the output type. */
 int h3s_linear_acc(void* ctx, const void* x, int dt, int64_t M, int64_t K, const void* w, int64_t N, const float* bias, void* out);
 int h3s_scale_rows(void* ctx, void* x, int dt, int64_t M, int64_t C, const float* s);
 int h3s_linear(void* ctx, const void* x, int dt, int64_t M, int64_t K, const void* w, int64_t N, const float* bias,
