@@ -65,6 +65,7 @@ struct Ctx {
         ATT_AUX,     //   the block scales and k's mean
         ATT_PART,    //   the split blocks' partial sums (O, m, l)
         LIN_F32,     // h3s_linear / h3s_linear_acc: the float32 product of a row chunk
+        GEMM_PART,   // the matrix-core GEMMs: the accumulators of the split last tiles' parts
         N_REGIONS
     };
     struct Area { void* p = nullptr; size_t bytes = 0; };

@@ -51,6 +51,7 @@ constexpr int kGemmStageBytes = (kGemmBM + kGemmBN) * kGemmBK;   // 64 KiB
 // the two stages, or the epilogue's scales and per-wavefront 32-row slices of float32 outputs, if larger
 constexpr int kGemmEpiBytes = 3 * 1024 + kGemmWaves * 32 * (kGemmWN * 4 + 16);
 constexpr int kGemmLds = kGemmStages * kGemmStageBytes > kGemmEpiBytes ? kGemmStages * kGemmStageBytes : kGemmEpiBytes;
+constexpr int kGemmTileAcc = kGemmBM * kGemmBN;                   // accumulators of a tile (a split tile's part)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -72,7 +73,13 @@ struct GemmArgs {
     void* out;                // [M, N]
     int out_dt;
     int tm, tn;               // tiles along M and N
-    int gh;                   // the height of a group of tiles an XCD walks (gemm_tile)
+    int gh;                   // the height of a group of tiles an XCD walks (gemm_tile_of)
+    // The last tiles split along K: blocks [0, main_tiles) take tiles 0 .. main_tiles - 1 whole; block main_tiles +
+    // u split + p takes part p of tile main_tiles + u (a contiguous share of the K steps) and leaves its
+    // accumulators in part[u split + p] (kGemmTileAcc values of 4 bytes, in register order); gemm_merge_kernel then
+    // sums each tile's parts in part order and applies the epilogue. split 1: every tile whole.
+    int main_tiles, split;
+    void* part;
 };
 
 __device__ __forceinline__ int gemm_unit(int r, int c) { return (r << 3) | (c ^ ((r >> 1) & 7)); }
@@ -81,9 +88,11 @@ __device__ __forceinline__ int gemm_unit(int r, int c) { return (r << 3) | (c ^ 
 // x q + min(x, r) + b / 8, q = total / 8, r = total % 8: the first r XCDs one id more), then GH-high groups of tiles
 // (GemmArgs::gh: 8, or 4 for the long-K products, whose A and W panels of 256 rows are larger: fc2's K = 14336 at
 // 47104 x 5376 took 3.50 against 3.64-3.66 ms with 4, config 5b's K = 4096 2.82 against 2.76-2.80 ms)
-__device__ __forceinline__ void gemm_tile(int b, int tm, int tn, int GH, int* im, int* in) {
-    const int total = tm * tn, q = total / 8, r = total % 8, x = b % 8;
-    const int id = x * q + (x < r ? x : r) + b / 8;
+__device__ __forceinline__ int gemm_xcd_id(int b, int total) {
+    const int q = total / 8, r = total % 8, x = b % 8;
+    return x * q + (x < r ? x : r) + b / 8;
+}
+__device__ __forceinline__ void gemm_tile_of(int id, int tm, int tn, int GH, int* im, int* in) {
     const int group = GH * tn;
     const int first = (id / group) * GH;
     const int rows = tm - first < GH ? tm - first : GH;
@@ -135,6 +144,23 @@ __device__ __forceinline__ void gemm_old4(const void* out, int64_t m, int64_t n,
     }
 }
 
+// The epilogue's values of out[m][n .. n + 3] from their accumulators a (gemm_body, and gemm_merge_kernel for the split
+// tiles: the same roundings in the same order): int8 dequant, acc s[m] wscale[n] or acc f1 with f1 = fl(s[m]
+// wscale[0]) (16-bit operands: acc itself), then + bias[n], + the old out (ACC), then the activation
+template <int OP, int ACT, bool PER_N, bool BIAS, bool ACC, typename E>
+__device__ __forceinline__ void gemm_values(const E (&a)[4], float sr, float f1, const float (&wq)[4], const float (&bq)[4],
+                                            const float (&oq)[4], float (&v)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if constexpr (OP != GEMM_I8) v[q] = a[q];
+        else if constexpr (PER_N) v[q] = (float) a[q] * sr * wq[q];
+        else v[q] = (float) a[q] * f1;
+        if constexpr (BIAS) v[q] = v[q] + bq[q];
+        if constexpr (ACC) v[q] = v[q] + oq[q];
+        v[q] = act<ACT>(v[q]);
+    }
+}
+
 // The kernel body for the operand type OP; ACC (16-bit operands only): out += the product.
 template <int OP, int ACT, bool PER_N, bool ACC>
 __device__ __forceinline__ void gemm_body(const GemmArgs& P) {
@@ -144,13 +170,22 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& P) {
     __shared__ __attribute__((aligned(16))) int8_t lds[kGemmLds];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / (kGemmBN / kGemmWN), wn = wave % (kGemmBN / kGemmWN);
-    int im, in;
-    gemm_tile((int) blockIdx.x, P.tm, P.tn, P.gh, &im, &in);
-    const int64_t m0 = (int64_t) im * kGemmBM, n0 = (int64_t) in * kGemmBN, K = P.K;
-
-    // K steps of 128 bytes, the last one 64 when K is an odd multiple of 64 (its two slices only)
+    const int64_t K = P.K;
+    // K steps of 128 bytes, the last one 64 when K is an odd multiple of 64 (its two slices only); a tile's part
+    // runs the steps [kb, ke)
     const int nk = (int) ((K + kGemmBK - 1) / kGemmBK);
-    const bool half_last = K % kGemmBK != 0;
+    int im, in, kb = 0, ke = nk, part = -1;
+    if ((int) blockIdx.x < P.main_tiles) {
+        gemm_tile_of(gemm_xcd_id((int) blockIdx.x, P.main_tiles), P.tm, P.tn, P.gh, &im, &in);
+    } else {
+        const int u = ((int) blockIdx.x - P.main_tiles) / P.split, p = ((int) blockIdx.x - P.main_tiles) % P.split;
+        gemm_tile_of(P.main_tiles + u, P.tm, P.tn, P.gh, &im, &in);
+        kb = p * nk / P.split;
+        ke = (p + 1) * nk / P.split;
+        part = u * P.split + p;
+    }
+    const int64_t m0 = (int64_t) im * kGemmBM, n0 = (int64_t) in * kGemmBN;
+    const bool half_last = K % kGemmBK != 0 && ke == nk;
     // Instruction q of wavefront w fills units 64 (4 w + q) .. + 63: rows 8 (4 w + q) + lane / 8, each lane the
     // chunk its unit holds, so one instruction reads 8 whole 128-byte segments. The loads go through buffer resources
     // (gemm_rsrc): rows past the matrix's end read zeros (their products are not stored), so the lanes' 32-bit offsets
@@ -225,12 +260,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& P) {
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_g, b[j]), __builtin_bit_cast(v8h_g, a[i]),
                                                                acc[i][j], 0, 0, 0);
     };
-    int issued = 0;
-    for (; issued < kGemmStages && issued < nk; ++issued) issue(issued);
+    int issued = kb;
+    for (; issued < kb + kGemmStages && issued < ke; ++issued) issue(issued);
     v4i xa[kGemmWI], xb[kGemmWJ], ya[kGemmWI], yb[kGemmWJ];
-    if (issued > 1) wait_vm<2 * kGemmLoads>(); else wait_vm<0>();
+    if (issued - kb > 1) wait_vm<2 * kGemmLoads>(); else wait_vm<0>();
     block_barrier();
-    read_half(0, 0, xa, xb);
+    read_half(kb, 0, xa, xb);
     // a slice's products (kGemmMF) with the next slice's fragment reads (kGemmWI + kGemmWJ) between them
     auto body16 = [&](const v4i (&a)[kGemmWI], const v4i (&b)[kGemmWJ]) {
         constexpr int NR = kGemmWI + kGemmWJ;
@@ -279,27 +314,39 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& P) {
             }
         }
     };
-    int kt = 0;
-    for (; kt < nk - 2; ++kt) step(kt, std::true_type{});
-    for (; kt < nk - 1; ++kt) step(kt, std::false_type{});
+    int kt = kb;
+    for (; kt < ke - 2; ++kt) step(kt, std::true_type{});
+    for (; kt < ke - 1; ++kt) step(kt, std::false_type{});
     // the last step: no stage after it; a half step has slices 0 and 1 only
-    read_half(nk - 1, 1, ya, yb);
+    read_half(ke - 1, 1, ya, yb);
     body16(xa, xb);
     if (!half_last) {
-        read_half(nk - 1, 2, xa, xb);
+        read_half(ke - 1, 2, xa, xb);
         body16(ya, yb);
-        read_half(nk - 1, 3, ya, yb);
+        read_half(ke - 1, 3, ya, yb);
         body16(xa, xb);
     }
 #pragma unroll
     for (int p = 0; p < kGemmMF; ++p) mfma(ya, yb, p);
     wait_vm<0>();
+    if (part >= 0) {
+        // a part of a split tile: its accumulators, register by register, 64 lanes' 4-byte values contiguous
+        using E = std::conditional_t<OP == GEMM_I8, int, float>;
+        E* dst = reinterpret_cast<E*>(P.part) + (size_t) part * kGemmTileAcc + wave * (kGemmMF * 16 * 64) + lane;
+#pragma unroll
+        for (int i = 0; i < kGemmWI; ++i)
+#pragma unroll
+            for (int j = 0; j < kGemmWJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) dst[((i * kGemmWJ + j) * 16 + r) * 64] = acc[i][j][r];
+        return;
+    }
     __syncthreads();   // every stage read: the LDS is the epilogue's now
 
     // ---- epilogue ----
     // Register r of acc[i][j] holds out[m][n] with m = wm 128 + 32 i + lane % 32 and
-    // n = wn 128 + 32 j + 8 (r / 4) + 4 (lane / 32) + r % 4: four consecutive columns per group of four registers.
-    // Per 32-row slice i of this wavefront's 128 x 128 region: dequant + activation in registers, the four columns
+    // n = wn 64 + 32 j + 8 (r / 4) + 4 (lane / 32) + r % 4: four consecutive columns per group of four registers.
+    // Per 32-row slice i of this wavefront's 128 x 64 region: dequant + activation in registers, the four columns
     // as one 8-byte (16-bit out) or 16-byte (float32 out) LDS write, then 16-byte row-contiguous global stores.
     // One wavefront writes and reads its own slice, and a wavefront's LDS operations run in order.
     float* srow = reinterpret_cast<float*>(lds);            // s[m] of the block's 256 rows
@@ -330,31 +377,20 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& P) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int cl = wn * kGemmWN + j * 32 + 8 * g + 4 * (lane >> 5);    // first of the four columns
-                    float v[4];
-                    if constexpr (OP != GEMM_I8) {
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) v[q] = acc[i][j][4 * g + q];
-                    } else if constexpr (PER_N) {
+                    using E = std::conditional_t<OP == GEMM_I8, int, float>;
+                    const E a[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                    float wq[4] = {0.0f, 0.0f, 0.0f, 0.0f}, bq[4] = {0.0f, 0.0f, 0.0f, 0.0f}, oq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    if constexpr (PER_N) {
                         const float4 w4 = *reinterpret_cast<const float4*>(wcol + cl);
-                        const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) v[q] = (float) acc[i][j][4 * g + q] * sr * wv[q];
-                    } else {
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) v[q] = (float) acc[i][j][4 * g + q] * f1;
+                        wq[0] = w4.x; wq[1] = w4.y; wq[2] = w4.z; wq[3] = w4.w;
                     }
                     if constexpr (BIAS) {
                         const float4 b4 = *reinterpret_cast<const float4*>(bcol + cl);
-                        v[0] = v[0] + b4.x; v[1] = v[1] + b4.y; v[2] = v[2] + b4.z; v[3] = v[3] + b4.w;
+                        bq[0] = b4.x; bq[1] = b4.y; bq[2] = b4.z; bq[3] = b4.w;
                     }
-                    if constexpr (ACC) {
-                        float o4[4];
-                        gemm_old4<OUT>(P.out, m0 + wm * kGemmWM + i * 32 + (lane & 31), n0 + cl, P.M, P.N, full, o4);
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) v[q] = v[q] + o4[q];
-                    }
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) v[q] = act<ACT>(v[q]);
+                    if constexpr (ACC) gemm_old4<OUT>(P.out, m0 + wm * kGemmWM + i * 32 + (lane & 31), n0 + cl, P.M, P.N, full, oq);
+                    float v[4];
+                    gemm_values<OP, ACT, PER_N, BIAS, ACC>(a, sr, f1, wq, bq, oq, v);
                     int8_t* at = slice + (lane & 31) * pitch + (j * 32 + 8 * g + 4 * (lane >> 5)) * esz;
                     if constexpr (OUT == H3S_F32)
                         *reinterpret_cast<float4*>(at) = make_float4(v[0], v[1], v[2], v[3]);
@@ -400,6 +436,75 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs P) {
 template <int OP, bool ACC>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_f16_kernel(GemmArgs P) {
     gemm_body<OP, H3S_ACT_NONE, false, ACC>(P);
+}
+
+// The split tiles' epilogue: a thread takes one group of four accumulators of a tile (the wavefront, 32 x 32 block,
+// register group and lane of the part layout), sums the tile's parts in part order (int32: exact, the whole tile's
+// sum; float32: a fixed order), then the epilogue of gemm_body on out[m][n .. n + 3]. 64 blocks of 256 a tile.
+constexpr int kGemmMergeBlocks = kGemmTileAcc / 4 / 256;
+template <int OP, int ACT, bool PER_N, bool ACC, int OUT, bool BIAS>
+__global__ __launch_bounds__(256) void gemm_merge_kernel(GemmArgs P) {
+    using E = std::conditional_t<OP == GEMM_I8, int, float>;
+    const int u = (int) blockIdx.x / kGemmMergeBlocks;
+    const int t = ((int) blockIdx.x % kGemmMergeBlocks) * 256 + (int) threadIdx.x;
+    const int lane = t & 63, grp = t >> 6;              // grp = ((wave kGemmWI + i) kGemmWJ + j) 4 + g
+    const int g = grp & 3, j = (grp >> 2) % kGemmWJ, i = (grp >> 2) / kGemmWJ % kGemmWI, wave = (grp >> 2) / kGemmMF;
+    const int wm = wave / (kGemmBN / kGemmWN), wn = wave % (kGemmBN / kGemmWN);
+    int im, in;
+    gemm_tile_of(P.main_tiles + u, P.tm, P.tn, P.gh, &im, &in);
+    const int64_t m = (int64_t) im * kGemmBM + wm * kGemmWM + i * 32 + (lane & 31);
+    const int64_t n = (int64_t) in * kGemmBN + wn * kGemmWN + j * 32 + 8 * g + 4 * (lane >> 5);
+    if (m >= P.M || n >= P.N) return;
+    const E* src = reinterpret_cast<const E*>(P.part) + (size_t) u * P.split * kGemmTileAcc +
+                   ((wave * kGemmWI + i) * kGemmWJ + j) * 16 * 64 + 4 * g * 64 + lane;
+    E a[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] = src[q * 64];
+    for (int p = 1; p < P.split; ++p)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[q] = a[q] + src[(size_t) p * kGemmTileAcc + q * 64];
+    float sr = 0.0f, f1 = 0.0f, wq[4] = {0.0f, 0.0f, 0.0f, 0.0f}, bq[4] = {0.0f, 0.0f, 0.0f, 0.0f}, oq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (OP == GEMM_I8) {
+        sr = P.sA[m];
+        if constexpr (!PER_N) f1 = sr * P.ws[0];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int64_t nq = n + q < P.N ? n + q : P.N - 1;
+        if constexpr (PER_N) wq[q] = P.ws[nq];
+        if constexpr (BIAS) bq[q] = P.bias[nq];
+    }
+    if constexpr (ACC) gemm_old4<OUT>(P.out, m, n, P.M, P.N, false, oq);
+    float v[4];
+    gemm_values<OP, ACT, PER_N, BIAS, ACC>(a, sr, f1, wq, bq, oq, v);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (n + q >= P.N) break;
+        const int64_t at = m * P.N + n + q;
+        if constexpr (OUT == H3S_F32) reinterpret_cast<float*>(P.out)[at] = v[q];
+        else if constexpr (OUT == H3S_BF16) reinterpret_cast<uint16_t*>(P.out)[at] = (uint16_t) pack_bf16(v[q], 0.0f);
+        else reinterpret_cast<uint16_t*>(P.out)[at] = (uint16_t) pack_f16(v[q], 0.0f);
+    }
+}
+
+// How the tiles of a launch split (host side): for rows of at least 12288 bytes (96 K steps), when the tiles leave a
+// last round of the device (one block a CU) at most half full, each of those tiles becomes `split` blocks of
+// consecutive K steps (at most 8, at least 2 steps each, and no more blocks than CUs); the rest run whole. The last
+// round runs faster than a full one (fewer CUs draw power: the clock rises), so what a split saves is about 0.4 of
+// the round's share it removes, and the merge costs about 15 us: fc2's 1386 tiles at 16896 x 14336 -> 5376 took
+// 1191-1194 against 1211-1221 us (2 parts), 3864 at 47104 tokens 3258-3261 against 3322 us (8 parts); with 7168-byte
+// rows, 16896 tokens lost 1.5 % (622 against 608-618 us) and 47104 gained 1 %.
+inline void gemm_plan_split(int64_t tiles, int64_t nk, int cus, int* main_tiles, int* split) {
+    *main_tiles = (int) tiles;
+    *split = 1;
+    const int64_t full = tiles / cus * cus, rem = tiles - full;
+    if (nk < 96 || rem == 0 || 2 * rem > cus) return;
+    int64_t s = cus / rem;
+    s = s < 8 ? s : 8;
+    s = s < nk / 2 ? s : nk / 2;
+    if (s < 2) return;
+    *main_tiles = (int) full;
+    *split = (int) s;
 }
 
 }  // namespace h3

@@ -45,22 +45,52 @@ static void* scratch_on(int device, std::string& why) {
     return nullptr;
 }
 
+// the GEMM of quantized rows, and (split last tiles) the merge of their parts; split_ok false: every tile whole (no
+// scratch, for the allocation-free entry point)
 int launch_gemm(Ctx* c, const char* fn, const int8_t* q, const float* s, int64_t M, int64_t K, const int8_t* w, int64_t N,
-                const float* wscale, int64_t n_wscale, const float* bias, int act_, void* out, int out_dt) {
+                const float* wscale, int64_t n_wscale, const float* bias, int act_, void* out, int out_dt, bool split_ok) {
     const int64_t tm = (M + kGemmBM - 1) / kGemmBM, tn = (N + kGemmBN - 1) / kGemmBN;
     if (tm * tn > 0x7fffffff || tm > 0x7fffffff || tn > 0x7fffffff) return fail(std::string(fn) + ": too many tiles");
-    const GemmArgs P{q, s, M, K, w, N, wscale, bias, out, out_dt, (int) tm, (int) tn, K >= 12288 ? 4 : 8};
-    const unsigned grid = (unsigned) (tm * tn);
+    int main_tiles = (int) (tm * tn), split = 1;
+    if (split_ok) gemm_plan_split(tm * tn, (K + kGemmBK - 1) / kGemmBK, c->cus, &main_tiles, &split);
+    const int64_t tail = tm * tn - main_tiles;
+    void* part = nullptr;
+    if (split > 1) {
+        part = c->scratch<int32_t>(Ctx::GEMM_PART, (size_t) (tail * split) * kGemmTileAcc);
+        if (!part) return -1;
+    }
+    const GemmArgs P{q, s, M, K, w, N, wscale, bias, out, out_dt, (int) tm, (int) tn, K >= 12288 ? 4 : 8, main_tiles, split, part};
+    const unsigned grid = (unsigned) (main_tiles + tail * split);
     const bool per_n = n_wscale > 1;
-#define LG(ACT, PN) gemm_i8_kernel<ACT, PN><<<grid, kGemmThreads, 0, c->stream>>>(P)
+    const unsigned mgrid = (unsigned) (tail * kGemmMergeBlocks);
+    // the merge for one activation, weight-scale kind, output type and bias
+#define LM(ACT, PN)                                                                                                  \
+    if (split > 1) {                                                                                                 \
+        if (out_dt == H3S_BF16) {                                                                                    \
+            if (bias) gemm_merge_kernel<GEMM_I8, ACT, PN, false, H3S_BF16, true><<<mgrid, 256, 0, c->stream>>>(P);    \
+            else gemm_merge_kernel<GEMM_I8, ACT, PN, false, H3S_BF16, false><<<mgrid, 256, 0, c->stream>>>(P);       \
+        } else if (out_dt == H3S_F16) {                                                                              \
+            if (bias) gemm_merge_kernel<GEMM_I8, ACT, PN, false, H3S_F16, true><<<mgrid, 256, 0, c->stream>>>(P);     \
+            else gemm_merge_kernel<GEMM_I8, ACT, PN, false, H3S_F16, false><<<mgrid, 256, 0, c->stream>>>(P);        \
+        } else {                                                                                                     \
+            if (bias) gemm_merge_kernel<GEMM_I8, ACT, PN, false, H3S_F32, true><<<mgrid, 256, 0, c->stream>>>(P);     \
+            else gemm_merge_kernel<GEMM_I8, ACT, PN, false, H3S_F32, false><<<mgrid, 256, 0, c->stream>>>(P);        \
+        }                                                                                                            \
+    }
+#define LG(ACT, PN)                                                        \
+    {                                                                      \
+        gemm_i8_kernel<ACT, PN><<<grid, kGemmThreads, 0, c->stream>>>(P);  \
+        LM(ACT, PN)                                                        \
+    }
 #define LA(ACT)                    \
-    if (per_n) LG(ACT, true);      \
-    else LG(ACT, false);
+    if (per_n) LG(ACT, true)       \
+    else LG(ACT, false)
     if (act_ == H3S_ACT_SILU) { LA(H3S_ACT_SILU); }
     else if (act_ == H3S_ACT_GELU_TANH) { LA(H3S_ACT_GELU_TANH); }
     else { LA(H3S_ACT_NONE); }
 #undef LA
 #undef LG
+#undef LM
     return launched(fn);
 }
 
@@ -87,7 +117,7 @@ H3S_EXPORT int h3s_int8_gemm_dequant(void* ctx, const int8_t* q, const float* s,
     if (act != H3S_ACT_NONE && act != H3S_ACT_SILU && act != H3S_ACT_GELU_TANH) return fail("h3s_int8_gemm_dequant: unknown activation");
     Ctx* c = ctx_of(ctx, "h3s_int8_gemm_dequant");
     if (!c) return -1;
-    return launch_gemm(c, "h3s_int8_gemm_dequant", q, s, M, K, w, N, wscale, n_wscale, bias, act, out, out_dt);
+    return launch_gemm(c, "h3s_int8_gemm_dequant", q, s, M, K, w, N, wscale, n_wscale, bias, act, out, out_dt, true);
 } catch (const std::exception& e) { return fail(e.what()); }
 
 namespace h3 {
@@ -105,7 +135,7 @@ static int linear_checks(const char* fn, const void* x, int x_dt, int64_t K, int
 // the quantizer, then the GEMM, rows at a time into xq [rows, K] and rs [rows]
 static int linear_chunks(Ctx* c, const char* fn, const void* x, int x_dt, int64_t M, int64_t K, const int8_t* w, int64_t N,
                          const float* wscale, int64_t n_wscale, const float* bias, void* out, int out_dt, int group, int8_t* xq,
-                         float* rs, int64_t rows, bool timed) {
+                         float* rs, int64_t rows, bool timed, bool split_ok) {
     const size_t xe = (size_t) elem_size(x_dt), oe = (size_t) elem_size(out_dt);
     for (int64_t r0 = 0; r0 < M; r0 += rows) {
         const int64_t n = M - r0 < rows ? M - r0 : rows;
@@ -114,7 +144,7 @@ static int linear_chunks(Ctx* c, const char* fn, const void* x, int x_dt, int64_
         if (launch_quantize(c, (const char*) x + (size_t) (r0 * K) * xe, x_dt, n, K, group, xq, rs)) return -1;
         t.mark();
         if (launch_gemm(c, fn, xq, rs, n, K, w, N, wscale, n_wscale, bias, H3S_ACT_NONE, (char*) out + (size_t) (r0 * N) * oe,
-                        out_dt))
+                        out_dt, split_ok))
             return -1;
         t.mark();
         const std::vector<float> ms = t.elapsed();
@@ -145,7 +175,7 @@ H3S_EXPORT int h3s_int8_linear(void* ctx, const void* x, int x_dt, int64_t M, in
     int8_t* xq = c->scratch<int8_t>(Ctx::LIN_CODES, (size_t) (rows * K));
     float* rs = c->scratch<float>(Ctx::LIN_SCALES, (size_t) rows);
     if (!xq || !rs) return -1;
-    return linear_chunks(c, fn, x, x_dt, M, K, w, N, wscale, n_wscale, bias, out, out_dt, group, xq, rs, rows, true);
+    return linear_chunks(c, fn, x, x_dt, M, K, w, N, wscale, n_wscale, bias, out, out_dt, group, xq, rs, rows, true, true);
 } catch (const std::exception& e) { return fail(e.what()); }
 
 // h3s_int8_linear with the quantized rows in the fixed device array: no allocation, any M (in chunks of at most
@@ -168,5 +198,5 @@ H3S_EXPORT int h3s_int8_linear_noalloc(void* ctx, const void* x, int x_dt, int64
     const int64_t by_codes = (int64_t) (kScratchCodes / (size_t) K);
     const int64_t rows = by_codes < kScratchRows ? by_codes : kScratchRows;
     return linear_chunks(c, fn, x, x_dt, M, K, w, N, wscale, n_wscale, bias, out, out_dt, group, reinterpret_cast<int8_t*>(base),
-                         reinterpret_cast<float*>(base + kScratchCodes), rows, false);
+                         reinterpret_cast<float*>(base + kScratchCodes), rows, false, false);
 } catch (const std::exception& e) { return fail(e.what()); }

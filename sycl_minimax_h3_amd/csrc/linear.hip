@@ -92,18 +92,43 @@ static bool mfma_takes(int dt, const void* x, const void* w, const void* out, in
     return (dt == H3S_BF16 || dt == H3S_F16) && K % 32 == 0 && 2 * K < ((int64_t) 1 << 24) && N > 128 &&
            aligned16(x) && aligned16(w) && aligned16(out) && tm * tn <= 0x7fffffff;
 }
+// the merge of the split last tiles for operand type OP (out_dt: the output type; ACC: h3s_linear_acc, out in dt)
+template <int OP, bool ACC>
+static void merge_f16(Ctx* c, const GemmArgs& P, unsigned mgrid) {
+    const bool b = P.bias != nullptr;
+    if (P.out_dt == H3S_BF16) {
+        if (b) gemm_merge_kernel<OP, H3S_ACT_NONE, false, ACC, H3S_BF16, true><<<mgrid, 256, 0, c->stream>>>(P);
+        else gemm_merge_kernel<OP, H3S_ACT_NONE, false, ACC, H3S_BF16, false><<<mgrid, 256, 0, c->stream>>>(P);
+    } else if (P.out_dt == H3S_F16) {
+        if (b) gemm_merge_kernel<OP, H3S_ACT_NONE, false, ACC, H3S_F16, true><<<mgrid, 256, 0, c->stream>>>(P);
+        else gemm_merge_kernel<OP, H3S_ACT_NONE, false, ACC, H3S_F16, false><<<mgrid, 256, 0, c->stream>>>(P);
+    } else if constexpr (!ACC) {
+        if (b) gemm_merge_kernel<OP, H3S_ACT_NONE, false, false, H3S_F32, true><<<mgrid, 256, 0, c->stream>>>(P);
+        else gemm_merge_kernel<OP, H3S_ACT_NONE, false, false, H3S_F32, false><<<mgrid, 256, 0, c->stream>>>(P);
+    }
+}
 static int linear_mfma(Ctx* c, const char* fn, const void* x, int dt, int64_t M, int64_t K, const void* w, int64_t N,
                        const float* bias, void* out, int out_dt, bool acc) {
     const int64_t tm = (M + kGemmBM - 1) / kGemmBM, tn = (N + kGemmBN - 1) / kGemmBN, kb = 2 * K;
+    int main_tiles = (int) (tm * tn), split = 1;
+    gemm_plan_split(tm * tn, (kb + kGemmBK - 1) / kGemmBK, c->cus, &main_tiles, &split);
+    const int64_t tail = tm * tn - main_tiles;
+    void* part = nullptr;
+    if (split > 1) {
+        part = c->scratch<float>(Ctx::GEMM_PART, (size_t) (tail * split) * kGemmTileAcc);
+        if (!part) return -1;
+    }
     const GemmArgs P{(const int8_t*) x, nullptr, M, kb, (const int8_t*) w, N, nullptr, bias, out, out_dt, (int) tm, (int) tn,
-                     kb >= 12288 ? 4 : 8};
-    const unsigned grid = (unsigned) (tm * tn);
+                     kb >= 12288 ? 4 : 8, main_tiles, split, part};
+    const unsigned grid = (unsigned) (main_tiles + tail * split), mgrid = (unsigned) (tail * kGemmMergeBlocks);
     if (dt == H3S_BF16) {
         if (acc) gemm_f16_kernel<GEMM_BF16, true><<<grid, kGemmThreads, 0, c->stream>>>(P);
         else gemm_f16_kernel<GEMM_BF16, false><<<grid, kGemmThreads, 0, c->stream>>>(P);
+        if (split > 1) { if (acc) merge_f16<GEMM_BF16, true>(c, P, mgrid); else merge_f16<GEMM_BF16, false>(c, P, mgrid); }
     } else {
         if (acc) gemm_f16_kernel<GEMM_F16, true><<<grid, kGemmThreads, 0, c->stream>>>(P);
         else gemm_f16_kernel<GEMM_F16, false><<<grid, kGemmThreads, 0, c->stream>>>(P);
+        if (split > 1) { if (acc) merge_f16<GEMM_F16, true>(c, P, mgrid); else merge_f16<GEMM_F16, false>(c, P, mgrid); }
     }
     return launched(fn);
 }
