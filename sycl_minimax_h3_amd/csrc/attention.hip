@@ -40,9 +40,12 @@ static void prep(Ctx* c, const void* q, const void* k, const void* v, int64_t S,
 #undef H3_QK
     };
     if (sage) {
-        // k's mean per (head, feature) of the D features; the 16-byte form takes 16 features a block
+        // k's mean per (head, feature) of the D features; the 16-byte form takes 16 features a block, or 32 where 16
+        // would make more blocks than the device runs at once
         const int64_t hd = Hkv * D;
-        if (vec && hd % kKmeanFeat == 0) attn_kmean_kernel<DT><<<(unsigned) (hd / kKmeanFeat), 256, 0, c->stream>>>(k, S, kv_stride, km);
+        const bool wide = hd % kKmeanFeatWide == 0 && hd / kKmeanFeat > c->cus;
+        if (vec && wide) attn_kmean_kernel<DT, kKmeanFeatWide><<<(unsigned) (hd / kKmeanFeatWide), 256, 0, c->stream>>>(k, S, kv_stride, km);
+        else if (vec && hd % kKmeanFeat == 0) attn_kmean_kernel<DT, kKmeanFeat><<<(unsigned) (hd / kKmeanFeat), 256, 0, c->stream>>>(k, S, kv_stride, km);
         else attn_kmean_rows_kernel<DT><<<(unsigned) ((hd + 255) / 256), 256, 0, c->stream>>>(k, S, hd, kv_stride, km);
         if (!q_in_kernel) qk(q, qs_stride, qblocks, nullptr, aq, qs);
         qk(k, kv_stride, kvblocks, km, ak, ks);

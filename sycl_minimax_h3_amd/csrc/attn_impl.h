@@ -68,20 +68,21 @@ __device__ __forceinline__ void attn_dma16(const void* g, const void* lds_dst) {
 // k's mean over the sequence per (head, feature): a float32 sum in token order, / S (h3sycl.cpp:1732-1737). Each
 // feature's sum is one serial chain of S additions (a wavefront issues a dependent v_add_f32 every 4.9 cycles), and
 // the features are few (4096 at 32 heads of 128), so the kernel spreads them thin to use every CU's memory
-// parallelism: a block takes 16 features (256 blocks at 4096 features; a block's loads in flight, not HBM, bound the
-// rate), one a lane of wavefront 0, which only reads four float32 rows of its feature at a time (ds_read_b128) and
-// adds them in order. Wavefronts 1-3 keep seven row chunks in flight with direct loads (attn_dma16) into a ring of
+// parallelism: a block takes F features (16: 256 blocks at 4096 features; a block's loads in flight, not HBM, bound
+// the rate; 32 where 16 would make more blocks than CUs, so that the serial chains run in one round: 224 blocks at
+// the DiT's 56 heads of 128), one a lane of wavefront 0, which only reads four float32 rows of its feature at a time
+// (ds_read_b128) and adds them in order. Wavefronts 1-3 keep seven row chunks in flight with direct loads (attn_dma16) into a ring of
 // eight 12 KiB stages (row-major, as in memory) and turn each landed chunk into float32 rows per feature
 // (feature-major, padded) in one of two buffers. One barrier a chunk: after barrier i, wavefront 0 sums chunk i - 1
 // while the others convert chunk i, refill chunk i - 1's stage with chunk i + 7 and wait for chunk i + 1. A chunk
 // past the last loads the last one again (into a stage no chunk uses then), so the wait is the same at every chunk.
 // Blocks of neighbouring features (which share 128-byte lines) are numbered onto one XCD. Needs the rows 16-byte
 // aligned (k and the stride); attn_kmean_rows_kernel is the general form.
-constexpr int kKmeanFeat = 16, kKmeanStages = 8, kKmeanChunk = 12288, kKmeanLoaders = 192;
-template <int DT>
+constexpr int kKmeanFeat = 16, kKmeanFeatWide = 32, kKmeanStages = 8, kKmeanChunk = 12288, kKmeanLoaders = 192;
+template <int DT, int F>
 __global__ __launch_bounds__(256) void attn_kmean_kernel(const void* __restrict__ k, int64_t S, int64_t stride,
                                                          float* __restrict__ mean) {
-    constexpr int F = kKmeanFeat, ESZ = DT == H3S_F32 ? 4 : 2, RB = F * ESZ;   // bytes of a row's F features
+    constexpr int ESZ = DT == H3S_F32 ? 4 : 2, RB = F * ESZ;   // bytes of a row's F features
     constexpr int SEG = RB / 16, ROWS = kKmeanChunk / RB, LPT = kKmeanChunk / (kKmeanLoaders * 16);
     constexpr int VS = 16 / ESZ;                 // values of a 16-byte segment
     constexpr int TS = ROWS + 4;                 // floats a feature takes in a converted buffer

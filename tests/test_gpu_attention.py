@@ -40,6 +40,15 @@ def dev_sage():
 
 
 @pytest.fixture(scope="module")
+def dev_sage4():
+    """The int8 form at every length with grids sized for 4 compute units (H3S_CUS=4): k's mean then takes 32
+    features a block wherever 16 would make more than 4 blocks."""
+    d = _open_with({"H3S_SAGE_MIN_S": "0", "H3S_CUS": "4"})
+    yield d
+    d.close()
+
+
+@pytest.fixture(scope="module")
 def dev_16():
     """A context that keeps every call on the 16-bit form (H3S_ATTN=onednn)."""
     d = _open_with({"H3S_ATTN": "onednn"})
@@ -106,17 +115,22 @@ def test_attention_peaked_and_shifted(dev_sage, dev_16, sage):
     check(got, want, o.F32, "peaked")
 
 
+@pytest.mark.parametrize("blocks", ["16", "32"])
 @pytest.mark.parametrize("dt", [o.BF16, o.F16, o.F32])
 @pytest.mark.parametrize("S,H,D", [(1, 2, 128), (191, 1, 64), (192, 2, 64), (384, 1, 128), (385, 2, 128),
                                    (2017, 3, 64), (5000, 1, 64)])
-def test_attention_kmean(dev_sage, dt, S, H, D):
+def test_attention_kmean(request, blocks, dt, S, H, D):
     """k's mean (h3sycl.cpp:1732-1737), seen through the output. A per-feature constant taken from k moves all of a
     query's scores alike and the softmax cancels it, so in ordinary inputs a wrong mean only shows through the
     quantization. Here each feature of k is a large power of two C_f plus or minus C_f 2^-7 in pairs of rows of
     opposite sign: the float32 sum in token order is exact and the mean is C_f, so k - mean is +-C_f 2^-7. A mean
     that misses one row then moves the output by a relative L2 of about 8e-2 (a CPU model of the scores from the
     oracle's quantizer), a missed chunk or mixed-up features by 0.15 to 1. Lengths around the 384- and 192-row
-    chunks of the 16-bit and float32 inputs, and past the eight-chunk ring."""
+    chunks of the 16-bit and float32 inputs, and past the eight-chunk ring. blocks "32": a context sized for 4 CUs,
+    where the mean takes 32 features a block (its chunks of 192 and 96 rows) for every case of 128 features or more."""
+    dev_sage = request.getfixturevalue("dev_sage" if blocks == "16" else "dev_sage4")
+    if blocks == "32" and (H * D) // 16 <= 4:
+        pytest.skip("16 features a block already fit the 4 CUs")
     stride = H * D
     g = np.random.default_rng(S + 7 * H)
     q = o.to_dt(g.standard_normal((S, stride)).astype(np.float32), dt).ravel()
