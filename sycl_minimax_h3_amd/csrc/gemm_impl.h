@@ -362,7 +362,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& P) {
         constexpr int OUT = decltype(out_tag)::value;
         constexpr bool BIAS = decltype(bias_tag)::value;
         constexpr int esz = OUT == H3S_F32 ? 4 : 2;
-        constexpr int pitch = kGemmWN * esz + 16;           // bytes a slice row (16 bytes of pad: distinct banks)
+        // h3s_linear_acc (ACC) stages the values unrounded, as float32, and adds the old output where it stores them:
+        // the old rows are then read as whole 16-byte pieces beside the stores
+        constexpr int sesz = ACC ? 4 : esz;
+        constexpr int pitch = kGemmWN * sesz + 16;          // bytes a slice row (16 bytes of pad: distinct banks)
         int8_t* slice = lds + 3 * 1024 + wave * (32 * pitch);
         const float ws0 = OP == GEMM_I8 && !PER_N ? P.ws[0] : 0.0f;
         // rows of out start on 16-byte boundaries and the block's tile lies inside out: plain 16-byte stores
@@ -388,11 +391,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& P) {
                         const float4 b4 = *reinterpret_cast<const float4*>(bcol + cl);
                         bq[0] = b4.x; bq[1] = b4.y; bq[2] = b4.z; bq[3] = b4.w;
                     }
-                    if constexpr (ACC) gemm_old4<OUT>(P.out, m0 + wm * kGemmWM + i * 32 + (lane & 31), n0 + cl, P.M, P.N, full, oq);
                     float v[4];
-                    gemm_values<OP, ACT, PER_N, BIAS, ACC>(a, sr, f1, wq, bq, oq, v);
-                    int8_t* at = slice + (lane & 31) * pitch + (j * 32 + 8 * g + 4 * (lane >> 5)) * esz;
-                    if constexpr (OUT == H3S_F32)
+                    gemm_values<OP, ACT, PER_N, BIAS, false>(a, sr, f1, wq, bq, oq, v);
+                    int8_t* at = slice + (lane & 31) * pitch + (j * 32 + 8 * g + 4 * (lane >> 5)) * sesz;
+                    if constexpr (OUT == H3S_F32 || ACC)
                         *reinterpret_cast<float4*>(at) = make_float4(v[0], v[1], v[2], v[3]);
                     else if constexpr (OUT == H3S_BF16)
                         *reinterpret_cast<uint2*>(at) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
@@ -400,6 +402,42 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& P) {
                         *reinterpret_cast<uint2*>(at) = make_uint2(pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
                 }
             const int64_t mt = m0 + wm * kGemmWM + i * 32, nt = n0 + wn * kGemmWN;
+            if constexpr (ACC) {
+                // each 16-byte piece of a row of out: its epc staged values + the old ones, rounded once
+#pragma unroll
+                for (int k = 0; k < 32 * per_row / 64; ++k) {
+                    const int ch = lane + 64 * k, rr = ch / per_row, cg = ch % per_row;
+                    const int64_t m = mt + rr, n = nt + (int64_t) cg * epc;
+                    float f[epc];
+#pragma unroll
+                    for (int q = 0; q < epc; q += 4) {
+                        const float4 t = *reinterpret_cast<const float4*>(slice + rr * pitch + (cg * epc + q) * 4);
+                        f[q] = t.x; f[q + 1] = t.y; f[q + 2] = t.z; f[q + 3] = t.w;
+                    }
+                    char* o = reinterpret_cast<char*>(P.out) + (m * P.N + n) * esz;
+                    if (full) {
+                        const uint4 old = *reinterpret_cast<const uint4*>(o);
+                        const uint32_t w4[4] = {old.x, old.y, old.z, old.w};
+                        uint32_t r4[4];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            if constexpr (OUT == H3S_F32) r4[q] = __float_as_uint(f[q] + __uint_as_float(w4[q]));
+                            else if constexpr (OUT == H3S_BF16) r4[q] = pack_bf16(f[2 * q] + bf16_lo(w4[q]), f[2 * q + 1] + bf16_hi(w4[q]));
+                            else r4[q] = pack_f16(f[2 * q] + f16_lo(w4[q]), f[2 * q + 1] + f16_hi(w4[q]));
+                        }
+                        st_nt(o, make_uint4(r4[0], r4[1], r4[2], r4[3]));
+                    } else if (m < P.M && n < P.N) {
+                        for (int e = 0; e < epc && n + e < P.N; ++e) {
+                            if constexpr (OUT == H3S_F32) reinterpret_cast<float*>(o)[e] = f[e] + reinterpret_cast<const float*>(o)[e];
+                            else if constexpr (OUT == H3S_BF16)
+                                reinterpret_cast<uint16_t*>(o)[e] = (uint16_t) pack_bf16(f[e] + bf16_lo(reinterpret_cast<const uint16_t*>(o)[e]), 0.0f);
+                            else
+                                reinterpret_cast<uint16_t*>(o)[e] = (uint16_t) pack_f16(f[e] + f16_lo(reinterpret_cast<const uint16_t*>(o)[e]), 0.0f);
+                        }
+                    }
+                }
+                continue;
+            }
 #pragma unroll
             for (int k = 0; k < 32 * per_row / 64; ++k) {
                 const int ch = lane + 64 * k, rr = ch / per_row, cg = ch % per_row;
