@@ -332,13 +332,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& P) {
     if (part >= 0) {
         // a part of a split tile: its accumulators, register by register, 64 lanes' 4-byte values contiguous
         using E = std::conditional_t<OP == GEMM_I8, int, float>;
+        // (the 32 x 32 blocks wholly past out's last row or column are not stored: the merge reads none of them)
         E* dst = reinterpret_cast<E*>(P.part) + (size_t) part * kGemmTileAcc + wave * (kGemmMF * 16 * 64) + lane;
 #pragma unroll
         for (int i = 0; i < kGemmWI; ++i)
 #pragma unroll
-            for (int j = 0; j < kGemmWJ; ++j)
+            for (int j = 0; j < kGemmWJ; ++j) {
+                if (m0 + wm * kGemmWM + 32 * i >= P.M || n0 + wn * kGemmWN + 32 * j >= P.N) continue;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) dst[((i * kGemmWJ + j) * 16 + r) * 64] = acc[i][j][r];
+            }
         return;
     }
     __syncthreads();   // every stage read: the LDS is the epilogue's now
@@ -532,15 +535,21 @@ __global__ __launch_bounds__(256) void gemm_merge_kernel(GemmArgs P) {
 // the round's share it removes, and the merge costs about 15 us: fc2's 1386 tiles at 16896 x 14336 -> 5376 took
 // 1191-1194 against 1211-1221 us (2 parts), 3864 at 47104 tokens 3258-3261 against 3322 us (8 parts); with 7168-byte
 // rows, 16896 tokens lost 1.5 % (622 against 608-618 us) and 47104 gained 1 %.
+// A launch of at most half as many tiles as CUs (a narrow product: a LoRA's first factor, 16896 x 5376 -> 64, is 66
+// tiles) splits every tile the same way, where that pays: there the split spreads one round's work over more CUs
+// instead of shortening a last round. A tile takes about 1.2 us a K step and a merge about 3 us plus 0.05 us a part
+// (its 256 KiB written and read), so the split is taken when 1.2 nk (1 - 1/s) > 0.05 T s + 3 (T tiles, s parts).
 inline void gemm_plan_split(int64_t tiles, int64_t nk, int cus, int* main_tiles, int* split) {
     *main_tiles = (int) tiles;
     *split = 1;
     const int64_t full = tiles / cus * cus, rem = tiles - full;
-    if (nk < 96 || rem == 0 || 2 * rem > cus) return;
+    const bool narrow = full == 0 && 2 * rem <= cus;
+    if (!narrow && (nk < 96 || rem == 0 || 2 * rem > cus)) return;
     int64_t s = cus / rem;
     s = s < 8 ? s : 8;
     s = s < nk / 2 ? s : nk / 2;
     if (s < 2) return;
+    if (narrow && 24 * nk * (s - 1) <= rem * s * s + 60 * s) return;
     *main_tiles = (int) full;
     *split = (int) s;
 }

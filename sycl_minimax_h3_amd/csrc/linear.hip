@@ -1,11 +1,10 @@
 // linear.hip - the plain (float) linear layers of kernels/h3sycl.h:87-93: h3s_linear (out = x w^T + bias),
 // h3s_linear_acc (out += x w^T + bias, a LoRA's second factor) and h3s_scale_rows (kernels/h3sycl.cpp:656-739).
-// bfloat16 and half operands with K a multiple of 32 and more than 128 outputs a row run on the matrix cores in
-// gemm_impl.h's pipeline (gemm_f16_kernel): float32 accumulation, and the epilogue adds the bias (and the old output)
-// in float32 and rounds once to the output type, as the reference's matmul post-ops do, with no intermediate in
-// memory. Every other call (float32 operands, other K, narrow outputs, unaligned rows) runs on rocBLAS (a plain
-// library GEMM, float32 accumulation, on the context's stream) into a float32 scratch, a chunk of rows at a time, and
-// the same epilogue as a kernel of its own.
+// bfloat16 and half operands with K a multiple of 32 run on the matrix cores in gemm_impl.h's pipeline
+// (gemm_f16_kernel): float32 accumulation, and the epilogue adds the bias (and the old output) in float32 and rounds
+// once to the output type, as the reference's matmul post-ops do, with no intermediate in memory. Every other call
+// (float32 operands, other K, unaligned rows) runs on rocBLAS (a plain library GEMM, float32 accumulation, on the
+// context's stream) into a float32 scratch, a chunk of rows at a time, and the same epilogue as a kernel of its own.
 #include <rocblas/rocblas.h>
 
 #include "gemm_impl.h"
@@ -84,13 +83,11 @@ static int launch_epilogue(Ctx* c, const float* acc, int64_t M, int64_t N, const
 }
 
 // whether gemm_f16_kernel takes the product: 16-bit operands whose rows are whole 64-byte units (the pipeline's
-// half K step) and start on 16-byte boundaries (out too), K * 2 below 2^24 bytes, tile counts within 32 bits, and
-// more than 128 outputs a row. A narrower product (a LoRA's first factor, rank 64: 16896 x 5376 -> 64 took 104 us
-// on the 256 x 256 tiles, three quarters of their products wasted, against rocBLAS's 63) stays on rocBLAS.
+// half K step) and start on 16-byte boundaries (out too), K * 2 below 2^24 bytes, tile counts within 32 bits
 static bool mfma_takes(int dt, const void* x, const void* w, const void* out, int64_t M, int64_t K, int64_t N) {
     const int64_t tm = (M + kGemmBM - 1) / kGemmBM, tn = (N + kGemmBN - 1) / kGemmBN;
-    return (dt == H3S_BF16 || dt == H3S_F16) && K % 32 == 0 && 2 * K < ((int64_t) 1 << 24) && N > 128 &&
-           aligned16(x) && aligned16(w) && aligned16(out) && tm * tn <= 0x7fffffff;
+    return (dt == H3S_BF16 || dt == H3S_F16) && K % 32 == 0 && 2 * K < ((int64_t) 1 << 24) && aligned16(x) &&
+           aligned16(w) && aligned16(out) && tm * tn <= 0x7fffffff;
 }
 // the merge of the split last tiles for operand type OP (out_dt: the output type; ACC: h3s_linear_acc, out in dt)
 template <int OP, bool ACC>

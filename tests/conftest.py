@@ -48,3 +48,22 @@ def dev_wave():
             os.environ["H3S_QUANT_WAVE_MIN_ROWS"] = old
     yield d
     d.close()
+
+
+@pytest.fixture(scope="session")
+def dev_cus16():
+    """A context that sizes its grids for 16 compute units (H3S_CUS=16): GEMMs of a few dozen tiles then make whole
+    rounds of tiles (XCD renumbering and tile groups, no split along K) at sizes the oracle checks quickly."""
+    from sycl_minimax_h3_amd import Device
+
+    old = os.environ.get("H3S_CUS")
+    os.environ["H3S_CUS"] = "16"
+    try:
+        d = Device.open()
+    finally:
+        if old is None:
+            del os.environ["H3S_CUS"]
+        else:
+            os.environ["H3S_CUS"] = old
+    yield d
+    d.close()

@@ -615,11 +615,13 @@ def test_int8_gemm_dequant(dev, act, K):
 
 @pytest.mark.parametrize("act", [o.ACT_NONE, o.ACT_SILU])
 @pytest.mark.parametrize("M,N,K", [(2560, 1024, 4096), (2716, 776, 4096), (1297, 763, 12288)])
-def test_int8_gemm_tile_order(dev, act, M, N, K):
+def test_int8_gemm_tile_order(dev_cus16, act, M, N, K):
     """Grids of more than 8 tile rows, renumbered across the XCDs in groups of 8 tile rows as at config 5b's size:
     10 x 4 tiles (a multiple of 8), and 11 x 4 = 44 (not one: the first four XCDs take one tile more), with a
     partial last tile row and column; and K = 12288, whose groups are 4 tile rows high (6 x 3 tiles: a full group and
-    a partial one)."""
+    a partial one). On a context sized for 16 CUs, so that the tiles run whole (on the whole device, so few tiles
+    would split along K), the 18 tiles at K = 12288 as 16 whole and 2 in parts."""
+    dev = dev_cus16
     rng = np.random.default_rng(74)
     q = rng.integers(-128, 128, M * K, dtype=np.int8)
     s = rng.uniform(0.001, 0.05, M).astype(np.float32)

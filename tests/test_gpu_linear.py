@@ -1,10 +1,10 @@
 """GPU parity of the plain linear layers (kernels/h3sycl.cpp:656-739) through the C ABI against the oracle's float64
 products: h3s_linear, h3s_linear_acc (row chunks included) and h3s_scale_rows. The reference's products are oneDNN's,
 whose accumulation order is not restated: the parity tolerance (relative L2 < 1e-3, one ulp of the output type).
-bfloat16 and half operands with K a multiple of 32 and N above 128 run on the matrix-core kernel (256 x 256 tiles:
-partial tiles at every edge, K steps of 64 elements with a last half step where K is an odd multiple of 32, the
-long-K tile order from K = 6144); K = 200, N of 128 or less and float32 operands run on rocBLAS with the separate
-epilogue."""
+bfloat16 and half operands with K a multiple of 32 run on the matrix-core kernel (256 x 256 tiles: partial tiles at
+every edge, K steps of 64 elements with a last half step where K is an odd multiple of 32, the long-K tile order
+from K = 6144; launches of few tiles split along K: 2000 x 1024 -> 64 or 100, 8 tiles in 8 parts each); K = 200 and
+float32 operands run on rocBLAS with the separate epilogue."""
 import numpy as np
 import pytest
 
@@ -36,7 +36,7 @@ def close(got, want, dt, what):
 
 @pytest.mark.parametrize("dt,out_dt", [(o.BF16, o.BF16), (o.BF16, o.F32), (o.F16, o.F16), (o.F32, o.F32), (o.F32, o.BF16)])
 @pytest.mark.parametrize("M,K,N", [(37, 256, 130), (300, 1024, 520), (8200, 64, 48), (1000, 2048, 700), (513, 6144, 300),
-                                   (600, 200, 90), (257, 96, 256)])
+                                   (600, 200, 90), (257, 96, 256), (2000, 1024, 64), (2000, 1024, 100)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_linear(dev, dt, out_dt, M, K, N, bias):
     x, w, b = mats(100 + K, M, K, N, dt)
