@@ -32,7 +32,10 @@
 // run of tiles, grouped 8 tiles high (4 for K of 12288 or more) so that the resident blocks of an XCD share A and W
 // panels in its L2.
 // Epilogue: per 32-row slice of a wavefront's region, dequant + activation in registers, the slice through LDS,
-// then 16-byte row-contiguous stores.
+// then 16-byte row-contiguous stores (h3s_linear_acc: the slice in float32, the old output added as it is stored).
+// Split tiles (gemm_plan_split): a short last round of long-K tiles, or every tile of a launch of few tiles, runs
+// as several blocks of consecutive K steps that leave their accumulators in scratch; gemm_merge_kernel sums them in
+// part order and applies the same epilogue arithmetic (gemm_values).
 #pragma once
 
 #include <type_traits>
