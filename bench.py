@@ -82,7 +82,7 @@ def bytes_cfg():
         "attn_sage_16896x32x128": 4 * M2 * 4096 * 2,     # q, k, v read, out written (the products are the bound)
         "attn_sage_47104x32x128": 4 * M4 * 4096 * 2,
         "attn_f16_4096x32x128": 4 * 4096 * 4096 * 2,     # the 16-bit form (below 8192 tokens)
-        **dit_bytes(M2), **dit_bytes(M4), **float_linear_bytes(M2),
+        **dit_bytes(M2), **dit_bytes(M4), **float_linear_bytes(M2), **lora_bytes(M4),
         "copy_probe_1GiB": 2 << 30,
         # a plain copy moving config 1's bytes (half read, half written): the floor a launch of that size reaches
         "copy_probe_cfg1_bytes": 2 * CFG1_COPY_ELEMS * 2,
@@ -157,6 +157,11 @@ def float_linear_bytes(M: int) -> dict:
         out[f"{name}_{M}x{K}x{N}"] = M * K * 2 + N * K * 2 + (N * 4 if bias else 0) + M * N * 2 * (2 if acc else 1)
     out[f"probe_matmul_bf16_{M}x{DH}x{DH}"] = M * DH * 2 + DH * DH * 2 + M * DH * 2
     return out
+
+
+def lora_bytes(M: int) -> dict:
+    """the LoRA factors alone at another token count"""
+    return {k: v for k, v in float_linear_bytes(M).items() if k.startswith("lora_")}
 
 
 def ring_size(nbytes: int) -> int:
@@ -576,19 +581,26 @@ def main() -> int:
     dit_compute(M4)
 
     # ---- the float linear on bfloat16 activations (h3s_linear, h3s_linear_acc) ----
+    # (the LoRA factors stream their rows: cache-cold rings as above; the linear of the hidden width is
+    # compute-bound: one buffer set)
     gen = torch.Generator(device="cpu").manual_seed(7)
-    for name, K, N, has_bias, acc in FLOAT_LINEARS:
-        key = f"{name}_{M2}x{K}x{N}"
-        if skip(key):
-            continue
-        w = (torch.randn(N, K, generator=gen) / K ** 0.5).to(torch.bfloat16).to(dev_t)
-        bias = (0.1 * torch.randn(N, generator=gen)).float().to(dev_t)
-        lin = ops.Linear(T(w), T(bias) if has_bias else None)
-        x, out = bf16(M2, K), bf16(M2, N)
-        X, O = T(x), T(out)
-        run(key, lambda: ((lambda: lin.forward_acc(X, O)) if acc else (lambda: lin.forward(X, O))), 10, ring=1)
-        del w, bias, lin, x, out, X, O
-        torch.cuda.empty_cache()
+
+    def make_fl(lin, Mf, K, N, acc):
+        def make():
+            X, O = T(bf16(Mf, K)), T(bf16(Mf, N))
+            return (lambda: lin.forward_acc(X, O)) if acc else (lambda: lin.forward(X, O))
+        return make
+    for Mf in (M2, M4):
+        for name, K, N, has_bias, acc in FLOAT_LINEARS:
+            key = f"{name}_{Mf}x{K}x{N}"
+            if skip(key) or key not in B:
+                continue
+            w = (torch.randn(N, K, generator=gen) / K ** 0.5).to(torch.bfloat16).to(dev_t)
+            bias = (0.1 * torch.randn(N, generator=gen)).float().to(dev_t)
+            lin = ops.Linear(T(w), T(bias) if has_bias else None)
+            run(key, make_fl(lin, Mf, K, N, acc), 10, ring=None if name.startswith("lora_") else 1)
+            del w, bias, lin
+            torch.cuda.empty_cache()
     key = f"probe_matmul_bf16_{M2}x{DH}x{DH}"
     if not skip(key):
         w = (torch.randn(DH, DH, generator=gen) / DH ** 0.5).to(torch.bfloat16).to(dev_t)

@@ -376,7 +376,21 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& P) {
         const float ws0 = OP == GEMM_I8 && !PER_N ? P.ws[0] : 0.0f;
         // rows of out start on 16-byte boundaries and the block's tile lies inside out: plain 16-byte stores
         const bool full = (P.N * esz) % 16 == 0 && m0 + kGemmBM <= P.M && n0 + kGemmBN <= P.N;
-        constexpr int per_row = kGemmWN * esz / 16, epc = 16 / esz;
+        constexpr int per_row = kGemmWN * esz / 16, epc = 16 / esz, kpl = 32 * per_row / 64;
+        // h3s_linear_acc on a tile inside out: the old output of a slice's pieces loaded a slice ahead (slice 0's
+        // before any arithmetic), so their latency passes under a slice's work instead of stalling its stores
+        uint4 oldv[2][ACC ? kpl : 1];
+        auto load_old = [&](int i, uint4 (&d)[ACC ? kpl : 1]) {
+#pragma unroll
+            for (int k = 0; k < kpl; ++k) {
+                const int ch = lane + 64 * k, rr = ch / per_row, cg = ch % per_row;
+                const int64_t m = m0 + wm * kGemmWM + i * 32 + rr, n = n0 + wn * kGemmWN + (int64_t) cg * epc;
+                d[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(P.out) + (m * P.N + n) * esz);
+            }
+        };
+        if constexpr (ACC) {
+            if (full) load_old(0, oldv[0]);
+        }
 #pragma unroll
         for (int i = 0; i < kGemmWI; ++i) {
             const float sr = srow[wm * kGemmWM + i * 32 + (lane & 31)];
@@ -409,9 +423,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& P) {
                 }
             const int64_t mt = m0 + wm * kGemmWM + i * 32, nt = n0 + wn * kGemmWN;
             if constexpr (ACC) {
+                if (full && i + 1 < kGemmWI) load_old(i + 1, oldv[(i + 1) & 1]);
                 // each 16-byte piece of a row of out: its epc staged values + the old ones, rounded once
 #pragma unroll
-                for (int k = 0; k < 32 * per_row / 64; ++k) {
+                for (int k = 0; k < kpl; ++k) {
                     const int ch = lane + 64 * k, rr = ch / per_row, cg = ch % per_row;
                     const int64_t m = mt + rr, n = nt + (int64_t) cg * epc;
                     float f[epc];
@@ -422,7 +437,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& P) {
                     }
                     char* o = reinterpret_cast<char*>(P.out) + (m * P.N + n) * esz;
                     if (full) {
-                        const uint4 old = *reinterpret_cast<const uint4*>(o);
+                        const uint4 old = oldv[i & 1][k];
                         const uint32_t w4[4] = {old.x, old.y, old.z, old.w};
                         uint32_t r4[4];
 #pragma unroll
