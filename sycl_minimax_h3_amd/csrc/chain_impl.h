@@ -265,15 +265,11 @@ template <int XDT> int chain_launch(Ctx* c, const char* fn, const ChainArgs& A, 
     const bool pair = XDT == H3S_BF16 && f != ROW_DYN && p.L >= 256 && p.cpl <= 2 &&
                       (f & (ROW_W | ROW_B | ROW_TAB | ROW_GATE)) && A.M >= (int64_t) c->cus * 16;
     const int64_t pairs = (A.M + 1) / 2;
-#ifndef H3_CHAIN_TAIL
-#define H3_CHAIN_TAIL 1
-#endif
     // the pairs that fill whole rounds of the device, and the rows of a last round at most half full as one-row
-    // blocks (H3_CHAIN_TAIL)
+    // blocks
     auto tail_split = [&](const void* k, int64_t& main_blocks, int64_t& tail_blocks) {
         main_blocks = pairs;
         tail_blocks = 0;
-        if (!H3_CHAIN_TAIL) return;
         const int64_t round = (int64_t) c->cus * blocks_per_cu(k, (int) R.threads);
         const int64_t full = pairs / round * round;
         if (full > 0 && full < pairs && 2 * (pairs - full) <= round) {
