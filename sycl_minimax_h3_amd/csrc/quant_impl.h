@@ -1052,13 +1052,14 @@ template <int XDT, int CPL> int quant_wave_launch(Ctx* c, const char* fn, const 
 // The model's own widths (docs/BASELINE.md:13), each with the layout measured fastest for it. With the checkpoints'
 // ConvRot group (regular 256), a lane holds 16 consecutive features of a group (two chunks, "pairs"), so every digit
 // of the rotation is inside the lane or one DPP operand away; without a rotation, one chunk a lane:
-//   5376 features (the hidden width):     the norm with a weight (and float32 tables: the DiT's AdaLN), or the
-//                                         quantizer on x: two wavefronts a row, 3 run pairs each, the row's last a
-//                                         quarter full (unrotated: the norm two wavefronts a row of 6 slots, the
-//                                         last of the second empty; the quantizer on x one wavefront a row, 11
-//                                         slots, the last half full); with ROW_OUTH h3s_rms_norm_mod itself
-//   7168 features (the attention's out):  the quantizer on x: seven wavefronts a row, one run pair each (two
-//                                         wavefronts of 7 slots unrotated)
+//   5376 features (the hidden width):     the norm with a weight (and float32 tables: the DiT's AdaLN): two
+//                                         wavefronts a row, 3 run pairs each, the row's last a quarter full; the
+//                                         quantizer on x: one wavefront a row of 6 run pairs, the last a quarter
+//                                         full (unrotated: the norm two wavefronts a row of 6 slots, the last of the
+//                                         second empty; the quantizer on x one wavefront a row, 11 slots, the last
+//                                         half full); with ROW_OUTH h3s_rms_norm_mod itself
+//   7168 features (the attention's out):  the quantizer on x: one wavefront a row, 7 run pairs (two wavefronts of
+//                                         7 slots unrotated)
 //   4096 features:                        the quantizer on x, rotated: two wavefronts a row, two run pairs each
 //   8192 features (the MLP's middle of    the quantizer on swiglu(x), rotated: four wavefronts a row, two run pairs
 //   the measured 47104 x 8192 workload):  each
@@ -1077,11 +1078,11 @@ template <int XDT> int quant_wave_model(Ctx* c, const char* fn, const QuantArgs&
         if (f == kQuantWTab32 && none) return quant_wave_one<XDT, 6, R0, kQuantWTab32, N, 2, false, 1, MN>(c, fn, A);
         if (f == kQuantW && reg256) return quant_wave_one<XDT, 6, R256, kQuantW, N, 2, true, 1, MN>(c, fn, A);
         if (f == kQuantW && none) return quant_wave_one<XDT, 6, R0, kQuantW, N, 2, false, 1, MN>(c, fn, A);
-        if (f == kQuantRaw && reg256) return quant_wave_one<XDT, 6, R256, kQuantRaw, N, 2, true, 1, MR>(c, fn, A);
+        if (f == kQuantRaw && reg256) return quant_wave_one<XDT, 12, R256, kQuantRaw, N, 1, true, 1, MR>(c, fn, A);
         if (f == kQuantRaw && none) return quant_wave_one<XDT, 11, R0, kQuantRaw, N, 1, false, 1, MR>(c, fn, A);
     }
     if (A.C == 7168 && f == kQuantRaw) {
-        if (reg256) return quant_wave_one<XDT, 2, R256, kQuantRaw, 896, 7, true, 1, MR>(c, fn, A);
+        if (reg256) return quant_wave_one<XDT, 14, R256, kQuantRaw, 896, 1, true, 1, MR>(c, fn, A);
         if (none) return quant_wave_one<XDT, 7, R0, kQuantRaw, 896, 2, false, 1, MR>(c, fn, A);
     }
     if (A.C == 4096 && f == kQuantRaw && reg256) return quant_wave_one<XDT, 4, R256, kQuantRaw, 512, 2, true, 1, MR>(c, fn, A);
