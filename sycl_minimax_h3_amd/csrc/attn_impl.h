@@ -60,10 +60,14 @@ __device__ __forceinline__ uint16_t half_bits(float x) {
 // tell the stages apart), which would make a ring's reads of a landed stage wait for the refills issued after it. The
 // caller's wait_vm before each barrier orders these loads; the memory clobber keeps the compiler from moving LDS
 // accesses across them.
+// (m0 is the compiler's reserved register: it holds nothing across these statements)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void attn_dma16(const void* g, const void* lds_dst) {
     const uint32_t m = (uint32_t) (uintptr_t) lds_dst;
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // k's mean over the sequence per (head, feature): a float32 sum in token order, / S (h3sycl.cpp:1732-1737). Each
 // feature's sum is one serial chain of S additions (a wavefront issues a dependent v_add_f32 every 4.9 cycles), and
