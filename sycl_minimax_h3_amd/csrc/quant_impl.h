@@ -473,7 +473,7 @@ __global__ __launch_bounds__(512) void quant_kernel(QuantArgs A, int lshift, int
         }
         m = row_max(m, red[slot], W);
         slot ^= 1;
-        const float sc = fmaxf(m / 127.0f, 1e-30f), r = 1.0f / sc;
+        const float sc = fmaxf(div127(m), 1e-30f), r = 1.0f / sc;
         if (t == 0) A.s[row] = sc;
 
         // ---- the codes, V bytes a chunk ----
@@ -860,7 +860,7 @@ __device__ __forceinline__ void quant_wave_body(const QuantArgs& A, int64_t blk,
             }
             m = m * cgs;
         }
-        const float sc = fmaxf(m / 127.0f, 1e-30f), r = 1.0f / sc;
+        const float sc = fmaxf(div127(m), 1e-30f), r = 1.0f / sc;
         if (!live) return;
         if (lane == 0 && ws == 0) A.s[row] = sc;
         const float sq = unscaled ? sc * 16.0f : sc, rq = unscaled ? r * 0.0625f : r;   // the codes' divisor
