@@ -296,7 +296,6 @@ template <int L> __device__ __forceinline__ float wave_max(float m) {
     return m;
 }
 
-// 1 / sqrt(mean + eps), each step correctly rounded (built with correctly rounded f32 division and square root)
 // fl(a / 127): Markstein's corrected product with fl(1 / 127), three instructions where the IEEE division takes
 // about eleven; equal to the division bit for bit for every non-negative float a (checked on gfx950 over all of them)
 __device__ __forceinline__ float div127(float a) {
@@ -304,6 +303,7 @@ __device__ __forceinline__ float div127(float a) {
     const float q1 = a * r;
     return __builtin_fmaf(__builtin_fmaf(-q1, 127.0f, a), r, q1);
 }
+// 1 / sqrt(mean + eps), each step correctly rounded (built with correctly rounded f32 division and square root)
 __device__ __forceinline__ float inv_root(float sum, float n, float eps) { return 1.0f / __builtin_sqrtf(sum / n + eps); }
 
 // rint(y / s) with y / s correctly rounded: q1 = y * r, e = y - q1 * s (exact, one fma), q = q1 + e * r, where
