@@ -297,11 +297,14 @@ template <int L> __device__ __forceinline__ float wave_max(float m) {
 }
 
 // fl(a / 127): Markstein's corrected product with fl(1 / 127), three instructions where the IEEE division takes
-// about eleven; equal to the division bit for bit for every non-negative float a (checked on gfx950 over all of them)
+// about eleven; equal to the division bit for bit for every non-negative finite float a (checked on gfx950 over all
+// of them). For a = +inf the correction's inf - inf would give NaN, so the product itself (inf) is returned, as the
+// division gives; NaN stays NaN.
 __device__ __forceinline__ float div127(float a) {
     constexpr float r = 1.0f / 127.0f;
     const float q1 = a * r;
-    return __builtin_fmaf(__builtin_fmaf(-q1, 127.0f, a), r, q1);
+    const float q = __builtin_fmaf(__builtin_fmaf(-q1, 127.0f, a), r, q1);
+    return q1 == __builtin_inff() ? q1 : q;
 }
 // 1 / sqrt(mean + eps), each step correctly rounded (built with correctly rounded f32 division and square root)
 __device__ __forceinline__ float inv_root(float sum, float n, float eps) { return 1.0f / __builtin_sqrtf(sum / n + eps); }
